@@ -1,0 +1,149 @@
+#!/usr/bin/env python3
+"""Benchmark: EmbeddingGemma-300M Q8_0 forward, config 2 (64 x 512 tokens) on
+one MI355X.  Prints ONE JSON line.
+
+A step is one batched forward (sg_forward_device) over the 64 packed
+sequences, token IDs already resident in HBM, embeddings left in HBM.
+`value` is embeddings/sec over the K timed steps.  `roofline` is the Q8_0
+GEMM (the dominant kernel class): algorithmic int8 ops (2*M*N*K per launch)
+over the HIP-event time of those launches inside the timed region, against
+MI355X's dense int8 peak.  `cpu_baseline` is the CPU oracle (a restatement
+of the reference's Go path; the reference itself cannot run here) timed on
+this host on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(ROOT, "go-semantica_amd"), ROOT):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "embeddings/sec (64×512 tok, Q8_0) on 1 MI355X; Q8_0 GEMM % of int8 peak"
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 (5.0 POP/s)
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--seq-len", type=int, default=512)
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, host CPUs)")
+    ap.add_argument("--cpu-seqs", type=int, default=0, help="0: 2 x cpu threads")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_baseline(model, toks, seq_len, threads, n_seq):
+    """The oracle's forward (AVX2 restatement of the reference's VNNI Go path,
+    one worker per sequence like embedPrompts) on n_seq of the workload's rows."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle
+    om = oracle.OracleModel(model)
+    off = np.arange(0, n_seq * seq_len + 1, seq_len, dtype=np.int32)
+    sample = np.ascontiguousarray(toks[: n_seq * seq_len])
+    om.forward_batch(sample[:seq_len], off[:2], 768, n_threads=1)  # warm caches / page in weights
+    t0 = time.perf_counter()
+    rc, _ = om.forward_batch(sample, off, 768, n_threads=threads)
+    dt = time.perf_counter() - t0
+    om.close()
+    if rc != 0:
+        raise RuntimeError(f"oracle forward failed: {rc}")
+    return {"value": round(n_seq / dt, 3), "unit": "embeddings/sec", "cores": threads, "kind": "port",
+            "sample": f"{n_seq} sequences x {seq_len} tokens (rows 0..{n_seq - 1} of the workload), "
+                      f"C oracle, AVX2 VNNI-order GEMM, {threads} threads, {dt:.1f} s"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the path shards as "
+              "pure data parallelism over sequences, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from semantica_gpu import Context, Model, synth
+
+    B, S = a.batch, a.seq_len
+    mdl = synth.make_model()
+    toks = synth.token_ids(B * S, mdl.config["vocab_size"], seed=0)
+    off = np.arange(0, B * S + 1, S, dtype=np.int32)
+    ctx = Context(0)
+    model = Model(ctx, mdl)
+    d_tok = torch.from_numpy(toks).cuda()
+    d_out = torch.empty((B, 768), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(a.warmup):
+        model.forward_device(d_tok.data_ptr(), off, 768, d_out.data_ptr())
+    torch.cuda.synchronize()
+
+    model.profile_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(a.steps):
+        model.forward_device(d_tok.data_ptr(), off, 768, d_out.data_ptr())
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    prof = model.profile_read()
+    model.profile_enable(False)
+
+    emb = d_out.cpu().numpy()
+    assert np.all(np.isfinite(emb)) and np.allclose(np.sum(emb.astype(np.float64) ** 2, axis=1), 1.0, atol=1e-4)
+
+    g = prof["gemm"]
+    gemm_tops = g["work"] / (g["ms"] * 1e-3) / 1e12 if g["ms"] > 0 else 0.0
+    kernels = {}
+    for name, p in prof.items():
+        if p["launches"] == 0:
+            continue
+        k = {"ms_per_step": round(p["ms"] / a.steps, 4), "launches_per_step": p["launches"] // a.steps}
+        if name == "gemm":
+            k["TOPS_int8"] = round(gemm_tops, 2)
+        elif name == "attention":
+            k["TFLOPS"] = round(p["work"] / (p["ms"] * 1e-3) / 1e12, 2)
+        else:
+            k["GB_s"] = round(p["work"] / (p["ms"] * 1e-3) / 1e9, 1)
+        kernels[name] = k
+
+    line = {
+        "metric": METRIC,
+        "value": round(B * a.steps / dt, 2),
+        "unit": "embeddings/sec",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(dt / a.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "config 2: EmbeddingGemma-300M Q8_0 forward, 64 x 512 tokens",
+                   "batch": B, "seq_len": S, "tokens": "U[2,262144) seed 0",
+                   "weights": "random Q8_0 (int8 U[-127,127], fp16 |N(0,1e-3)|) seed 5; norms U[0.5,1.5] seed 2"},
+        "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "kernel": "k_gemm_q8 (all Q8_0 GEMM launches; int8 TOP/s)",
+                     "avg_launch_ms": round(g["ms"] / max(g["launches"], 1), 4)},
+        "kernels": kernels,
+        "gemm_frac_of_step": round(g["ms"] / (dt * 1e3), 3),
+    }
+    model.close()
+    ctx.close()
+    if not a.no_cpu_baseline:
+        threads = a.cpu_threads or min(16, os.cpu_count() or 1)
+        line["cpu_baseline"] = cpu_baseline(mdl, toks, S, threads, a.cpu_seqs or 2 * threads)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,520 @@
+// k_rows.hip -- bandwidth-bound per-row kernels: token embedding, RMSNorm
+// (pre, post, final), per-sequence int8 quantization, QK-norm + RoPE,
+// GELUQuick * up, mean-pool + L2, and the load-time Q8_0 repack.
+//
+// Row kernels give each row to an aligned group of 8 lanes (a wave covers 8
+// rows): lane j of the group owns elements j, j+8, j+16, ... which is the lane
+// structure of the reference's AVX2 fp32 dot product, so RMSNorm's sum of
+// squares is reproduced bit for bit (see sg_rmsnorm8 in sg_device.h).
+#include "sg_device.h"
+#include "sg_kernels.h"
+
+namespace {
+
+constexpr int kRowsPerBlock = 32;  // 256 threads, 8 lanes per row
+constexpr int kThreads = 256;
+
+__device__ __forceinline__ uint16_t rd_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+// ---------------------------------------------------------------- repack --
+
+// One thread per Q8_0 block: 2-byte fp16 scale + 32 int8 values
+// (GGUF Q8_0 layout; extractQ8_0Scales model_int8.go:543-569 reads the same bytes).
+__global__ void k_repack_q8_0(const uint8_t* __restrict__ raw, int rows, int cols, _Float16* __restrict__ w16,
+                              float* __restrict__ st, int ld_st, int row_off) {
+  const int nb = cols / 32;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (int64_t)rows * nb) return;
+  const int r = (int)(id / nb), b = (int)(id % nb);
+  const uint8_t* blk = raw + id * 34;
+  st[(int64_t)b * ld_st + row_off + r] = sg_f16_ieee(rd_u16(blk));
+  _Float16* dst = w16 + (int64_t)(row_off + r) * cols + b * 32;
+#pragma unroll
+  for (int i = 0; i < 32; i += 8) {
+    half8_t v;
+#pragma unroll
+    for (int t = 0; t < 8; t++) v[t] = (_Float16)(float)(int8_t)blk[2 + i + t];
+    *reinterpret_cast<half8_t*>(dst + i) = v;
+  }
+}
+
+// Token table: int8 values plus the block scale through the gguf converter
+// (ParseQ8_0Block gguf/tensor.go:94-112).
+__global__ void k_repack_embd(const uint8_t* __restrict__ raw, int vocab, int d, int8_t* __restrict__ q,
+                              float* __restrict__ sc) {
+  const int nb = d / 32;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= (int64_t)vocab * nb) return;
+  const uint8_t* blk = raw + id * 34;
+  sc[id] = sg_f16_gguf(rd_u16(blk));
+  int8_t* dst = q + id * 32;
+#pragma unroll
+  for (int i = 0; i < 32; i++) dst[i] = (int8_t)blk[2 + i];
+}
+
+__global__ void k_i8_to_f16(const int8_t* __restrict__ x, _Float16* __restrict__ y, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = (_Float16)(float)x[i];
+}
+
+__global__ void k_fill(float* __restrict__ p, float v, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// ------------------------------------------------------------- embedding --
+
+// Embedding (model_int8.go:166-184): h = float32(q) * d' (d' through the
+// halving converter), then h *= float32(sqrt(d)) as a second rounding.
+template <int NPL>
+__device__ __forceinline__ int gather_row(const int32_t* tokens, int row, const int8_t* __restrict__ eq,
+                                          const float* __restrict__ es, int vocab, float sqrt_d, int j,
+                                          float (&x)[NPL], int32_t* err) {
+  constexpr int D = NPL * 8;
+  int id = tokens[row];
+  if (id < 0 || id >= vocab) {
+    if (j == 0) atomicOr(err, 1);
+    id = 0;  // keep the access in bounds; the call reports SG_ERR_TOKEN
+  }
+  const int8_t* qr = eq + (int64_t)id * D;
+  const float* sr = es + (int64_t)id * (D / 32);
+#pragma unroll
+  for (int i = 0; i < NPL; i++) {
+    const int c = 8 * i + j;
+    const float v = (float)qr[c] * sr[c >> 5];
+    x[i] = v * sqrt_d;
+  }
+  return id;
+}
+
+template <int NPL>
+__global__ __launch_bounds__(kThreads) void k_embed_norm(const int32_t* __restrict__ tokens, int T,
+                                                         const int8_t* __restrict__ eq, const float* __restrict__ es,
+                                                         int vocab, float sqrt_d, const float* __restrict__ w,
+                                                         float eps, const int32_t* __restrict__ row_seq,
+                                                         float* __restrict__ h, float* __restrict__ xn,
+                                                         float* __restrict__ amax, int32_t* __restrict__ err) {
+  constexpr int D = NPL * 8;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
+  const int j = threadIdx.x & 7;
+  if (row >= T) return;
+  float x[NPL];
+  gather_row<NPL>(tokens, row, eq, es, vocab, sqrt_d, j, x, err);
+  float* hr = h + (int64_t)row * D;
+#pragma unroll
+  for (int i = 0; i < NPL; i++) hr[8 * i + j] = x[i];
+  sg_rmsnorm8<NPL>(x, w, j, eps);
+  float* yr = xn + (int64_t)row * D;
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NPL; i++) {
+    yr[8 * i + j] = x[i];
+    m = fmaxf(m, fabsf(x[i]));
+  }
+  m = sg_max8(m);
+  if (j == 0 && amax) sg_atomic_max_nonneg(amax + row_seq[row], m);
+}
+
+template <int NPL>
+__global__ __launch_bounds__(kThreads) void k_embed_only(const int32_t* __restrict__ tokens, int T,
+                                                         const int8_t* __restrict__ eq, const float* __restrict__ es,
+                                                         int vocab, float sqrt_d, float* __restrict__ h,
+                                                         int32_t* __restrict__ err) {
+  constexpr int D = NPL * 8;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
+  const int j = threadIdx.x & 7;
+  if (row >= T) return;
+  float x[NPL];
+  gather_row<NPL>(tokens, row, eq, es, vocab, sqrt_d, j, x, err);
+  float* hr = h + (int64_t)row * D;
+#pragma unroll
+  for (int i = 0; i < NPL; i++) hr[8 * i + j] = x[i];
+}
+
+// -------------------------------------------------------------- quantize --
+
+// quantize.go:29-103 with the tensor max replaced by the per-sequence max
+// gathered into amax (one reference call quantizes one sequence):
+// scale = m/127 (fp32), inv = 1/scale (fp32),
+// q = clamp(round_half_away(float64(x)*float64(inv)), +-127); m == 0 -> scale 1, q 0.
+template <bool F16>
+__global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__ x, int ldx, int rows, int cols,
+                                                       const int32_t* __restrict__ row_seq,
+                                                       const float* __restrict__ amax, _Float16* __restrict__ qf,
+                                                       int8_t* __restrict__ qi, float* __restrict__ row_scale) {
+  const int c4n = cols >> 2;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)rows * c4n) return;
+  const int row = (int)(gid / c4n), c4 = (int)(gid % c4n);
+  const float m = amax[row_seq[row]];
+  float scale = 1.0f, inv = 0.0f;
+  if (m != 0.0f) {
+    scale = m / 127.0f;
+    inv = 1.0f / scale;
+  }
+  if (c4 == 0) row_scale[row] = scale;
+  const f32x4_t v = *reinterpret_cast<const f32x4_t*>(x + (int64_t)row * ldx + 4 * c4);
+  int qv[4];
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    int q = 0;
+    if (m != 0.0f) {
+      q = (int)round((double)v[t] * (double)inv);
+      q = q > 127 ? 127 : (q < -127 ? -127 : q);
+    }
+    qv[t] = q;
+  }
+  const int64_t o = (int64_t)row * cols + 4 * c4;
+  if (F16) {
+    half4_t h;
+#pragma unroll
+    for (int t = 0; t < 4; t++) h[t] = (_Float16)(float)qv[t];
+    *reinterpret_cast<half4_t*>(qf + o) = h;
+  } else {
+    char4 c;
+    c.x = (signed char)qv[0]; c.y = (signed char)qv[1]; c.z = (signed char)qv[2]; c.w = (signed char)qv[3];
+    *reinterpret_cast<char4*>(qi + o) = c;
+  }
+}
+
+__global__ void k_seq_scales(const float* __restrict__ amax, int n, float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float m = amax[i];
+  out[i] = m == 0.0f ? 1.0f : m / 127.0f;
+}
+
+// --------------------------------------------------------------- RMSNorm --
+
+template <int NPL>
+__global__ __launch_bounds__(kThreads) void k_rmsnorm(float* dst, const float* src, const float* __restrict__ w,
+                                                      int rows, float eps, const int32_t* __restrict__ row_seq,
+                                                      float* __restrict__ amax) {
+  constexpr int D = NPL * 8;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
+  const int j = threadIdx.x & 7;
+  if (row >= rows) return;
+  float x[NPL];
+  const float* sr = src + (int64_t)row * D;
+#pragma unroll
+  for (int i = 0; i < NPL; i++) x[i] = sr[8 * i + j];
+  sg_rmsnorm8<NPL>(x, w, j, eps);
+  float* dr = dst + (int64_t)row * D;
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NPL; i++) {
+    dr[8 * i + j] = x[i];
+    m = fmaxf(m, fabsf(x[i]));
+  }
+  if (amax) {
+    m = sg_max8(m);
+    if (j == 0) sg_atomic_max_nonneg(amax + row_seq[row], m);
+  }
+}
+
+// h = RMSNorm(o; w_post) + h (model_int8.go:203-210 / :225-232), then
+// xn = RMSNorm(h; w_next) -- the next pre-norm (:194/:216) or output_norm (:236).
+template <int NPL>
+__global__ __launch_bounds__(kThreads) void k_post_res_norm(const float* __restrict__ o, float* __restrict__ h,
+                                                            const float* __restrict__ w_post,
+                                                            const float* __restrict__ w_next, float eps, int T,
+                                                            float* __restrict__ xn,
+                                                            const int32_t* __restrict__ row_seq,
+                                                            float* __restrict__ amax) {
+  constexpr int D = NPL * 8;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
+  const int j = threadIdx.x & 7;
+  if (row >= T) return;
+  float x[NPL];
+  const float* orow = o + (int64_t)row * D;
+#pragma unroll
+  for (int i = 0; i < NPL; i++) x[i] = orow[8 * i + j];
+  if (w_post) sg_rmsnorm8<NPL>(x, w_post, j, eps);
+  float* hr = h + (int64_t)row * D;
+#pragma unroll
+  for (int i = 0; i < NPL; i++) {
+    x[i] = x[i] + hr[8 * i + j];
+    hr[8 * i + j] = x[i];
+  }
+  if (w_next) sg_rmsnorm8<NPL>(x, w_next, j, eps);
+  float* yr = xn + (int64_t)row * D;
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NPL; i++) {
+    yr[8 * i + j] = x[i];
+    m = fmaxf(m, fabsf(x[i]));
+  }
+  if (amax) {
+    m = sg_max8(m);
+    if (j == 0) sg_atomic_max_nonneg(amax + row_seq[row], m);
+  }
+}
+
+// -------------------------------------------------------- QK-norm + RoPE --
+
+// Per (token, head) 8-lane group: RMSNorm over head_dim=256 with
+// attn_q_norm/attn_k_norm (model_int8.go:374-440), then the cached NeoX
+// rotation of pairs (i, i+128) at position p (rope_cache.go:85-104):
+// x0' = x0*c - x1*s, x1' = x0*s + x1*c, every product rounded.  Element
+// 8i+j and its partner 8(i+16)+j live in the same lane.
+__global__ __launch_bounds__(kThreads) void k_qknorm_rope(float* __restrict__ q, int ldq, float* __restrict__ k,
+                                                          int ldk, const float* __restrict__ qw,
+                                                          const float* __restrict__ kw, int H, int HKV, int T,
+                                                          const int32_t* __restrict__ row_pos,
+                                                          const float* __restrict__ cos_t,
+                                                          const float* __restrict__ sin_t, float eps) {
+  constexpr int NPL = 32, HALF = 128;
+  const int g = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
+  const int j = threadIdx.x & 7;
+  const int per = H + HKV;
+  if (g >= T * per) return;
+  const int t = g / per, hh = g % per;
+  float* p;
+  const float* w;
+  if (hh < H) {
+    p = q + (int64_t)t * ldq + hh * 256;
+    w = qw;
+  } else {
+    p = k + (int64_t)t * ldk + (hh - H) * 256;
+    w = kw;
+  }
+  float x[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; i++) x[i] = p[8 * i + j];
+  if (w) sg_rmsnorm8<NPL>(x, w, j, eps);
+  const int pos = row_pos[t];
+  const float* cr = cos_t + (int64_t)pos * HALF;
+  const float* sr = sin_t + (int64_t)pos * HALF;
+#pragma unroll
+  for (int i = 0; i < NPL / 2; i++) {
+    const int e = 8 * i + j;
+    const float c = cr[e], s = sr[e];
+    const float v0 = x[i], v1 = x[i + NPL / 2];
+    const float a = v0 * c, b = v1 * s, cc = v0 * s, dd = v1 * c;
+    x[i] = a - b;
+    x[i + NPL / 2] = cc + dd;
+  }
+#pragma unroll
+  for (int i = 0; i < NPL; i++) p[8 * i + j] = x[i];
+}
+
+// ------------------------------------------------------------ GELU * up --
+
+// GELUQuickSIMD (activation.go:47-95) then VecMulF32 (matmul.go:238-259):
+// g = geluquick(gate) * up, one row per block, plus the row's max|g|.
+__global__ __launch_bounds__(kThreads) void k_gelu_mul(float* __restrict__ g, int ldd, const float* __restrict__ gate,
+                                                       int ldg, const float* __restrict__ up, int ldu, int cols,
+                                                       const int32_t* __restrict__ row_seq,
+                                                       float* __restrict__ amax) {
+  __shared__ float red[kThreads / SG_WAVE];
+  const int row = blockIdx.x;
+  const float* gr = gate + (int64_t)row * ldg;
+  const float* ur = up + (int64_t)row * ldu;
+  float* dr = g + (int64_t)row * ldd;
+  float m = 0.0f;
+  for (int c4 = threadIdx.x; c4 < (cols >> 2); c4 += kThreads) {
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(gr + 4 * c4);
+    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(ur + 4 * c4);
+    f32x4_t r;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      r[t] = sg_gelu_quick(a[t]) * b[t];
+      m = fmaxf(m, fabsf(r[t]));
+    }
+    *reinterpret_cast<f32x4_t*>(dr + 4 * c4) = r;
+  }
+  if (!amax) return;
+  m = sg_wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float mm = red[0];
+    for (int i = 1; i < kThreads / SG_WAVE; i++) mm = fmaxf(mm, red[i]);
+    sg_atomic_max_nonneg(amax + row_seq[row], mm);
+  }
+}
+
+
+// Per-row max|x| folded into the row's sequence maximum (absMaxScalar,
+// quantize.go:80-90, over a whole sequence).
+__global__ __launch_bounds__(kThreads) void k_absmax_rows(const float* __restrict__ x, int ldx, int cols,
+                                                          const int32_t* __restrict__ row_seq,
+                                                          float* __restrict__ amax) {
+  __shared__ float red[kThreads / SG_WAVE];
+  const float* xr = x + (int64_t)blockIdx.x * ldx;
+  float m = 0.0f;
+  for (int c = threadIdx.x; c < cols; c += kThreads) m = fmaxf(m, fabsf(xr[c]));
+  m = sg_wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float mm = red[0];
+    for (int i = 1; i < kThreads / SG_WAVE; i++) mm = fmaxf(mm, red[i]);
+    sg_atomic_max_nonneg(amax + row_seq[blockIdx.x], mm);
+  }
+}
+
+// ---------------------------------------------------------- pool and L2 --
+
+// MeanPoolingPartial (attention.go:423-445): per column, serial sum over the
+// sequence's rows then * (1/float32(S)); l2Normalize (runtime/model.go:808-820):
+// serial sum of squares, norm = float32(sqrt(float64(ss))), v /= norm.
+__global__ __launch_bounds__(kThreads) void k_pool_l2(float* __restrict__ out, const float* __restrict__ x, int ldx,
+                                                      int out_dim, const int32_t* __restrict__ seq_off) {
+  __shared__ float pooled[1024];
+  __shared__ float nrm;
+  const int sq = blockIdx.x;
+  const int r0 = seq_off[sq], S = seq_off[sq + 1] - r0;
+  const float sc = 1.0f / (float)S;
+  for (int c = threadIdx.x; c < out_dim; c += kThreads) {
+    float acc = 0.0f;
+    const float* p = x + (int64_t)r0 * ldx + c;
+    for (int s = 0; s < S; s++) acc = acc + p[(int64_t)s * ldx];
+    pooled[c] = acc * sc;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float ss = 0.0f;
+    for (int c = 0; c < out_dim; c++) {
+      const float t = pooled[c] * pooled[c];
+      ss = ss + t;
+    }
+    nrm = ss == 0.0f ? 0.0f : __fsqrt_rn(ss);
+  }
+  __syncthreads();
+  const float n = nrm;
+  for (int c = threadIdx.x; c < out_dim; c += kThreads)
+    out[(int64_t)sq * out_dim + c] = n == 0.0f ? pooled[c] : pooled[c] / n;
+}
+
+inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+namespace sgk {
+
+hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, float* st, int ld_st, int row_off,
+                       hipStream_t s) {
+  const int64_t n = (int64_t)rows * (cols / 32);
+  hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(n, 256)), dim3(256), 0, s, raw, rows, cols, w16, st, ld_st,
+                     row_off);
+  return hipGetLastError();
+}
+
+hipError_t repack_embd(const uint8_t* raw, int vocab, int d, int8_t* q, float* sc, hipStream_t s) {
+  const int64_t n = (int64_t)vocab * (d / 32);
+  hipLaunchKernelGGL(k_repack_embd, dim3(blocks_for(n, 256)), dim3(256), 0, s, raw, vocab, d, q, sc);
+  return hipGetLastError();
+}
+
+hipError_t i8_to_f16(const int8_t* x, _Float16* y, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_i8_to_f16, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, y, n);
+  return hipGetLastError();
+}
+
+hipError_t fill_f32(float* p, float v, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, v, n);
+  return hipGetLastError();
+}
+
+#define SG_DISPATCH_NPL(n, NPLV, ...)         \
+  switch (n) {                                \
+    case 256: { constexpr int NPLV = 32; __VA_ARGS__; break; }  \
+    case 512: { constexpr int NPLV = 64; __VA_ARGS__; break; }  \
+    case 768: { constexpr int NPLV = 96; __VA_ARGS__; break; }  \
+    case 1024: { constexpr int NPLV = 128; __VA_ARGS__; break; } \
+    case 1152: { constexpr int NPLV = 144; __VA_ARGS__; break; } \
+    default: return hipErrorInvalidValue;     \
+  }
+
+hipError_t embed_norm(const int32_t* tokens, int T, const int8_t* eq, const float* es, int vocab, int d,
+                      float sqrt_d, const float* w, float eps, const int32_t* row_seq, float* h, float* xn,
+                      float* amax, int32_t* err, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  SG_DISPATCH_NPL(d, NPL,
+                  hipLaunchKernelGGL(k_embed_norm<NPL>, dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads), 0, s,
+                                     tokens, T, eq, es, vocab, sqrt_d, w, eps, row_seq, h, xn, amax, err));
+  return hipGetLastError();
+}
+
+hipError_t embed_only(const int32_t* tokens, int T, const int8_t* eq, const float* es, int vocab, int d,
+                      float sqrt_d, float* h, int32_t* err, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  SG_DISPATCH_NPL(d, NPL,
+                  hipLaunchKernelGGL(k_embed_only<NPL>, dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads), 0, s,
+                                     tokens, T, eq, es, vocab, sqrt_d, h, err));
+  return hipGetLastError();
+}
+
+hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
+                    _Float16* f16, int8_t* i8, float* row_scale, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (cols % 4 || ldx % 4) return hipErrorInvalidValue;
+  const int64_t n = (int64_t)rows * (cols / 4);
+  if (f16)
+    hipLaunchKernelGGL(k_quantize<true>, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, s, x, ldx, rows, cols,
+                       row_seq, amax, f16, nullptr, row_scale);
+  else
+    hipLaunchKernelGGL(k_quantize<false>, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, s, x, ldx, rows, cols,
+                       row_seq, amax, nullptr, i8, row_scale);
+  return hipGetLastError();
+}
+
+hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(k_seq_scales, dim3(blocks_for(n_seq, 256)), dim3(256), 0, s, amax, n_seq, out);
+  return hipGetLastError();
+}
+
+hipError_t rmsnorm(float* dst, const float* src, const float* w, int rows, int n, float eps, const int32_t* row_seq,
+                   float* amax, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  SG_DISPATCH_NPL(n, NPL,
+                  hipLaunchKernelGGL(k_rmsnorm<NPL>, dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0, s,
+                                     dst, src, w, rows, eps, row_seq, amax));
+  return hipGetLastError();
+}
+
+hipError_t qknorm_rope(float* q, int ldq, float* k, int ldk, const float* qw, const float* kw, int H, int HKV, int T,
+                       const int32_t* row_pos, const float* cos_t, const float* sin_t, float eps, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  const int64_t groups = (int64_t)T * (H + HKV);
+  hipLaunchKernelGGL(k_qknorm_rope, dim3(blocks_for(groups, kRowsPerBlock)), dim3(kThreads), 0, s, q, ldq, k, ldk,
+                     qw, kw, H, HKV, T, row_pos, cos_t, sin_t, eps);
+  return hipGetLastError();
+}
+
+hipError_t post_res_norm(const float* o, float* h, const float* w_post, const float* w_next, float eps, int T, int d,
+                         float* xn, const int32_t* row_seq, float* amax, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  SG_DISPATCH_NPL(d, NPL,
+                  hipLaunchKernelGGL(k_post_res_norm<NPL>, dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads), 0,
+                                     s, o, h, w_post, w_next, eps, T, xn, row_seq, amax));
+  return hipGetLastError();
+}
+
+hipError_t gelu_mul(float* g, int ldd, const float* gate, int ldg, const float* up, int ldu, int rows, int cols,
+                    const int32_t* row_seq, float* amax, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (cols % 4 || ldd % 4 || ldg % 4 || ldu % 4) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_gelu_mul, dim3(rows), dim3(kThreads), 0, s, g, ldd, gate, ldg, up, ldu, cols, row_seq, amax);
+  return hipGetLastError();
+}
+
+hipError_t pool_l2(float* out, const float* x, int ldx, int out_dim, const int32_t* seq_off, int n_seq,
+                   hipStream_t s) {
+  if (n_seq <= 0) return hipSuccess;
+  if (out_dim > 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pool_l2, dim3(n_seq), dim3(kThreads), 0, s, out, x, ldx, out_dim, seq_off);
+  return hipGetLastError();
+}
+
+hipError_t absmax_rows(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, float* amax,
+                       hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_absmax_rows, dim3(rows), dim3(kThreads), 0, s, x, ldx, cols, row_seq, amax);
+  return hipGetLastError();
+}
+
+}  // namespace sgk

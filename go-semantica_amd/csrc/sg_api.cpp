@@ -1,0 +1,840 @@
+// sg_api.cpp -- the C ABI of libsemantica_gpu.so: context, model upload and
+// repack, the batched forward orchestration and the kernel-seam entry points.
+//
+// The forward replaces forwardINT8WithDim (internal/runtime/model_int8.go:148-256)
+// for a packed batch of sequences.  Per layer the reference op order is kept:
+//   RMSNorm -> quantize -> Q/K/V GEMM -> QK-norm -> RoPE -> attention -> quantize
+//   -> O GEMM -> post-norm -> +residual -> RMSNorm -> quantize -> gate/up GEMM
+//   -> GELUQuick*up -> quantize -> down GEMM -> post-norm -> +residual
+// with Q/K/V and gate/up fused into one GEMM each (weights concatenated by
+// row; every output column is computed exactly as before) and each
+// post-norm + residual fused with the following pre-norm.
+#include "semantica_gpu.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "sg_kernels.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define SG_HIP(call)                                                                                     \
+  do {                                                                                                   \
+    hipError_t e_ = (call);                                                                              \
+    if (e_ != hipSuccess)                                                                                \
+      return fail(e_ == hipErrorInvalidValue ? SG_ERR_INVALID : SG_ERR_DEVICE, "%s: %s (%s:%d)", #call,  \
+                  hipGetErrorString(e_), __FILE__, __LINE__);                                            \
+  } while (0)
+
+#define SG_TRY(expr)        \
+  do {                      \
+    int r_ = (expr);        \
+    if (r_ != SG_OK) return r_; \
+  } while (0)
+
+// Grow-only device buffer.
+struct DevBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  template <typename T>
+  T* as() const { return static_cast<T*>(p); }
+  int ensure(size_t bytes) {
+    if (bytes <= n) return SG_OK;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+    if (bytes == 0) return SG_OK;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+      p = nullptr;
+      return fail(SG_ERR_NOMEM, "hipMalloc(%zu bytes) failed", bytes);
+    }
+    n = bytes;
+    return SG_OK;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+};
+
+// Grow-only pinned host buffer (staging for metadata / small copies).
+struct HostBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  template <typename T>
+  T* as() const { return static_cast<T*>(p); }
+  int ensure(size_t bytes) {
+    if (bytes <= n) return SG_OK;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    n = 0;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+      p = nullptr;
+      return fail(SG_ERR_NOMEM, "hipHostMalloc(%zu bytes) failed", bytes);
+    }
+    n = bytes;
+    return SG_OK;
+  }
+  void release() {
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    n = 0;
+  }
+};
+
+// Per-call sequence metadata built on the host from CSR offsets.
+struct Meta {
+  int T = 0, n_seq = 0, n_items = 0;
+  double sum_sq = 0;  // sum over sequences of S^2 (attention work)
+  // device views into one buffer
+  int32_t* row_seq = nullptr;
+  int32_t* row_pos = nullptr;
+  int32_t* seq_off = nullptr;
+  sg_item* items = nullptr;
+};
+
+size_t meta_bytes(int T, int n_seq, int n_items) {
+  return sizeof(int32_t) * ((size_t)2 * T + n_seq + 1) + sizeof(sg_item) * (size_t)n_items + 64;
+}
+
+int count_items(const int32_t* off, int n_seq) {
+  int n = 0;
+  for (int i = 0; i < n_seq; i++) n += (off[i + 1] - off[i] + 31) / 32;
+  return n;
+}
+
+// Fills `host` with [row_seq | row_pos | seq_off | items] and copies it to
+// `dev` on stream s (the copy is complete when this returns).
+int stage_meta(const int32_t* off, int n_seq, HostBuf& host, DevBuf& dev, hipStream_t s, Meta& m) {
+  const int T = off[n_seq];
+  const int n_items = count_items(off, n_seq);
+  const size_t bytes = meta_bytes(T, n_seq, n_items);
+  SG_TRY(host.ensure(bytes));
+  SG_TRY(dev.ensure(bytes));
+  int32_t* h = host.as<int32_t>();
+  int32_t* rs = h;
+  int32_t* rp = rs + T;
+  int32_t* so = rp + T;
+  sg_item* it = reinterpret_cast<sg_item*>(so + n_seq + 1);
+  int k = 0;
+  for (int i = 0; i < n_seq; i++) {
+    so[i] = off[i];
+    for (int r = off[i]; r < off[i + 1]; r++) {
+      rs[r] = i;
+      rp[r] = r - off[i];
+    }
+    for (int q0 = 0; q0 < off[i + 1] - off[i]; q0 += 32) it[k++] = sg_item{i, q0};
+  }
+  so[n_seq] = off[n_seq];
+  SG_HIP(hipMemcpyAsync(dev.p, host.p, bytes, hipMemcpyHostToDevice, s));
+  SG_HIP(hipStreamSynchronize(s));
+  int32_t* d = dev.as<int32_t>();
+  m.T = T;
+  m.n_seq = n_seq;
+  m.sum_sq = 0;
+  for (int i = 0; i < n_seq; i++) m.sum_sq += (double)(off[i + 1] - off[i]) * (off[i + 1] - off[i]);
+  m.n_items = n_items;
+  m.row_seq = d;
+  m.row_pos = d + T;
+  m.seq_off = d + 2 * T;
+  m.items = reinterpret_cast<sg_item*>(d + 2 * T + n_seq + 1);
+  return SG_OK;
+}
+
+// Offsets sanity for the kernel seam (sizes only; the model seam applies the
+// reference's error cases).
+int check_offsets(const int32_t* off, int n_seq, int rows) {
+  if (!off || n_seq <= 0) return fail(SG_ERR_INVALID, "seq_offsets must describe at least one sequence");
+  if (off[0] != 0) return fail(SG_ERR_INVALID, "seq_offsets[0] must be 0");
+  for (int i = 0; i < n_seq; i++)
+    if (off[i + 1] < off[i]) return fail(SG_ERR_INVALID, "seq_offsets must be non-decreasing");
+  if (rows >= 0 && off[n_seq] != rows)
+    return fail(SG_ERR_INVALID, "seq_offsets[n_seq]=%d does not match rows=%d", off[n_seq], rows);
+  return SG_OK;
+}
+
+// NewRoPECache (internal/kernels/rope_cache.go:15-44): freq_i =
+// float32(1/pow(base, 2i/hd)) in float64; theta = float32(p) * freq_i in
+// float32; cos/sin evaluated in float64 and rounded to float32.
+void rope_tables(int hd, float base, int max_pos, std::vector<float>& c, std::vector<float>& s) {
+  const int half = hd / 2;
+  std::vector<float> freq(half);
+  for (int i = 0; i < half; i++) freq[i] = (float)(1.0 / std::pow((double)base, (double)(2 * i) / (double)hd));
+  c.resize((size_t)max_pos * half);
+  s.resize((size_t)max_pos * half);
+  for (int p = 0; p < max_pos; p++) {
+    const float pf = (float)p;
+    for (int i = 0; i < half; i++) {
+      const float th = pf * freq[i];
+      c[(size_t)p * half + i] = (float)std::cos((double)th);
+      s[(size_t)p * half + i] = (float)std::sin((double)th);
+    }
+  }
+}
+
+}  // namespace
+
+struct sg_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::mutex mu;  // guards the scratch below for the kernel seam
+  HostBuf meta_h;
+  DevBuf meta_d, f16, amax, tab;
+};
+
+struct sg_q8_weight {
+  sg_ctx* ctx = nullptr;
+  int N = 0, K = 0;
+  _Float16* w = nullptr;  // [N][K]
+  float* st = nullptr;    // [K/32][N]
+};
+
+namespace {
+
+struct LayerDev {
+  _Float16 *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wd = nullptr;
+  float *sqkv = nullptr, *so = nullptr, *sgu = nullptr, *sd = nullptr;
+  float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+  float *post_attn = nullptr, *ffn_norm = nullptr, *post_ffw = nullptr;
+};
+
+hipStream_t pick(sg_ctx* c, void* stream) { return stream ? static_cast<hipStream_t>(stream) : c->stream; }
+
+int set_device(sg_ctx* c) {
+  SG_HIP(hipSetDevice(c->device));
+  return SG_OK;
+}
+
+}  // namespace
+
+// Event-bracketed launch accounting for sg_profile_* (events are pooled and
+// reused across forwards; records are folded in after each forward's sync).
+struct Profiler {
+  bool on = false;
+  std::vector<hipEvent_t> pool;
+  size_t used = 0;
+  struct Rec {
+    int cls;
+    hipEvent_t a, b;
+    double work;
+  };
+  std::vector<Rec> recs;
+  sg_profile acc{};
+  hipEvent_t next() {
+    if (used == pool.size()) {
+      hipEvent_t e = nullptr;
+      if (hipEventCreate(&e) != hipSuccess) return nullptr;
+      pool.push_back(e);
+    }
+    return pool[used++];
+  }
+  int fold() {
+    for (const Rec& r : recs) {
+      float ms = 0.f;
+      SG_HIP(hipEventElapsedTime(&ms, r.a, r.b));
+      acc.ms[r.cls] += ms;
+      acc.work[r.cls] += r.work;
+      acc.launches[r.cls] += 1;
+    }
+    recs.clear();
+    used = 0;
+    return SG_OK;
+  }
+  ~Profiler() {
+    for (hipEvent_t e : pool) (void)hipEventDestroy(e);
+  }
+};
+
+struct sg_model {
+  sg_ctx* ctx = nullptr;
+  Profiler prof;
+  sg_model_config cfg{};
+  int hd = 0, qd = 0, kvd = 0, nqkv = 0;
+  float attn_scale = 0.f, sqrt_d = 0.f;
+  std::vector<void*> allocs;
+  int8_t* emb_q = nullptr;
+  float* emb_s = nullptr;
+  float* out_norm = nullptr;
+  float *cos_t = nullptr, *sin_t = nullptr;
+  std::vector<LayerDev> layers;
+  // forward workspace (grown on demand)
+  DevBuf h, xn, qkv, att, o, gu, g, a16, sx, amax, meta_d, tokens, out, err;
+  HostBuf meta_h, io_h;
+  std::mutex mu;
+
+  template <typename T>
+  int alloc(T** p, size_t count) {
+    void* q = nullptr;
+    if (hipMalloc(&q, sizeof(T) * count) != hipSuccess) return fail(SG_ERR_NOMEM, "hipMalloc failed (model)");
+    allocs.push_back(q);
+    *p = static_cast<T*>(q);
+    return SG_OK;
+  }
+  ~sg_model() {
+    for (void* p : allocs) (void)hipFree(p);
+    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &gu, &g, &a16, &sx, &amax, &meta_d, &tokens, &out, &err}) b->release();
+    meta_h.release();
+    io_h.release();
+  }
+};
+
+namespace {
+
+int upload_f32(sg_model* m, float** dst, const float* src, int n) {
+  if (!src) {
+    *dst = nullptr;
+    return SG_OK;
+  }
+  SG_TRY(m->alloc(dst, (size_t)n));
+  SG_HIP(hipMemcpy(*dst, src, sizeof(float) * n, hipMemcpyHostToDevice));
+  return SG_OK;
+}
+
+// Copies one raw Q8_0 matrix through `stage` and repacks it into rows
+// [row_off, row_off+rows) of w16 / columns of st.
+int upload_q8(const void* raw, int rows, int cols, DevBuf& stage, _Float16* w16, float* st, int ld_st, int row_off,
+              hipStream_t s) {
+  if (!raw) return fail(SG_ERR_INVALID, "missing Q8_0 tensor");
+  const size_t bytes = (size_t)rows * (cols / 32) * 34;
+  SG_TRY(stage.ensure(bytes));
+  SG_HIP(hipMemcpyAsync(stage.p, raw, bytes, hipMemcpyHostToDevice, s));
+  SG_HIP(sgk::repack_q8_0(stage.as<uint8_t>(), rows, cols, w16, st, ld_st, row_off, s));
+  SG_HIP(hipStreamSynchronize(s));
+  return SG_OK;
+}
+
+int validate_config(const sg_model_config& c) {
+  if (c.embed_dim <= 0 || c.num_layers <= 0 || c.num_heads <= 0 || c.num_kv_heads <= 0 || c.interm_dim <= 0 ||
+      c.max_seq_len <= 0 || c.vocab_size <= 0)
+    return fail(SG_ERR_INVALID, "model config has a non-positive dimension");
+  if (c.embed_dim % c.num_heads) return fail(SG_ERR_INVALID, "embed_dim %% num_heads != 0");
+  const int hd = c.embed_dim / c.num_heads;
+  if (hd != 256) return fail(SG_ERR_INVALID, "head_dim %d unsupported (kernels are built for 256)", hd);
+  if (c.num_heads % c.num_kv_heads || c.num_heads / c.num_kv_heads > 4)
+    return fail(SG_ERR_INVALID, "num_heads/num_kv_heads must be an integer <= 4");
+  if (c.embed_dim != 256 && c.embed_dim != 512 && c.embed_dim != 768 && c.embed_dim != 1024)
+    return fail(SG_ERR_INVALID, "embed_dim %d unsupported (256/512/768/1024)", c.embed_dim);
+  if (c.interm_dim % 32) return fail(SG_ERR_INVALID, "feed_forward_length must be a multiple of 32");
+  return SG_OK;
+}
+
+// Launch wrapper: with profiling on, brackets the launch with events on `s`.
+#define SG_LAUNCH(cls, work, call)                                   \
+  do {                                                               \
+    hipEvent_t a_ = nullptr;                                         \
+    if (m->prof.on && (a_ = m->prof.next())) SG_HIP(hipEventRecord(a_, s)); \
+    SG_HIP(call);                                                    \
+    if (a_) {                                                        \
+      hipEvent_t b_ = m->prof.next();                                \
+      if (b_) {                                                      \
+        SG_HIP(hipEventRecord(b_, s));                               \
+        m->prof.recs.push_back(Profiler::Rec{cls, a_, b_, (double)(work)}); \
+      }                                                              \
+    }                                                                \
+  } while (0)
+
+// The per-layer launch sequence.  amax sites per layer: 0 pre-attention
+// norm, 1 attention output, 2 pre-FFN norm, 3 GELU*up; each [n_seq].
+// Work figures are the algorithmic ones: 2*M*N*K int8 ops per GEMM,
+// 4*H*hd*S^2 flops per sequence for attention, and bytes read + written at
+// the reference's dtypes (fp32 activations, int8 quantized) elsewhere.
+int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_dim, float* d_out, hipStream_t s) {
+  const sg_model_config& c = m->cfg;
+  const int T = meta.T, ns = meta.n_seq, d = c.embed_dim, ff = c.interm_dim, L = c.num_layers;
+  const int qd = m->qd, kvd = m->kvd, nqkv = m->nqkv;
+  float* h = m->h.as<float>();
+  float* xn = m->xn.as<float>();
+  float* qkv = m->qkv.as<float>();
+  float* att = m->att.as<float>();
+  float* o = m->o.as<float>();
+  float* gu = m->gu.as<float>();
+  float* g = m->g.as<float>();
+  _Float16* a16 = m->a16.as<_Float16>();
+  float* sx = m->sx.as<float>();
+  float* amax = m->amax.as<float>();
+  auto site = [&](int l, int k) { return amax + ((size_t)4 * l + k) * ns; };
+  const float eps = c.norm_eps;
+  const double t = T;
+  auto gemm_ops = [&](int N, int K) { return 2.0 * t * N * K; };
+  auto quant_bytes = [&](int K) { return t * K * 5.0; };
+  const double attn_flops = 4.0 * c.num_heads * m->hd * meta.sum_sq;
+  const double attn_bytes = t * (2.0 * qd + 2.0 * kvd) * 4.0;
+  (void)attn_bytes;
+
+  SG_LAUNCH(SG_K_OTHER, 4.0 * 4 * L * ns, sgk::fill_f32(amax, 0.0f, (int64_t)4 * L * ns, s));
+  SG_LAUNCH(SG_K_OTHER, 4.0, sgk::fill_f32(m->err.as<float>(), 0.0f, 1, s));
+  SG_LAUNCH(SG_K_NORM, t * (34.0 * d / 32 + 8.0 * d),
+            sgk::embed_norm(d_tokens, T, m->emb_q, m->emb_s, c.vocab_size, d, m->sqrt_d, m->layers[0].attn_norm,
+                            eps, meta.row_seq, h, xn, site(0, 0), m->err.as<int32_t>(), s));
+  for (int l = 0; l < L; l++) {
+    const LayerDev& ly = m->layers[l];
+    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 0), a16, nullptr, sx, s));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), sgk::gemm_q8(a16, ly.wqkv, ly.sqkv, sx, qkv, nullptr, T, nqkv, d, s));
+    SG_LAUNCH(SG_K_NORM, t * (qd + kvd) * 8.0,
+              sgk::qknorm_rope(qkv, nqkv, qkv + qd, nqkv, ly.q_norm, ly.k_norm, c.num_heads, c.num_kv_heads, T,
+                               meta.row_pos, m->cos_t, m->sin_t, eps, s));
+    SG_LAUNCH(SG_K_ATTENTION, attn_flops,
+              sgk::attention(qkv, nqkv, qkv + qd, qkv + qd + kvd, nqkv, att, qd, meta.seq_off, meta.items,
+                             meta.n_items, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale, site(l, 1), s));
+    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), sgk::quantize(att, qd, T, qd, meta.row_seq, site(l, 1), a16, nullptr, sx, s));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), sgk::gemm_q8(a16, ly.wo, ly.so, sx, o, nullptr, T, d, qd, s));
+    SG_LAUNCH(SG_K_NORM, t * d * 16.0,
+              sgk::post_res_norm(o, h, ly.post_attn, ly.ffn_norm, eps, T, d, xn, meta.row_seq, site(l, 2), s));
+    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 2), a16, nullptr, sx, s));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(2 * ff, d), sgk::gemm_q8(a16, ly.wgu, ly.sgu, sx, gu, nullptr, T, 2 * ff, d, s));
+    SG_LAUNCH(SG_K_GELU, t * ff * 12.0,
+              sgk::gelu_mul(g, ff, gu, 2 * ff, gu + ff, 2 * ff, T, ff, meta.row_seq, site(l, 3), s));
+    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(ff), sgk::quantize(g, ff, T, ff, meta.row_seq, site(l, 3), a16, nullptr, sx, s));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), sgk::gemm_q8(a16, ly.wd, ly.sd, sx, o, nullptr, T, d, ff, s));
+    const bool last = l + 1 == L;
+    SG_LAUNCH(SG_K_NORM, t * d * 16.0,
+              sgk::post_res_norm(o, h, ly.post_ffw, last ? m->out_norm : m->layers[l + 1].attn_norm, eps, T, d, xn,
+                                 meta.row_seq, last ? nullptr : site(l + 1, 0), s));
+  }
+  SG_LAUNCH(SG_K_POOL, 4.0 * out_dim * (t + ns), sgk::pool_l2(d_out, xn, d, out_dim, meta.seq_off, ns, s));
+  return SG_OK;
+}
+
+// Reference error cases (forwardINT8WithDim model_int8.go:150-155 per
+// sequence, ForwardWithDim model.go:661-667 for the dimension).
+int check_forward_args(const sg_model* m, const int32_t* off, int n_seq, int out_dim) {
+  const sg_model_config& c = m->cfg;
+  if (out_dim <= 0 || out_dim > c.embed_dim)
+    return fail(SG_ERR_DIM, "target dimension %d out of range (1..%d)", out_dim, c.embed_dim);
+  if (!off || n_seq <= 0) return fail(SG_ERR_INVALID, "no sequences");
+  if (off[0] != 0) return fail(SG_ERR_INVALID, "seq_offsets[0] must be 0");
+  for (int i = 0; i < n_seq; i++) {
+    const int S = off[i + 1] - off[i];
+    if (S < 0) return fail(SG_ERR_INVALID, "seq_offsets must be non-decreasing");
+    if (S == 0) return fail(SG_ERR_EMPTY, "empty input");
+    if (S > c.max_seq_len) return fail(SG_ERR_TOO_LONG, "sequence too long: %d > %d", S, c.max_seq_len);
+  }
+  return SG_OK;
+}
+
+int ensure_workspace(sg_model* m, int T, int n_seq) {
+  const sg_model_config& c = m->cfg;
+  const size_t t = (size_t)T;
+  const int amax_cols = c.embed_dim > c.interm_dim ? c.embed_dim : c.interm_dim;
+  const int a_cols = amax_cols > m->qd ? amax_cols : m->qd;
+  SG_TRY(m->h.ensure(sizeof(float) * t * c.embed_dim));
+  SG_TRY(m->xn.ensure(sizeof(float) * t * c.embed_dim));
+  SG_TRY(m->qkv.ensure(sizeof(float) * t * m->nqkv));
+  SG_TRY(m->att.ensure(sizeof(float) * t * m->qd));
+  SG_TRY(m->o.ensure(sizeof(float) * t * c.embed_dim));
+  SG_TRY(m->gu.ensure(sizeof(float) * t * 2 * c.interm_dim));
+  SG_TRY(m->g.ensure(sizeof(float) * t * c.interm_dim));
+  SG_TRY(m->a16.ensure(sizeof(_Float16) * t * a_cols));
+  SG_TRY(m->sx.ensure(sizeof(float) * t));
+  SG_TRY(m->amax.ensure(sizeof(float) * 4 * (size_t)c.num_layers * n_seq));
+  SG_TRY(m->err.ensure(64));
+  return SG_OK;
+}
+
+int forward_device_locked(sg_model* m, const int32_t* d_tokens, const int32_t* off, int n_seq, int out_dim,
+                          float* d_out, hipStream_t s) {
+  SG_TRY(check_forward_args(m, off, n_seq, out_dim));
+  SG_TRY(set_device(m->ctx));
+  const int T = off[n_seq];
+  SG_TRY(ensure_workspace(m, T, n_seq));
+  Meta meta;
+  SG_TRY(stage_meta(off, n_seq, m->meta_h, m->meta_d, s, meta));
+  SG_TRY(run_forward(m, d_tokens, meta, out_dim, d_out, s));
+  SG_TRY(m->io_h.ensure(64));
+  SG_HIP(hipMemcpyAsync(m->io_h.p, m->err.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  SG_HIP(hipStreamSynchronize(s));
+  if (m->prof.on) SG_TRY(m->prof.fold());
+  if (*m->io_h.as<int32_t>() != 0) return fail(SG_ERR_TOKEN, "token ID out of range");
+  return SG_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sg_last_error(void) { return g_err.c_str(); }
+int sg_abi_version(void) { return SG_ABI_VERSION; }
+
+int sg_init(int device_ordinal, sg_ctx** out) {
+  if (!out) return fail(SG_ERR_INVALID, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  SG_HIP(hipGetDeviceCount(&n));
+  if (device_ordinal < 0 || device_ordinal >= n)
+    return fail(SG_ERR_INVALID, "device %d out of range (%d devices)", device_ordinal, n);
+  SG_HIP(hipSetDevice(device_ordinal));
+  sg_ctx* c = new sg_ctx;
+  c->device = device_ordinal;
+  // A blocking stream (default flags and priority): it orders with the legacy
+  // default stream, so callers that stage data there need no extra sync.
+  if (hipStreamCreate(&c->stream) != hipSuccess) {
+    delete c;
+    return fail(SG_ERR_DEVICE, "hipStreamCreate failed");
+  }
+  *out = c;
+  return SG_OK;
+}
+
+void sg_shutdown(sg_ctx* c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  c->meta_h.release();
+  c->meta_d.release();
+  c->f16.release();
+  c->amax.release();
+  c->tab.release();
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+int sg_model_load(sg_ctx* ctx, const sg_model_desc* desc, sg_model** out) {
+  if (!ctx || !desc || !out) return fail(SG_ERR_INVALID, "NULL argument");
+  *out = nullptr;
+  SG_TRY(validate_config(desc->config));
+  if (!desc->token_embd || !desc->layers) return fail(SG_ERR_INVALID, "token_embd and layers are required");
+  SG_TRY(set_device(ctx));
+  sg_model* m = new sg_model;
+  m->ctx = ctx;
+  m->cfg = desc->config;
+  const sg_model_config& c = m->cfg;
+  m->hd = c.embed_dim / c.num_heads;
+  m->qd = c.num_heads * m->hd;
+  m->kvd = c.num_kv_heads * m->hd;
+  m->nqkv = m->qd + 2 * m->kvd;
+  m->attn_scale = 1.0f / (float)std::sqrt((double)m->hd);  // parseConfig model.go:475
+  m->sqrt_d = (float)std::sqrt((double)c.embed_dim);       // model_int8.go:181
+  hipStream_t s = ctx->stream;
+  DevBuf stage;
+  auto done = [&](int r) {
+    stage.release();
+    if (r != SG_OK) delete m;
+    return r;
+  };
+  const int d = c.embed_dim, ff = c.interm_dim, qd = m->qd, kvd = m->kvd;
+  int r;
+  // token table
+  if ((r = m->alloc(&m->emb_q, (size_t)c.vocab_size * d)) || (r = m->alloc(&m->emb_s, (size_t)c.vocab_size * (d / 32))))
+    return done(r);
+  {
+    const size_t bytes = (size_t)c.vocab_size * (d / 32) * 34;
+    if ((r = stage.ensure(bytes))) return done(r);
+    if (hipMemcpy(stage.p, desc->token_embd, bytes, hipMemcpyHostToDevice) != hipSuccess)
+      return done(fail(SG_ERR_DEVICE, "token_embd upload failed"));
+    if (sgk::repack_embd(stage.as<uint8_t>(), c.vocab_size, d, m->emb_q, m->emb_s, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+      return done(fail(SG_ERR_DEVICE, "token_embd repack failed"));
+  }
+  if ((r = upload_f32(m, &m->out_norm, desc->output_norm, d))) return done(r);
+  {
+    std::vector<float> ct, st;
+    rope_tables(m->hd, c.rope_base, c.max_seq_len, ct, st);
+    if ((r = m->alloc(&m->cos_t, ct.size())) || (r = m->alloc(&m->sin_t, st.size()))) return done(r);
+    if (hipMemcpy(m->cos_t, ct.data(), sizeof(float) * ct.size(), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m->sin_t, st.data(), sizeof(float) * st.size(), hipMemcpyHostToDevice) != hipSuccess)
+      return done(fail(SG_ERR_DEVICE, "rope table upload failed"));
+  }
+  m->layers.resize(c.num_layers);
+  for (int l = 0; l < c.num_layers; l++) {
+    const sg_layer_desc& ld = desc->layers[l];
+    LayerDev& ly = m->layers[l];
+    const int nqkv = m->nqkv;
+    if ((r = m->alloc(&ly.wqkv, (size_t)nqkv * d)) || (r = m->alloc(&ly.sqkv, (size_t)(d / 32) * nqkv)) ||
+        (r = m->alloc(&ly.wo, (size_t)d * qd)) || (r = m->alloc(&ly.so, (size_t)(qd / 32) * d)) ||
+        (r = m->alloc(&ly.wgu, (size_t)2 * ff * d)) || (r = m->alloc(&ly.sgu, (size_t)(d / 32) * 2 * ff)) ||
+        (r = m->alloc(&ly.wd, (size_t)d * ff)) || (r = m->alloc(&ly.sd, (size_t)(ff / 32) * d)))
+      return done(r);
+    if ((r = upload_q8(ld.attn_q, qd, d, stage, ly.wqkv, ly.sqkv, nqkv, 0, s)) ||
+        (r = upload_q8(ld.attn_k, kvd, d, stage, ly.wqkv, ly.sqkv, nqkv, qd, s)) ||
+        (r = upload_q8(ld.attn_v, kvd, d, stage, ly.wqkv, ly.sqkv, nqkv, qd + kvd, s)) ||
+        (r = upload_q8(ld.attn_output, d, qd, stage, ly.wo, ly.so, d, 0, s)) ||
+        (r = upload_q8(ld.ffn_gate, ff, d, stage, ly.wgu, ly.sgu, 2 * ff, 0, s)) ||
+        (r = upload_q8(ld.ffn_up, ff, d, stage, ly.wgu, ly.sgu, 2 * ff, ff, s)) ||
+        (r = upload_q8(ld.ffn_down, d, ff, stage, ly.wd, ly.sd, d, 0, s)))
+      return done(r);
+    if (!ld.attn_norm || !ld.ffn_norm) return done(fail(SG_ERR_INVALID, "layer %d: attn_norm/ffn_norm required", l));
+    if ((r = upload_f32(m, &ly.attn_norm, ld.attn_norm, d)) || (r = upload_f32(m, &ly.q_norm, ld.attn_q_norm, m->hd)) ||
+        (r = upload_f32(m, &ly.k_norm, ld.attn_k_norm, m->hd)) ||
+        (r = upload_f32(m, &ly.post_attn, ld.post_attention_norm, d)) ||
+        (r = upload_f32(m, &ly.ffn_norm, ld.ffn_norm, d)) || (r = upload_f32(m, &ly.post_ffw, ld.post_ffw_norm, d)))
+      return done(r);
+  }
+  *out = m;
+  return done(SG_OK);
+}
+
+void sg_model_free(sg_model* m) {
+  if (!m) return;
+  (void)hipSetDevice(m->ctx->device);
+  (void)hipDeviceSynchronize();
+  delete m;
+}
+
+int sg_forward_device(sg_model* m, const int32_t* d_tokens, const int32_t* seq_offsets, int32_t n_seq,
+                      int32_t out_dim, float* d_out, void* stream) {
+  if (!m || !d_tokens || !d_out) return fail(SG_ERR_INVALID, "NULL argument");
+  std::lock_guard<std::mutex> lk(m->mu);
+  return forward_device_locked(m, d_tokens, seq_offsets, n_seq, out_dim, d_out, pick(m->ctx, stream));
+}
+
+int sg_forward(sg_model* m, const int32_t* tokens, const int32_t* off, int32_t n_seq, int32_t out_dim, float* out) {
+  if (!m || !tokens || !out) return fail(SG_ERR_INVALID, "NULL argument");
+  std::lock_guard<std::mutex> lk(m->mu);
+  SG_TRY(check_forward_args(m, off, n_seq, out_dim));
+  const int T = off[n_seq];
+  // Sequences are checked in order, each fully (length, then tokens), so the
+  // error returned is the one the reference's request-ordered fan-out reports
+  // first (api.go:286-292; model_int8.go:150-171).
+  for (int sq = 0; sq < n_seq; sq++) {
+    const int S = off[sq + 1] - off[sq];
+    if (S == 0) return fail(SG_ERR_EMPTY, "empty input");
+    if (S > m->cfg.max_seq_len) return fail(SG_ERR_TOO_LONG, "sequence too long: %d > %d", S, m->cfg.max_seq_len);
+    for (int i = off[sq]; i < off[sq + 1]; i++)
+      if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab_size)
+        return fail(SG_ERR_TOKEN, "token ID out of range: %d", tokens[i]);
+  }
+  SG_TRY(set_device(m->ctx));
+  hipStream_t s = m->ctx->stream;
+  SG_TRY(m->tokens.ensure(sizeof(int32_t) * (size_t)T));
+  SG_TRY(m->out.ensure(sizeof(float) * (size_t)n_seq * out_dim));
+  SG_HIP(hipMemcpyAsync(m->tokens.p, tokens, sizeof(int32_t) * (size_t)T, hipMemcpyHostToDevice, s));
+  SG_TRY(forward_device_locked(m, m->tokens.as<int32_t>(), off, n_seq, out_dim, m->out.as<float>(), s));
+  SG_HIP(hipMemcpyAsync(out, m->out.p, sizeof(float) * (size_t)n_seq * out_dim, hipMemcpyDeviceToHost, s));
+  SG_HIP(hipStreamSynchronize(s));
+  return SG_OK;
+}
+
+int sg_profile_enable(sg_model* m, int on) {
+  if (!m) return fail(SG_ERR_INVALID, "NULL argument");
+  std::lock_guard<std::mutex> lk(m->mu);
+  m->prof.on = on != 0;
+  m->prof.recs.clear();
+  m->prof.used = 0;
+  m->prof.acc = sg_profile{};
+  return SG_OK;
+}
+
+int sg_profile_read(sg_model* m, sg_profile* out) {
+  if (!m || !out) return fail(SG_ERR_INVALID, "NULL argument");
+  std::lock_guard<std::mutex> lk(m->mu);
+  SG_TRY(set_device(m->ctx));
+  SG_HIP(hipStreamSynchronize(m->ctx->stream));
+  SG_TRY(m->prof.fold());
+  *out = m->prof.acc;
+  return SG_OK;
+}
+
+// ---- kernel seam ----------------------------------------------------------
+
+int sg_q8_weight_create(sg_ctx* ctx, const void* q8, int32_t out_dim, int32_t in_dim, sg_q8_weight** out) {
+  if (!ctx || !q8 || !out) return fail(SG_ERR_INVALID, "NULL argument");
+  *out = nullptr;
+  if (out_dim <= 0 || in_dim <= 0 || in_dim % 32) return fail(SG_ERR_INVALID, "in_dim must be a positive multiple of 32");
+  SG_TRY(set_device(ctx));
+  sg_q8_weight* w = new sg_q8_weight;
+  w->ctx = ctx;
+  w->N = out_dim;
+  w->K = in_dim;
+  DevBuf stage;
+  int r = SG_OK;
+  if (hipMalloc(&w->w, sizeof(_Float16) * (size_t)out_dim * in_dim) != hipSuccess ||
+      hipMalloc(&w->st, sizeof(float) * (size_t)out_dim * (in_dim / 32)) != hipSuccess)
+    r = fail(SG_ERR_NOMEM, "hipMalloc failed (weight)");
+  if (r == SG_OK) r = upload_q8(q8, out_dim, in_dim, stage, w->w, w->st, out_dim, 0, ctx->stream);
+  stage.release();
+  if (r != SG_OK) {
+    sg_q8_weight_free(w);
+    return r;
+  }
+  *out = w;
+  return SG_OK;
+}
+
+void sg_q8_weight_free(sg_q8_weight* w) {
+  if (!w) return;
+  if (w->w) (void)hipFree(w->w);
+  if (w->st) (void)hipFree(w->st);
+  delete w;
+}
+
+int sg_quantize_act(sg_ctx* ctx, const float* x, int32_t rows, int32_t cols, const int32_t* off, int32_t n_seq,
+                    int8_t* q_out, float* scale_out, void* stream) {
+  if (!ctx || !x || !q_out || !scale_out) return fail(SG_ERR_INVALID, "NULL argument");
+  if (cols <= 0 || cols % 4) return fail(SG_ERR_INVALID, "cols must be a positive multiple of 4");
+  SG_TRY(check_offsets(off, n_seq, rows));
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  SG_TRY(set_device(ctx));
+  hipStream_t s = pick(ctx, stream);
+  Meta meta;
+  SG_TRY(stage_meta(off, n_seq, ctx->meta_h, ctx->meta_d, s, meta));
+  SG_TRY(ctx->amax.ensure(sizeof(float) * ((size_t)n_seq + (size_t)rows)));
+  float* amax = ctx->amax.as<float>();
+  float* row_scale = amax + n_seq;
+  SG_HIP(sgk::fill_f32(amax, 0.0f, n_seq, s));
+  SG_HIP(sgk::absmax_rows(x, cols, rows, cols, meta.row_seq, amax, s));
+  SG_HIP(sgk::quantize(x, cols, rows, cols, meta.row_seq, amax, nullptr, q_out, row_scale, s));
+  SG_HIP(sgk::seq_scales(amax, n_seq, scale_out, s));
+  SG_HIP(hipStreamSynchronize(s));
+  return SG_OK;
+}
+
+static int matmul_common(sg_ctx* ctx, float* dst, int32_t* sums, const sg_q8_weight* w, const int8_t* x,
+                         const float* row_scale, int32_t batch, void* stream) {
+  if (!ctx || !w || !x || (!dst && !sums)) return fail(SG_ERR_INVALID, "NULL argument");
+  if (batch < 0) return fail(SG_ERR_INVALID, "batch < 0");
+  if (batch == 0) return SG_OK;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  SG_TRY(set_device(ctx));
+  hipStream_t s = pick(ctx, stream);
+  const int64_t n = (int64_t)batch * w->K;
+  SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)n));
+  SG_HIP(sgk::i8_to_f16(x, ctx->f16.as<_Float16>(), n, s));
+  if (sums) {
+    SG_TRY(ctx->amax.ensure(sizeof(float) * (size_t)batch));
+    float* ones = ctx->amax.as<float>();
+    SG_HIP(sgk::fill_f32(ones, 1.0f, batch, s));
+    float* scratch_y = nullptr;
+    DevBuf y;
+    SG_TRY(y.ensure(sizeof(float) * (size_t)batch * w->N));
+    scratch_y = y.as<float>();
+    hipError_t e = sgk::gemm_q8(ctx->f16.as<_Float16>(), w->w, w->st, ones, scratch_y, sums, batch, w->N, w->K, s);
+    hipError_t e2 = hipStreamSynchronize(s);
+    y.release();
+    SG_HIP(e);
+    SG_HIP(e2);
+    return SG_OK;
+  }
+  if (!row_scale) return fail(SG_ERR_INVALID, "row_scale is NULL");
+  SG_HIP(sgk::gemm_q8(ctx->f16.as<_Float16>(), w->w, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s));
+  SG_HIP(hipStreamSynchronize(s));
+  return SG_OK;
+}
+
+int sg_matmul_q8_0_int8(sg_ctx* ctx, float* dst, const sg_q8_weight* w, const int8_t* x, const float* row_scale,
+                        int32_t batch, void* stream) {
+  return matmul_common(ctx, dst, nullptr, w, x, row_scale, batch, stream);
+}
+
+int sg_q8_block_sums(sg_ctx* ctx, int32_t* out, const sg_q8_weight* w, const int8_t* x, int32_t batch, void* stream) {
+  return matmul_common(ctx, nullptr, out, w, x, nullptr, batch, stream);
+}
+
+int sg_rmsnorm(sg_ctx* ctx, float* dst, const float* src, const float* weight, int32_t rows, int32_t n, float eps,
+               void* stream) {
+  if (!ctx || !dst || !src || !weight) return fail(SG_ERR_INVALID, "NULL argument");
+  if (rows < 0) return fail(SG_ERR_INVALID, "rows < 0");
+  SG_TRY(set_device(ctx));
+  hipError_t e = sgk::rmsnorm(dst, src, weight, rows, n, eps, nullptr, nullptr, pick(ctx, stream));
+  if (e == hipErrorInvalidValue) return fail(SG_ERR_INVALID, "row length %d unsupported (256/512/768/1024/1152)", n);
+  SG_HIP(e);
+  return SG_OK;
+}
+
+int sg_qknorm_rope(sg_ctx* ctx, float* q, int32_t ldq, float* k, int32_t ldk, const float* q_norm, const float* k_norm,
+                   int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, float eps, float rope_base,
+                   int32_t max_seq_len, const int32_t* off, int32_t n_seq, void* stream) {
+  if (!ctx || !q || !k) return fail(SG_ERR_INVALID, "NULL argument");
+  if (head_dim != 256) return fail(SG_ERR_INVALID, "head_dim must be 256");
+  SG_TRY(check_offsets(off, n_seq, -1));
+  for (int i = 0; i < n_seq; i++)
+    if (off[i + 1] - off[i] > max_seq_len) return fail(SG_ERR_TOO_LONG, "sequence longer than max_seq_len");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  SG_TRY(set_device(ctx));
+  hipStream_t s = pick(ctx, stream);
+  Meta meta;
+  SG_TRY(stage_meta(off, n_seq, ctx->meta_h, ctx->meta_d, s, meta));
+  std::vector<float> ct, st;
+  rope_tables(head_dim, rope_base, max_seq_len, ct, st);
+  SG_TRY(ctx->tab.ensure(sizeof(float) * (ct.size() + st.size())));
+  float* tc = ctx->tab.as<float>();
+  SG_HIP(hipMemcpy(tc, ct.data(), sizeof(float) * ct.size(), hipMemcpyHostToDevice));
+  SG_HIP(hipMemcpy(tc + ct.size(), st.data(), sizeof(float) * st.size(), hipMemcpyHostToDevice));
+  SG_HIP(sgk::qknorm_rope(q, ldq, k, ldk, q_norm, k_norm, n_heads, n_kv_heads, meta.T, meta.row_pos, tc,
+                          tc + ct.size(), eps, s));
+  SG_HIP(hipStreamSynchronize(s));
+  return SG_OK;
+}
+
+int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const float* k, const float* v, int32_t ldkv,
+                 int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, const int32_t* off, int32_t n_seq,
+                 void* stream) {
+  if (!ctx || !out || !q || !k || !v) return fail(SG_ERR_INVALID, "NULL argument");
+  if (head_dim != 256 || n_kv_heads <= 0 || n_heads % n_kv_heads || n_heads / n_kv_heads > 4)
+    return fail(SG_ERR_INVALID, "unsupported attention shape");
+  SG_TRY(check_offsets(off, n_seq, -1));
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  SG_TRY(set_device(ctx));
+  hipStream_t s = pick(ctx, stream);
+  Meta meta;
+  SG_TRY(stage_meta(off, n_seq, ctx->meta_h, ctx->meta_d, s, meta));
+  const float scale = 1.0f / (float)std::sqrt((double)head_dim);
+  SG_HIP(sgk::attention(q, ldq, k, v, ldkv, out, n_heads * head_dim, meta.seq_off, meta.items, meta.n_items, n_heads,
+                        n_kv_heads, head_dim, scale, nullptr, s));
+  SG_HIP(hipStreamSynchronize(s));
+  return SG_OK;
+}
+
+int sg_gelu_quick_mul(sg_ctx* ctx, float* dst, int32_t ldd, const float* gate, int32_t ldg, const float* up,
+                      int32_t ldu, int32_t rows, int32_t cols, void* stream) {
+  if (!ctx || !dst || !gate || !up) return fail(SG_ERR_INVALID, "NULL argument");
+  SG_TRY(set_device(ctx));
+  hipError_t e = sgk::gelu_mul(dst, ldd, gate, ldg, up, ldu, rows, cols, nullptr, nullptr, pick(ctx, stream));
+  if (e == hipErrorInvalidValue) return fail(SG_ERR_INVALID, "cols and strides must be multiples of 4");
+  SG_HIP(e);
+  return SG_OK;
+}
+
+int sg_embed_tokens(sg_model* m, float* dst, const int32_t* d_tokens, int32_t n_tokens, void* stream) {
+  if (!m || !dst || !d_tokens) return fail(SG_ERR_INVALID, "NULL argument");
+  std::lock_guard<std::mutex> lk(m->mu);
+  SG_TRY(set_device(m->ctx));
+  hipStream_t s = pick(m->ctx, stream);
+  SG_TRY(m->err.ensure(64));
+  SG_TRY(m->io_h.ensure(64));
+  SG_HIP(sgk::fill_f32(m->err.as<float>(), 0.0f, 1, s));
+  SG_HIP(sgk::embed_only(d_tokens, n_tokens, m->emb_q, m->emb_s, m->cfg.vocab_size, m->cfg.embed_dim, m->sqrt_d, dst,
+                         m->err.as<int32_t>(), s));
+  SG_HIP(hipMemcpyAsync(m->io_h.p, m->err.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  SG_HIP(hipStreamSynchronize(s));
+  if (*m->io_h.as<int32_t>() != 0) return fail(SG_ERR_TOKEN, "token ID out of range");
+  return SG_OK;
+}
+
+int sg_pool_l2(sg_ctx* ctx, float* out, const float* x, int32_t ldx, int32_t out_dim, const int32_t* off, int32_t n_seq,
+               void* stream) {
+  if (!ctx || !out || !x) return fail(SG_ERR_INVALID, "NULL argument");
+  if (out_dim <= 0 || out_dim > 1024 || out_dim > ldx) return fail(SG_ERR_DIM, "out_dim %d out of range", out_dim);
+  SG_TRY(check_offsets(off, n_seq, -1));
+  for (int i = 0; i < n_seq; i++)
+    if (off[i + 1] == off[i]) return fail(SG_ERR_EMPTY, "empty input");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  SG_TRY(set_device(ctx));
+  hipStream_t s = pick(ctx, stream);
+  Meta meta;
+  SG_TRY(stage_meta(off, n_seq, ctx->meta_h, ctx->meta_d, s, meta));
+  SG_HIP(sgk::pool_l2(out, x, ldx, out_dim, meta.seq_off, n_seq, s));
+  SG_HIP(hipStreamSynchronize(s));
+  return SG_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,129 @@
+// sg_device.h -- device-side building blocks shared by the gfx950 kernels.
+//
+// Every function here restates one piece of reference arithmetic with the
+// same rounding steps (the library is built with -ffp-contract=off, so a*b+c
+// is two roundings unless fmaf() is written out, exactly as Go on amd64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+#define SG_WAVE 64
+
+// fastExp, internal/kernels/activation.go:100-145: clamp at +-10, 2^(x*log2e)
+// split into integer part (truncation) and a 4th-order polynomial on the
+// fraction, exponent bits built directly.  All float32, no fused ops.
+__device__ __forceinline__ float sg_fast_exp(float x) {
+  if (x < -10.0f) return 0.0f;
+  if (x > 10.0f) return 22026.4657948f;
+  const float y = x * 1.442695041f;
+  const int ip = (int)y;  // v_cvt_i32_f32 truncates toward zero, like Go's int32()
+  const float f = y - (float)ip;
+  const float poly =
+      1.0f + f * (0.693147180559945f + f * (0.240226506959101f + f * (0.055504108664821f + f * 0.009676036358193f)));
+  if (ip >= -126 && ip <= 127) return poly * __uint_as_float((uint32_t)(ip + 127) << 23);
+  if (ip < -126) return 0.0f;
+  return 3.402823e+38f;
+}
+
+// GELUQuickSIMD element, activation.go:55-75: x * sigmoid(1.702 x) with the
+// sign-split sigmoid.
+__device__ __forceinline__ float sg_gelu_quick(float x) {
+  const float sx = 1.702f * x;
+  float sig;
+  if (sx >= 0.0f) {
+    const float e = sg_fast_exp(-sx);
+    sig = 1.0f / (1.0f + e);
+  } else {
+    const float e = sg_fast_exp(sx);
+    sig = e / (1.0f + e);
+  }
+  return x * sig;
+}
+
+// fp16 -> fp32 with subnormal support, internal/runtime/model_int8.go:571-597.
+__device__ __host__ __forceinline__ float sg_f16_ieee(uint16_t h) {
+  uint32_t sign = (h >> 15) & 1u;
+  int32_t ex = (h >> 10) & 0x1f;
+  uint32_t fr = h & 0x3ffu;
+  if (ex == 0) {
+    if (fr == 0) return __uint_as_float(sign << 31);
+    while ((fr & 0x400u) == 0) { fr <<= 1; ex--; }
+    ex++;
+    fr &= 0x3ffu;
+  } else if (ex == 0x1f) {
+    return __uint_as_float((sign << 31) | 0x7f800000u | (fr << 13));
+  }
+  return __uint_as_float((sign << 31) | ((uint32_t)(ex + 112) << 23) | (fr << 13));
+}
+
+// fp16 -> fp32 as internal/gguf/tensor.go:207-240 computes it: the subnormal
+// branch normalizes from exponent 112 without the +1, so subnormals halve.
+// The token-embedding lookup (DequantizeQ8_0Row) goes through this one.
+__device__ __host__ __forceinline__ float sg_f16_gguf(uint16_t h) {
+  uint32_t sign = (h >> 15) & 1u, ex = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (ex == 0) {
+    if (m == 0) return __uint_as_float(sign << 31);
+    uint32_t e = 112u;
+    while ((m & 0x400u) == 0) { m <<= 1; e--; }
+    return __uint_as_float((sign << 31) | (e << 23) | ((m & 0x3ffu) << 13));
+  }
+  if (ex == 0x1f) return __uint_as_float((sign << 31) | (0xffu << 23) | (m << 13));
+  return __uint_as_float((sign << 31) | (((ex + 112u) & 0xffu) << 23) | (m << 13));
+}
+
+// Horizontal sum across the 8 lanes of an aligned lane group, in the order of
+// the AVX2 reduction VEXTRACTF128/VADDPS/VHADDPS/VHADDPS
+// (internal/kernels/simd_amd64.s:50-54): ((a0+a4)+(a1+a5))+((a2+a6)+(a3+a7)).
+// fp32 addition is commutative bit for bit, so every lane of the group ends
+// with the identical value.
+__device__ __forceinline__ float sg_hsum8(float a) {
+  float s = a + __shfl_xor(a, 4);
+  s = s + __shfl_xor(s, 1);
+  return s + __shfl_xor(s, 2);
+}
+
+__device__ __forceinline__ float sg_max8(float a) {
+  a = fmaxf(a, __shfl_xor(a, 4));
+  a = fmaxf(a, __shfl_xor(a, 2));
+  return fmaxf(a, __shfl_xor(a, 1));
+}
+
+__device__ __forceinline__ float sg_wave_max(float a) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+  return a;
+}
+
+// RMSNorm of one row held by an 8-lane group, internal/kernels/norm.go:8-36.
+// Lane j of the group holds x[i] = row[8*i + j] (NPL = n/8 values): that is
+// exactly lane j of dotProductAVX2Asm's YMM accumulator, which runs
+// acc_j = fma(row[8i+j], row[8i+j], acc_j) in i order (simd_amd64.s:36-46).
+// Then meanSq = ss/float32(n); rms = float32(sqrt(float64(meanSq+eps)))
+// (a correctly rounded float sqrt gives the same bits); inv = 1/rms;
+// y = (x*inv)*w with two roundings (VecScaleF32 then VecMulF32).
+template <int NPL>
+__device__ __forceinline__ void sg_rmsnorm8(float (&x)[NPL], const float* __restrict__ w, int j, float eps) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NPL; i++) acc = __builtin_fmaf(x[i], x[i], acc);
+  const float ss = sg_hsum8(acc);
+  const float ms = ss / (float)(NPL * 8);
+  const float rms = __fsqrt_rn(ms + eps);
+  const float inv = 1.0f / rms;
+#pragma unroll
+  for (int i = 0; i < NPL; i++) {
+    const float t = x[i] * inv;
+    x[i] = t * w[8 * i + j];
+  }
+}
+
+// Monotone float max for non-negative values via the uint bit pattern.
+__device__ __forceinline__ void sg_atomic_max_nonneg(float* addr, float v) {
+  atomicMax(reinterpret_cast<unsigned int*>(addr), __float_as_uint(v));
+}

@@ -1,0 +1,63 @@
+// sg_kernels.h -- host-side launchers for the gfx950 kernels (internal to the
+// library; the public surface is include/semantica_gpu.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+struct sg_item { int32_t seq, q0; };  // one attention work item: 32 query rows of a sequence
+
+namespace sgk {
+
+// ---- load-time repack (k_rows.hip) ----
+// Raw Q8_0 rows [rows][cols/32][34 B] -> fp16 integer weights w16[(row_off+r)*cols + k]
+// and fp32 block scales (IEEE converter) transposed st[b*ld_st + row_off + r].
+hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, float* st, int ld_st,
+                       int row_off, hipStream_t s);
+// token_embd: int8 values q[v][d] and per-block scales (gguf halving converter) sc[v][d/32].
+hipError_t repack_embd(const uint8_t* raw, int vocab, int d, int8_t* q, float* sc, hipStream_t s);
+hipError_t i8_to_f16(const int8_t* x, _Float16* y, int64_t n, hipStream_t s);
+hipError_t fill_f32(float* p, float v, int64_t n, hipStream_t s);
+
+// ---- per-row kernels (k_rows.hip) ----
+// Embedding gather * sqrt(d) -> h; then RMSNorm(w) -> xn and per-sequence max|xn| -> amax.
+hipError_t embed_norm(const int32_t* tokens, int T, const int8_t* eq, const float* es, int vocab, int d,
+                      float sqrt_d, const float* w, float eps, const int32_t* row_seq, float* h, float* xn,
+                      float* amax, int32_t* err, hipStream_t s);
+// Per-sequence symmetric quantization of x[rows][cols] (stride ldx) using amax[row_seq[r]].
+// Writes fp16-encoded integers (f16 != null) or int8 (i8 != null) [rows][cols] and row_scale[rows].
+hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
+                    _Float16* f16, int8_t* i8, float* row_scale, hipStream_t s);
+hipError_t absmax_rows(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, float* amax,
+                       hipStream_t s);
+hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s);
+// RMSNorm rows in the reference's order; amax (optional) collects per-sequence max|y|.
+hipError_t rmsnorm(float* dst, const float* src, const float* w, int rows, int n, float eps,
+                   const int32_t* row_seq, float* amax, hipStream_t s);
+// QK-norm + RoPE, in place; head_dim 256.
+hipError_t qknorm_rope(float* q, int ldq, float* k, int ldk, const float* qw, const float* kw, int H, int HKV,
+                       int T, const int32_t* row_pos, const float* cos_t, const float* sin_t, float eps,
+                       hipStream_t s);
+// h = RMSNorm(o; w_post) + h ; xn = RMSNorm(h; w_next) ; amax (optional) per sequence of max|xn|.
+hipError_t post_res_norm(const float* o, float* h, const float* w_post, const float* w_next, float eps, int T,
+                         int d, float* xn, const int32_t* row_seq, float* amax, hipStream_t s);
+// g = geluquick(gate)*up over rows x cols; amax (optional) per sequence of max|g|.
+hipError_t gelu_mul(float* g, int ldd, const float* gate, int ldg, const float* up, int ldu, int rows, int cols,
+                    const int32_t* row_seq, float* amax, hipStream_t s);
+hipError_t pool_l2(float* out, const float* x, int ldx, int out_dim, const int32_t* seq_off, int n_seq,
+                   hipStream_t s);
+hipError_t embed_only(const int32_t* tokens, int T, const int8_t* eq, const float* es, int vocab, int d,
+                      float sqrt_d, float* h, int32_t* err, hipStream_t s);
+
+// ---- GEMM (k_gemm.hip) ----
+// Y[M][N] = (sum_b float(P_b) * St[b][n]) * row_scale[m]; A fp16 [M][K], W fp16 [N][K].
+// sums != null additionally dumps the exact block sums int32 [M][N][K/32].
+hipError_t gemm_q8(const _Float16* A, const _Float16* W, const float* St, const float* row_scale, float* Y,
+                   int32_t* sums, int M, int N, int K, hipStream_t s);
+
+// ---- attention (k_attention.hip) ----
+hipError_t attention(const float* q, int ldq, const float* k, const float* v, int ldkv, float* out, int ldo,
+                     const int32_t* seq_off, const sg_item* items, int n_items, int H, int HKV, int hd,
+                     float scale, float* amax, hipStream_t s);
+
+}  // namespace sgk

@@ -1,0 +1,208 @@
+/*
+ * semantica_gpu.h -- C ABI of the MI355X (gfx950) EmbeddingGemma-300M Q8_0
+ * forward library (libsemantica_gpu.so).
+ *
+ * Plain C types only: host or device pointers, sizes, int status codes.  No
+ * exception or abort crosses this boundary; failures return a negative SG_ERR_*
+ * code and sg_last_error() (thread-local) describes the most recent one.
+ *
+ * Each entry point replaces one seam of the reference Go implementation
+ * (headlands-org/go-semantica); the citation is given beside it.  Paths are
+ * relative to that source tree.
+ */
+#ifndef SEMANTICA_GPU_H
+#define SEMANTICA_GPU_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SG_ABI_VERSION 1
+
+/* Status codes.  The first four are the error cases of forwardINT8WithDim
+ * (internal/runtime/model_int8.go:150-171) and ForwardWithDim
+ * (internal/runtime/model.go:661-667). */
+#define SG_OK 0
+#define SG_ERR_EMPTY (-1)     /* "empty input": a sequence with no tokens        */
+#define SG_ERR_TOO_LONG (-2)  /* "sequence too long: %d > %d"                    */
+#define SG_ERR_TOKEN (-3)     /* "token ID out of range: %d"                     */
+#define SG_ERR_DIM (-4)       /* "target dimension %d out of range (1..%d)"      */
+#define SG_ERR_INVALID (-5)   /* bad argument / unsupported shape (kernel seams panic here) */
+#define SG_ERR_DEVICE (-6)    /* HIP runtime failure                              */
+#define SG_ERR_NOMEM (-7)     /* device or host allocation failed                 */
+
+typedef struct sg_ctx sg_ctx;             /* one GPU: device ordinal + stream + scratch */
+typedef struct sg_model sg_model;         /* weights resident in HBM + forward workspace */
+typedef struct sg_q8_weight sg_q8_weight; /* one repacked Q8_0 matrix                    */
+
+/* ModelConfig, internal/runtime/model.go:16-31 (fields parseConfig fills,
+ * :424-517).  head_dim = embed_dim / num_heads and the attention scale
+ * 1/sqrt(head_dim) are derived exactly as parseConfig derives them. */
+typedef struct sg_model_config {
+  int32_t embed_dim;    /* gemma-embedding.embedding_length  (768)  */
+  int32_t num_layers;   /* block_count                        (24)   */
+  int32_t num_heads;    /* attention.head_count               (3)    */
+  int32_t num_kv_heads; /* attention.head_count_kv            (1)    */
+  int32_t interm_dim;   /* feed_forward_length                (1152) */
+  int32_t max_seq_len;  /* context_length                     (2048) */
+  int32_t vocab_size;   /* len(tokenizer.ggml.tokens)         (262144) */
+  float norm_eps;       /* attention.layer_norm_rms_epsilon   (1e-6) */
+  float rope_base;      /* rope.freq_base                     (10000) */
+} sg_model_config;
+
+/* Host pointers to one layer's GGUF tensors, exactly as stored in the file
+ * (loadLayerINT8, internal/runtime/model_int8.go:54-119): Q8_0 matrices are
+ * raw 34-byte blocks, row-major [out][in/32]; norms are F32 vectors. */
+typedef struct sg_layer_desc {
+  const void *attn_q, *attn_k, *attn_v, *attn_output; /* blk.N.attn_{q,k,v,output}.weight */
+  const void *ffn_gate, *ffn_up, *ffn_down;           /* blk.N.ffn_{gate,up,down}.weight  */
+  const float *attn_norm, *attn_q_norm, *attn_k_norm; /* blk.N.attn_norm / attn_{q,k}_norm */
+  const float *post_attention_norm, *ffn_norm, *post_ffw_norm;
+} sg_layer_desc;
+
+typedef struct sg_model_desc {
+  sg_model_config config;
+  const void *token_embd;     /* token_embd.weight, Q8_0 [vocab][embed_dim/32][34 B] */
+  const float *output_norm;   /* output_norm.weight [embed_dim] */
+  const sg_layer_desc *layers;/* num_layers entries */
+} sg_model_desc;
+
+/* ---- context ----------------------------------------------------------- */
+
+/* Opens device `device_ordinal`, creates a default-priority stream.
+ * (The reference has no device; this is the handle the Go cgo shim keeps.) */
+int sg_init(int device_ordinal, sg_ctx **out);
+void sg_shutdown(sg_ctx *ctx);
+const char *sg_last_error(void);
+int sg_abi_version(void);
+
+/* ---- model seam --------------------------------------------------------- */
+
+/* Replaces LoadModel/loadModel's weight setup (internal/runtime/model.go:233-315,
+ * :520-552; model_int8.go:54-140): copies every tensor to HBM once, repacks
+ * the Q8_0 matrices for the MFMA GEMM and extracts the fp32 block scales with
+ * the IEEE converter (model_int8.go:543-597); the token embedding keeps the
+ * halving converter of DequantizeQ8_0Row (gguf/tensor.go:157-240).  Host
+ * buffers may be freed after return (unlike the Go zero-copy views). */
+int sg_model_load(sg_ctx *ctx, const sg_model_desc *desc, sg_model **out);
+void sg_model_free(sg_model *model);
+
+/* Batched ForwardWithDim (internal/runtime/model.go:661-667 ->
+ * forwardINT8WithDim model_int8.go:148-256) over n_seq packed sequences:
+ * tokens[seq_offsets[i] .. seq_offsets[i+1]) is sequence i (CSR offsets,
+ * seq_offsets[0] == 0).  out[n_seq][out_dim] receives each sequence's
+ * mean-pooled, L2-normalized embedding truncated to out_dim (1..embed_dim).
+ * Every sequence is computed exactly as the reference computes it alone
+ * (per-sequence activation scales, attention and pooling).  Host buffers;
+ * synchronous.  A model serves one call at a time (calls are serialized by a
+ * per-model mutex), as the reference serves concurrent callers. */
+int sg_forward(sg_model *model, const int32_t *tokens, const int32_t *seq_offsets,
+               int32_t n_seq, int32_t out_dim, float *out);
+
+/* Same, with tokens and out in device memory (tokens already resident in
+ * HBM); seq_offsets stays on the host.  `stream` (hipStream_t, may be NULL
+ * for the context stream) orders the work; the call returns after the
+ * result is complete and token IDs have been validated on the device. */
+int sg_forward_device(sg_model *model, const int32_t *d_tokens, const int32_t *seq_offsets,
+                      int32_t n_seq, int32_t out_dim, float *d_out, void *stream);
+
+/* ---- measurement hook ---------------------------------------------------
+ * No counterpart in the reference (its benchmark only times whole Embed
+ * calls, cmd/benchmark/main.go:553-715).  While enabled, sg_forward*
+ * brackets every kernel launch with HIP events on the launch stream and
+ * accumulates, per kernel class, the event-measured time, the launch count
+ * and the algorithmic work of those launches (int8 ops for the GEMM, flops
+ * for attention's two products, bytes read+written at the reference dtypes
+ * for the bandwidth kernels).  sg_profile_read synchronizes and returns the
+ * totals since the last enable. */
+enum {
+  SG_K_GEMM = 0,      /* Q8_0 GEMMs (QKV, O, gate/up, down)          */
+  SG_K_ATTENTION = 1, /* fused MQA attention                          */
+  SG_K_QUANTIZE = 2,  /* per-sequence int8 quantization               */
+  SG_K_NORM = 3,      /* embed+norm, post-norm+residual+norm, QK-norm+RoPE */
+  SG_K_GELU = 4,      /* GELUQuick * up                               */
+  SG_K_POOL = 5,      /* mean-pool + L2                               */
+  SG_K_OTHER = 6,     /* fills                                        */
+  SG_K_CLASSES = 7
+};
+typedef struct sg_profile {
+  double ms[SG_K_CLASSES];        /* summed event time of the class's launches */
+  double work[SG_K_CLASSES];      /* ops (GEMM), flops (attention) or bytes    */
+  int64_t launches[SG_K_CLASSES];
+} sg_profile;
+int sg_profile_enable(sg_model *model, int on);
+int sg_profile_read(sg_model *model, sg_profile *out);
+
+/* ---- kernel seam (device pointers, asynchronous on `stream`) ------------ */
+
+/* Repacks one raw Q8_0 matrix [out_dim][in_dim/32][34 B] (host pointer) into
+ * the device layout used by the GEMM.  in_dim must be a multiple of 32.
+ * (extractQ8_0Scales model_int8.go:543-569 + the weight bytes it views.) */
+int sg_q8_weight_create(sg_ctx *ctx, const void *q8, int32_t out_dim, int32_t in_dim,
+                        sg_q8_weight **out);
+void sg_q8_weight_free(sg_q8_weight *w);
+
+/* QuantizeSymmetricINT8Into (internal/kernels/quantize.go:29-103) applied to
+ * each sequence of a packed tensor: x[rows][cols] fp32, rows grouped by the
+ * host CSR seq_offsets[n_seq+1].  One scale per sequence (max|x|/127; all-zero
+ * input gives scale 1 and zeros).  q_out int8 [rows][cols], scale_out[n_seq]. */
+int sg_quantize_act(sg_ctx *ctx, const float *x, int32_t rows, int32_t cols,
+                    const int32_t *seq_offsets, int32_t n_seq,
+                    int8_t *q_out, float *scale_out, void *stream);
+
+/* MatMulQ8_0INT8 (internal/kernels/quantize.go:346-458):
+ * dst[b][n] = (sum_blocks float(P_block) * d[n][block]) * row_scale[b] with
+ * P_block the exact int32 dot of a 32-wide block, accumulated block by block
+ * with a fused multiply-add.  x int8 [batch][in_dim]; row_scale[batch]
+ * (the reference's single input.Scale, repeated per row of a sequence). */
+int sg_matmul_q8_0_int8(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const int8_t *x,
+                        const float *row_scale, int32_t batch, void *stream);
+
+/* The exact int32 block dot products of the same GEMM, out[batch][out_dim][in_dim/32]
+ * (what matmulInnerLoop* converts with VCVTDQ2PS, simd_amd64.s:290). */
+int sg_q8_block_sums(sg_ctx *ctx, int32_t *out, const sg_q8_weight *w, const int8_t *x,
+                     int32_t batch, void *stream);
+
+/* RMSNorm per row (internal/kernels/norm.go:8-36), AVX2 8-lane order.
+ * dst may equal src.  n must be a multiple of 8. */
+int sg_rmsnorm(sg_ctx *ctx, float *dst, const float *src, const float *weight,
+               int32_t rows, int32_t n, float eps, void *stream);
+
+/* Per-head RMSNorm with attn_q_norm / attn_k_norm then RoPE (model_int8.go:371-452;
+ * rope_cache.go:15-107) on q[rows][n_heads*head_dim] and k[rows][n_kv*head_dim]
+ * (row strides ldq, ldk floats), in place.  Positions restart at 0 for each
+ * sequence of the host CSR seq_offsets.  head_dim must be 256. */
+int sg_qknorm_rope(sg_ctx *ctx, float *q, int32_t ldq, float *k, int32_t ldk,
+                   const float *q_norm, const float *k_norm, int32_t n_heads, int32_t n_kv_heads,
+                   int32_t head_dim, float eps, float rope_base, int32_t max_seq_len,
+                   const int32_t *seq_offsets, int32_t n_seq, void *stream);
+
+/* MultiHeadAttentionChunked with mask=nil (internal/kernels/attention.go:88-363) per
+ * sequence: bidirectional MQA, scale 1/sqrt(head_dim), fastExp softmax.
+ * q[rows][ldq] (heads at h*head_dim), k,v[rows][ldkv]; out[rows][n_heads*head_dim].
+ * head_dim must be 256 and n_heads/n_kv_heads <= 4. */
+int sg_attention(sg_ctx *ctx, float *out, const float *q, int32_t ldq, const float *k,
+                 const float *v, int32_t ldkv, int32_t n_heads, int32_t n_kv_heads,
+                 int32_t head_dim, const int32_t *seq_offsets, int32_t n_seq, void *stream);
+
+/* GELUQuickSIMD then VecMulF32 (activation.go:47-145, matmul.go:238-259):
+ * dst[i] = geluquick(gate[i]) * up[i], for `rows` rows of `cols` (strides ldg, ldu, ldd). */
+int sg_gelu_quick_mul(sg_ctx *ctx, float *dst, int32_t ldd, const float *gate, int32_t ldg,
+                      const float *up, int32_t ldu, int32_t rows, int32_t cols, void *stream);
+
+/* Token embedding lookup + sqrt(embed_dim) scaling (model_int8.go:166-184, with
+ * DequantizeQ8_0Row's halving fp16 converter) for the model's token_embd. */
+int sg_embed_tokens(sg_model *model, float *dst, const int32_t *d_tokens, int32_t n_tokens,
+                    void *stream);
+
+/* MeanPoolingPartial + l2Normalize (attention.go:423-445, runtime/model.go:808-820)
+ * per sequence: x[rows][ldx], out[n_seq][out_dim]. */
+int sg_pool_l2(sg_ctx *ctx, float *out, const float *x, int32_t ldx, int32_t out_dim,
+               const int32_t *seq_offsets, int32_t n_seq, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SEMANTICA_GPU_H */
