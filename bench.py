@@ -35,7 +35,7 @@ def parse():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--seq-len", type=int, default=512)
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, host CPUs)")
-    ap.add_argument("--cpu-seqs", type=int, default=0, help="0: 2 x cpu threads")
+    ap.add_argument("--cpu-seqs", type=int, default=0, help="0: 6 x cpu threads")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -139,7 +139,7 @@ def main():
     ctx.close()
     if not a.no_cpu_baseline:
         threads = a.cpu_threads or min(16, os.cpu_count() or 1)
-        line["cpu_baseline"] = cpu_baseline(mdl, toks, S, threads, a.cpu_seqs or 2 * threads)
+        line["cpu_baseline"] = cpu_baseline(mdl, toks, S, threads, a.cpu_seqs or 6 * threads)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -379,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void k_pool_l2(float* __restrict__ out, c
       const float t = pooled[c] * pooled[c];
       ss = ss + t;
     }
-    nrm = ss == 0.0f ? 0.0f : __fsqrt_rn(ss);
+    nrm = ss == 0.0f ? 0.0f : sg_sqrt(ss);
   }
   __syncthreads();
   const float n = nrm;

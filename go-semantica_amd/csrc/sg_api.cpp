@@ -358,7 +358,9 @@ int validate_config(const sg_model_config& c) {
 // Work figures are the algorithmic ones: 2*M*N*K int8 ops per GEMM,
 // 4*H*hd*S^2 flops per sequence for attention, and bytes read + written at
 // the reference's dtypes (fp32 activations, int8 quantized) elsewhere.
-int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_dim, float* d_out, hipStream_t s) {
+// stop >= 0: return after `stop` layers with the residual stream copied to d_out.
+int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_dim, float* d_out, hipStream_t s,
+                int stop = -1) {
   const sg_model_config& c = m->cfg;
   const int T = meta.T, ns = meta.n_seq, d = c.embed_dim, ff = c.interm_dim, L = c.num_layers;
   const int qd = m->qd, kvd = m->kvd, nqkv = m->nqkv;
@@ -387,6 +389,7 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
             sgk::embed_norm(d_tokens, T, m->emb_q, m->emb_s, c.vocab_size, d, m->sqrt_d, m->layers[0].attn_norm,
                             eps, meta.row_seq, h, xn, site(0, 0), m->err.as<int32_t>(), s));
   for (int l = 0; l < L; l++) {
+    if (l == stop) break;
     const LayerDev& ly = m->layers[l];
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 0), a16, nullptr, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), sgk::gemm_q8(a16, ly.wqkv, ly.sqkv, sx, qkv, nullptr, T, nqkv, d, s));
@@ -410,6 +413,10 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
     SG_LAUNCH(SG_K_NORM, t * d * 16.0,
               sgk::post_res_norm(o, h, ly.post_ffw, last ? m->out_norm : m->layers[l + 1].attn_norm, eps, T, d, xn,
                                  meta.row_seq, last ? nullptr : site(l + 1, 0), s));
+  }
+  if (stop >= 0) {
+    SG_HIP(hipMemcpyAsync(d_out, h, sizeof(float) * (size_t)T * d, hipMemcpyDeviceToDevice, s));
+    return SG_OK;
   }
   SG_LAUNCH(SG_K_POOL, 4.0 * out_dim * (t + ns), sgk::pool_l2(d_out, xn, d, out_dim, meta.seq_off, ns, s));
   return SG_OK;
@@ -452,14 +459,14 @@ int ensure_workspace(sg_model* m, int T, int n_seq) {
 }
 
 int forward_device_locked(sg_model* m, const int32_t* d_tokens, const int32_t* off, int n_seq, int out_dim,
-                          float* d_out, hipStream_t s) {
+                          float* d_out, hipStream_t s, int stop = -1) {
   SG_TRY(check_forward_args(m, off, n_seq, out_dim));
   SG_TRY(set_device(m->ctx));
   const int T = off[n_seq];
   SG_TRY(ensure_workspace(m, T, n_seq));
   Meta meta;
   SG_TRY(stage_meta(off, n_seq, m->meta_h, m->meta_d, s, meta));
-  SG_TRY(run_forward(m, d_tokens, meta, out_dim, d_out, s));
+  SG_TRY(run_forward(m, d_tokens, meta, out_dim, d_out, s, stop));
   SG_TRY(m->io_h.ensure(64));
   SG_HIP(hipMemcpyAsync(m->io_h.p, m->err.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
   SG_HIP(hipStreamSynchronize(s));
@@ -597,10 +604,22 @@ int sg_forward_device(sg_model* m, const int32_t* d_tokens, const int32_t* seq_o
   return forward_device_locked(m, d_tokens, seq_offsets, n_seq, out_dim, d_out, pick(m->ctx, stream));
 }
 
+int sg_forward_hidden(sg_model* m, const int32_t* d_tokens, const int32_t* seq_offsets, int32_t n_seq,
+                      int32_t n_layers, float* d_hidden, void* stream) {
+  if (!m || !d_tokens || !d_hidden) return fail(SG_ERR_INVALID, "NULL argument");
+  if (n_layers < 0 || n_layers > m->cfg.num_layers)
+    return fail(SG_ERR_INVALID, "n_layers %d out of range (0..%d)", n_layers, m->cfg.num_layers);
+  std::lock_guard<std::mutex> lk(m->mu);
+  return forward_device_locked(m, d_tokens, seq_offsets, n_seq, m->cfg.embed_dim, d_hidden, pick(m->ctx, stream),
+                               n_layers);
+}
+
 int sg_forward(sg_model* m, const int32_t* tokens, const int32_t* off, int32_t n_seq, int32_t out_dim, float* out) {
   if (!m || !tokens || !out) return fail(SG_ERR_INVALID, "NULL argument");
   std::lock_guard<std::mutex> lk(m->mu);
-  SG_TRY(check_forward_args(m, off, n_seq, out_dim));
+  if (out_dim <= 0 || out_dim > m->cfg.embed_dim)
+    return fail(SG_ERR_DIM, "target dimension %d out of range (1..%d)", out_dim, m->cfg.embed_dim);
+  SG_TRY(check_offsets(off, n_seq, -1));
   const int T = off[n_seq];
   // Sequences are checked in order, each fully (length, then tokens), so the
   // error returned is the one the reference's request-ordered fan-out reports

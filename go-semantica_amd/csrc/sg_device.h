@@ -77,6 +77,14 @@ __device__ __host__ __forceinline__ float sg_f16_gguf(uint16_t h) {
   return __uint_as_float((sign << 31) | (((ex + 112u) & 0xffu) << 23) | (m << 13));
 }
 
+// Correctly rounded float sqrt (equal to float32(math.Sqrt(float64(x))): the
+// double result rounded to float cannot differ from the correctly rounded
+// float one).  sqrtf lowers to llvm.sqrt.f32, which this library's build
+// flag -fhip-fp32-correctly-rounded-divide-sqrt keeps exact; HIP's __fsqrt_rn
+// maps to the approximate native sqrt unless OCML_BASIC_ROUNDED_OPERATIONS is
+// defined, so it is not used.
+__device__ __forceinline__ float sg_sqrt(float x) { return sqrtf(x); }
+
 // Horizontal sum across the 8 lanes of an aligned lane group, in the order of
 // the AVX2 reduction VEXTRACTF128/VADDPS/VHADDPS/VHADDPS
 // (internal/kernels/simd_amd64.s:50-54): ((a0+a4)+(a1+a5))+((a2+a6)+(a3+a7)).
@@ -114,7 +122,7 @@ __device__ __forceinline__ void sg_rmsnorm8(float (&x)[NPL], const float* __rest
   for (int i = 0; i < NPL; i++) acc = __builtin_fmaf(x[i], x[i], acc);
   const float ss = sg_hsum8(acc);
   const float ms = ss / (float)(NPL * 8);
-  const float rms = __fsqrt_rn(ms + eps);
+  const float rms = sg_sqrt(ms + eps);
   const float inv = 1.0f / rms;
 #pragma unroll
   for (int i = 0; i < NPL; i++) {

@@ -147,6 +147,14 @@ class Model:
                                               ctypes.c_void_p(stream) if stream else None))
 
 
+    def forward_hidden(self, d_tokens_ptr: int, offsets: np.ndarray, n_layers: int, d_hidden_ptr: int,
+                       stream: int = 0):
+        """sg_forward_hidden: residual stream after n_layers layers into a [T, embed_dim] device buffer."""
+        offsets = np.ascontiguousarray(offsets, np.int32)
+        _lib.check(self.lib.sg_forward_hidden(self.handle, ctypes.c_void_p(d_tokens_ptr), _ptr(offsets),
+                                              len(offsets) - 1, n_layers, ctypes.c_void_p(d_hidden_ptr),
+                                              ctypes.c_void_p(stream) if stream else None))
+
     def profile_enable(self, on: bool = True):
         _lib.check(self.lib.sg_profile_enable(self.handle, 1 if on else 0))
 

@@ -108,6 +108,14 @@ int sg_forward(sg_model *model, const int32_t *tokens, const int32_t *seq_offset
 int sg_forward_device(sg_model *model, const int32_t *d_tokens, const int32_t *seq_offsets,
                       int32_t n_seq, int32_t out_dim, float *d_out, void *stream);
 
+/* Layer tap for parity work (no counterpart in the reference API; it mirrors
+ * the CPU oracle's stop-layer tap): runs the embedding and the first
+ * n_layers layers (0..num_layers) of the batched forward and copies the
+ * residual stream h [T][embed_dim] (before the final norm) into d_hidden.
+ * Same argument checks and synchronization as sg_forward_device. */
+int sg_forward_hidden(sg_model *model, const int32_t *d_tokens, const int32_t *seq_offsets,
+                      int32_t n_seq, int32_t n_layers, float *d_hidden, void *stream);
+
 /* ---- measurement hook ---------------------------------------------------
  * No counterpart in the reference (its benchmark only times whole Embed
  * calls, cmd/benchmark/main.go:553-715).  While enabled, sg_forward*

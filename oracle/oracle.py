@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libsg_oracle.so")
 
 F16_RUNTIME, F16_GGUF, F16_KERNELS = 0, 1, 2
-ORDER_VNNI, ORDER_AVX2, ORDER_BLOCK_SERIAL = 0, 1, 2
+ORDER_VNNI, ORDER_AVX2, ORDER_BLOCK_SERIAL, ORDER_ARM64 = 0, 1, 2, 3
 
 _lib = None
 

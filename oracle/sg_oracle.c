@@ -141,14 +141,19 @@ static inline float hsum8(const float a[8]) {
 /* One output element over nb whole blocks: the scalar definition of the
  * three orders. xr: int8 activations of one row, wr: raw Q8_0 row. */
 static float q8_dot_scalar(const int8_t *xr, const uint8_t *wr, const float *sc, int nb, int order) {
-  if (order == SGO_ORDER_BLOCK_SERIAL) {
+  if (order == SGO_ORDER_BLOCK_SERIAL || order == SGO_ORDER_ARM64) {
     float acc = 0.0f;
     for (int b = 0; b < nb; b++) {
       const int8_t *w = (const int8_t *)(wr + (int64_t)b * 34 + 2);
       const int8_t *x = xr + (int64_t)b * 32;
       int32_t p = 0;
       for (int k = 0; k < 32; k++) p += (int32_t)x[k] * (int32_t)w[k];
-      acc = fmaf((float)p, sc[b], acc);
+      if (order == SGO_ORDER_BLOCK_SERIAL) {
+        acc = fmaf((float)p, sc[b], acc);
+      } else { /* SDOT + ADDP, SCVTF, FMULS, FADDS: simd_arm64_matmul.s:25-46 */
+        float t = (float)p * sc[b];
+        acc = acc + t;
+      }
     }
     return acc;
   }
@@ -207,7 +212,7 @@ void sgo_matmul_q8_0_int8(float *dst, const uint8_t *w, const float *scales,
                           int batch, int in_dim, int out_dim, int order) {
   int nb = in_dim / 32;
   int64_t row_bytes = (int64_t)nb * 34;
-  int simd = sgo_simd_level() && order != SGO_ORDER_BLOCK_SERIAL;
+  int simd = sgo_simd_level() && (order == SGO_ORDER_VNNI || order == SGO_ORDER_AVX2);
   const int JT = 64; /* column tile: keeps a weight tile hot while rows stream */
   for (int j0 = 0; j0 < out_dim; j0 += JT) {
     int j1 = j0 + JT < out_dim ? j0 + JT : out_dim;

@@ -39,7 +39,9 @@ void sgo_extract_q8_0_scales(const uint8_t *q8, int rows, int cols, float *scale
  *   BLOCK_SERIAL: acc = fma(float(P_b), d_b, acc) over whole-block sums, the order
  *                 the GPU kernel uses (also the arm64 / fallback structure,
  *                 matmul_inner_loop_fallback.go:25-36, with a fused multiply-add). */
-enum { SGO_ORDER_VNNI = 0, SGO_ORDER_AVX2 = 1, SGO_ORDER_BLOCK_SERIAL = 2 };
+enum { SGO_ORDER_VNNI = 0, SGO_ORDER_AVX2 = 1, SGO_ORDER_BLOCK_SERIAL = 2, SGO_ORDER_ARM64 = 3 };
+/*   ARM64: matmulInnerLoopAsm simd_arm64_matmul.s:6-56 -- whole-block SDOT sum,
+ *          SCVTF, then FMULS and FADDS (two roundings per block). */
 
 /* MatMulQ8_0INT8, internal/kernels/quantize.go:346-458.
  * dst[batch][out_dim]; w = raw Q8_0 rows [out_dim][in_dim/32][34 B];

@@ -156,9 +156,9 @@ def test_qknorm_rope_bit_exact(gpu_ctx, oracle):
         assert np.array_equal(gk[sl].view(np.uint32), rk.view(np.uint32)), i
 
 
-# fp16 matrix-core tolerance for attention: q, k, v and the weights are
-# rounded to fp16 (relative 2^-11) with fp32 accumulation.
-ATTN_REL_TOL = 2e-3
+# Attention runs its products as split fp16 (hi + lo, ~2^-22 relative) with
+# fp32 accumulation; the oracle is the reference's fp32 order.
+ATTN_REL_TOL = 1e-5
 
 
 def test_attention_vs_oracle(gpu_ctx, oracle):
@@ -180,7 +180,7 @@ def test_attention_vs_oracle(gpu_ctx, oracle):
         sl = slice(off[i], off[i + 1])
         ref = oracle.attention(q[sl], k[sl], v[sl], 3, 1, 256)
         assert rel_err(got[sl], ref) < ATTN_REL_TOL, (i, rel_err(got[sl], ref))
-        assert np.max(np.abs(got[sl] - ref)) < 1e-2 * np.max(np.abs(v[sl])), i
+        assert np.max(np.abs(got[sl] - ref)) < 1e-4 * np.max(np.abs(v[sl])), i
 
 
 def test_attention_clamped_keys_are_exact_zero(gpu_ctx, oracle):
