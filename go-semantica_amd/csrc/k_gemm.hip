@@ -8,24 +8,107 @@
 // Block sums on the fp16 matrix cores: both operands hold int8 values stored
 // as fp16 (exact), every product is an integer below 2^14 and every partial
 // sum of a 32-wide block is an integer below 2^19, so the fp32 accumulation
-// inside v_mfma_f32_32x32x16_f16 is exact in any order: two MFMAs (k 0..15,
-// 16..31) started from a zero accumulator produce float(P_b) with no rounding
-// at all.  That removes the int32->float conversion from the epilogue, which
-// leaves one v_fma_f32 per (m, n, block): with the int8 MFMA the epilogue
-// would need a convert and an FMA per element (2 VALU ops per 32 MACs) and
-// would cap the matrix cores at a quarter of their int8 rate.
+// inside v_mfma_f32_32x32x16_f16 is exact in any order: two MFMAs started
+// from a zero accumulator produce float(P_b) with no rounding at all.  That
+// removes the int32->float conversion from the epilogue, which leaves one
+// v_fma_f32 per (m, n, block); with the int8 MFMA the epilogue would need a
+// convert and an FMA per element (2 VALU ops per 32 MACs) and cap the matrix
+// cores at a quarter of their int8 rate.  Per 32x32 tile and block: 2 MFMAs
+// (64 cycles) against 16 FMAs (64 cycles) -- the two pipes are balanced.
 //
-// Layout: A [M][K] fp16 row-major (the quantized activations), W [N][K] fp16
-// row-major (repacked weight rows), St [K/32][N] fp32 block scales (transposed
-// so a wave's 32 columns read one contiguous 128-byte line per block).
+// Operand layout (written by the quantize kernel and the load-time repack):
+// block-major fp16 [K/32][rows][32], i.e. a K-block of a 32-row group is one
+// contiguous 2 KB piece.  Lane (r, h) of a wave reads the 32 bytes
+// k = 16h..16h+15 of row r: the first MFMA takes k 16h..16h+7, the second
+// 16h+8..16h+15.  A and W use the same assignment, so each block's dot
+// product is complete whatever k order the matrix core applies internally.
+// Block scales are St [K/32][N] fp32 (32 consecutive columns = 128 bytes).
 #include "sg_device.h"
 #include "sg_kernels.h"
 
 namespace {
 
+struct Frag {
+  half8_t lo, hi;
+};
+
+// XCD-aware tile order.  Workgroups are handed to the 8 XCDs round-robin by
+// linear id, and each XCD has its own L2.  All N-tiles of one M-tile read the
+// same A rows, so they are mapped to one XCD: linear id p runs on XCD p % 8;
+// that XCD's consecutive slots p / 8 walk its M-tiles (xcd, xcd+8, ...) with
+// every N-tile of each.  A is then fetched from HBM about once instead of
+// once per N-tile, and W (at most a few MB) stays resident in every L2.
+__device__ __forceinline__ void xcd_tile(int& bx, int& by) {
+  const int gx = gridDim.x, gy = gridDim.y;
+  if ((gy & 7) == 0) {
+    const int p = blockIdx.x + blockIdx.y * gx;
+    const int xcd = p & 7, slot = p >> 3;
+    by = (slot / gx) * 8 + xcd;
+    bx = slot % gx;
+  } else {
+    bx = blockIdx.x;
+    by = blockIdx.y;
+  }
+}
+
+template <int TM, int TN>
+struct Stage {
+  Frag a[TM], w[TN];
+  float d[TN];
+};
+
+template <int TM, int TN>
+__device__ __forceinline__ void fetch(Stage<TM, TN>& st, const _Float16* const (&ap)[TM],
+                                      const _Float16* const (&wp)[TN], const float* const (&sp)[TN], int b,
+                                      int64_t a_bstride, int64_t w_bstride, int N) {
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++) {
+    const _Float16* p = ap[tm] + b * a_bstride;
+    st.a[tm].lo = *reinterpret_cast<const half8_t*>(p);
+    st.a[tm].hi = *reinterpret_cast<const half8_t*>(p + 8);
+  }
+#pragma unroll
+  for (int tn = 0; tn < TN; tn++) {
+    const _Float16* p = wp[tn] + b * w_bstride;
+    st.w[tn].lo = *reinterpret_cast<const half8_t*>(p);
+    st.w[tn].hi = *reinterpret_cast<const half8_t*>(p + 8);
+    st.d[tn] = sp[tn][(int64_t)b * N];
+  }
+}
+
+template <int TM, int TN, bool SUMS>
+__device__ __forceinline__ void compute(const Stage<TM, TN>& st, f32x16_t (&acc)[TM][TN], int32_t* sums, int M,
+                                        int N, int nb, int b, int m_base, int n_base, int lr, int lh) {
+  const f32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  f32x16_t p[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+      p[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(st.a[tm].lo, st.w[tn].lo, zero, 0, 0, 0);
+      p[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(st.a[tm].hi, st.w[tn].hi, p[tm][tn], 0, 0, 0);
+    }
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+      if (SUMS) {
+        const int col = n_base + tn * 32 + lr;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int row = m_base + tm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          if (row < M && col < N) sums[((int64_t)row * N + col) * nb + b] = (int32_t)p[tm][tn][r];
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[tm][tn][r] = __builtin_fmaf(p[tm][tn][r], st.d[tn], acc[tm][tn][r]);
+    }
+}
+
 // WM x WN waves per workgroup, each wave owns TM x TN tiles of 32x32 outputs.
+// A has a_rows rows per K-block (>= the padded M the grid covers).
 template <int WM, int WN, int TM, int TN, bool SUMS>
-__global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8(const _Float16* __restrict__ A,
+__global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8(const _Float16* __restrict__ A, int a_rows,
                                                              const _Float16* __restrict__ W,
                                                              const float* __restrict__ St,
                                                              const float* __restrict__ row_scale,
@@ -33,30 +116,25 @@ __global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8(const _Float16* __r
                                                              int N, int K) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / WN, wn = wave % WN;
-  const int m_base = blockIdx.y * (WM * TM * 32) + wm * TM * 32;
-  const int n_base = blockIdx.x * (WN * TN * 32) + wn * TN * 32;
+  int bx, by;
+  xcd_tile(bx, by);
+  const int m_base = by * (WM * TM * 32) + wm * TM * 32;
+  const int n_base = bx * (WN * TN * 32) + wn * TN * 32;
   const int lr = lane & 31, lh = lane >> 5;
   const int nb = K >> 5;
+  const int64_t a_bstride = (int64_t)a_rows * 32, w_bstride = (int64_t)N * 32;
 
-  // Operand fetch: lane (lr, lh) supplies row lr of the 32-row group and the
-  // 8 consecutive k at 8*lh (+16 for the second MFMA) of every block.  A and
-  // B use the same (lane half, slot) -> k assignment, so each block's dot
-  // product is complete whatever k order the matrix core applies.
   const _Float16* ap[TM];
   const _Float16* wp[TN];
-  int scol[TN];
+  const float* sp[TN];
 #pragma unroll
-  for (int tm = 0; tm < TM; tm++) {
-    int r = m_base + tm * 32 + lr;
-    r = r < M ? r : M - 1;
-    ap[tm] = A + (int64_t)r * K + lh * 8;
-  }
+  for (int tm = 0; tm < TM; tm++) ap[tm] = A + (int64_t)(m_base + tm * 32 + lr) * 32 + 16 * lh;
 #pragma unroll
   for (int tn = 0; tn < TN; tn++) {
     int c = n_base + tn * 32 + lr;
     c = c < N ? c : N - 1;
-    wp[tn] = W + (int64_t)c * K + lh * 8;
-    scol[tn] = c;
+    wp[tn] = W + (int64_t)c * 32 + 16 * lh;
+    sp[tn] = St + c;
   }
 
   f32x16_t acc[TM][TN];
@@ -67,66 +145,396 @@ __global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8(const _Float16* __r
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[tm][tn][r] = 0.0f;
 
-  const f32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  for (int b = 0; b < nb; b++) {
-    half8_t a0[TM], a1[TM], w0[TN], w1[TN];
-    float d[TN];
-#pragma unroll
-    for (int tm = 0; tm < TM; tm++) {
-      a0[tm] = *reinterpret_cast<const half8_t*>(ap[tm] + b * 32);
-      a1[tm] = *reinterpret_cast<const half8_t*>(ap[tm] + b * 32 + 16);
-    }
-#pragma unroll
-    for (int tn = 0; tn < TN; tn++) {
-      w0[tn] = *reinterpret_cast<const half8_t*>(wp[tn] + b * 32);
-      w1[tn] = *reinterpret_cast<const half8_t*>(wp[tn] + b * 32 + 16);
-      d[tn] = St[(int64_t)b * N + scol[tn]];
-    }
-#pragma unroll
-    for (int tm = 0; tm < TM; tm++) {
-#pragma unroll
-      for (int tn = 0; tn < TN; tn++) {
-        f32x16_t p = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0[tm], w0[tn], zero, 0, 0, 0);
-        p = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[tm], w1[tn], p, 0, 0, 0);
-        if (SUMS) {
-          const int col = n_base + tn * 32 + lr;
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const int row = m_base + tm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            if (row < M && col < N) sums[((int64_t)row * N + col) * nb + b] = (int32_t)p[r];
-          }
-        }
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[tm][tn][r] = __builtin_fmaf(p[r], d[tn], acc[tm][tn][r]);
-      }
-    }
+  // Register double buffer: block b+1 is in flight while block b computes.
+  Stage<TM, TN> s0, s1;
+  fetch<TM, TN>(s0, ap, wp, sp, 0, a_bstride, w_bstride, N);
+  int b = 0;
+  for (; b + 2 <= nb; b += 2) {
+    fetch<TM, TN>(s1, ap, wp, sp, b + 1, a_bstride, w_bstride, N);
+    compute<TM, TN, SUMS>(s0, acc, sums, M, N, nb, b, m_base, n_base, lr, lh);
+    if (b + 2 < nb) fetch<TM, TN>(s0, ap, wp, sp, b + 2, a_bstride, w_bstride, N);
+    compute<TM, TN, SUMS>(s1, acc, sums, M, N, nb, b + 1, m_base, n_base, lr, lh);
   }
+  if (b < nb) compute<TM, TN, SUMS>(s0, acc, sums, M, N, nb, b, m_base, n_base, lr, lh);
 
   // 32x32 accumulator layout: lane holds column lr; register r holds row
-  // 8*(r/4) + 4*lh + r%4 of the tile.
+  // 8*(r/4) + 4*lh + r%4 of the tile.  The row scales are fetched for all
+  // rows first (clamped index, no branch) so the loads overlap.
 #pragma unroll
   for (int tm = 0; tm < TM; tm++) {
+    float rs[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int row = m_base + tm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-      if (row >= M) continue;
-      const float rs = row_scale[row];
+      rs[r] = row_scale[row < M ? row : M - 1];
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = m_base + tm * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
 #pragma unroll
       for (int tn = 0; tn < TN; tn++) {
         const int col = n_base + tn * 32 + lr;
-        if (col < N) Y[(int64_t)row * N + col] = acc[tm][tn][r] * rs;
+        if (row < M && col < N) Y[(int64_t)row * N + col] = acc[tm][tn][r] * rs[r];
       }
     }
   }
 }
 
-template <int WM, int WN, int TM, int TN, bool SUMS>
-hipError_t launch(const _Float16* A, const _Float16* W, const float* St, const float* rs, float* Y, int32_t* sums,
-                  int M, int N, int K, hipStream_t s) {
+// LDS-pipelined variant: the workgroup copies each K-block's A tile (BM rows x
+// 64 B, contiguous in the block-major layout) and W tile (BN x 64 B) plus the
+// BN block scales into an LDS buffer with one coalesced 32-byte read per
+// thread per tile; waves read their MFMA fragments from LDS.  Two register
+// stages keep the global reads two blocks ahead of the compute, and each
+// byte is fetched once per workgroup instead of once per wave.
+template <int WM, int WN, int TM, int TN>
+__global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8_lds(const _Float16* __restrict__ A, int a_rows,
+                                                                 const _Float16* __restrict__ W,
+                                                                 const float* __restrict__ St,
+                                                                 const float* __restrict__ row_scale,
+                                                                 float* __restrict__ Y, int M, int N, int K) {
+  constexpr int NT = WM * WN * SG_WAVE;
   constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
-  dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM);
-  hipLaunchKernelGGL((k_gemm_q8<WM, WN, TM, TN, SUMS>), grid, dim3(WM * WN * SG_WAVE), 0, s, A, W, St, rs, Y, sums,
+  constexpr int A_CH = BM * 2, W_CH = BN * 2;     // 32-byte chunks per tile
+  constexpr int A_PT = (A_CH + NT - 1) / NT, W_PT = (W_CH + NT - 1) / NT;
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * 32];
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[2][BN * 32];
+  __shared__ float Ss[2][BN];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  int bx, by;
+  xcd_tile(bx, by);
+  const int m0 = by * BM, n0 = bx * BN;
+  const int lr = lane & 31, lh = lane >> 5;
+  const int nb = K >> 5;
+  const int64_t a_bstride = (int64_t)a_rows * 32, w_bstride = (int64_t)N * 32;
+
+  struct Reg {
+    half8_t a[A_PT][2], w[W_PT][2];
+    float s;
+  };
+  auto gload = [&](Reg& r, int b) {
+    const _Float16* ab = A + b * a_bstride + (int64_t)m0 * 32;
+#pragma unroll
+    for (int i = 0; i < A_PT; i++) {
+      const int c = tid + i * NT;
+      if (c < A_CH) {
+        r.a[i][0] = *reinterpret_cast<const half8_t*>(ab + c * 16);
+        r.a[i][1] = *reinterpret_cast<const half8_t*>(ab + c * 16 + 8);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < W_PT; i++) {
+      const int c = tid + i * NT;
+      if (c < W_CH) {
+        int row = n0 + (c >> 1);
+        row = row < N ? row : N - 1;
+        const _Float16* wb = W + b * w_bstride + (int64_t)row * 32 + (c & 1) * 16;
+        r.w[i][0] = *reinterpret_cast<const half8_t*>(wb);
+        r.w[i][1] = *reinterpret_cast<const half8_t*>(wb + 8);
+      }
+    }
+    if (tid < BN) {
+      const int col = n0 + tid < N ? n0 + tid : N - 1;
+      r.s = St[(int64_t)b * N + col];
+    }
+  };
+  auto lstore = [&](const Reg& r, int buf) {
+#pragma unroll
+    for (int i = 0; i < A_PT; i++) {
+      const int c = tid + i * NT;
+      if (c < A_CH) {
+        *reinterpret_cast<half8_t*>(&As[buf][c * 16]) = r.a[i][0];
+        *reinterpret_cast<half8_t*>(&As[buf][c * 16 + 8]) = r.a[i][1];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < W_PT; i++) {
+      const int c = tid + i * NT;
+      if (c < W_CH) {
+        *reinterpret_cast<half8_t*>(&Ws[buf][c * 16]) = r.w[i][0];
+        *reinterpret_cast<half8_t*>(&Ws[buf][c * 16 + 8]) = r.w[i][1];
+      }
+    }
+    if (tid < BN) Ss[buf][tid] = r.s;
+  };
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[tm][tn][r] = 0.0f;
+
+  auto compute = [&](int buf) {
+    const f32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    Frag fa[TM], fw[TN];
+    float d[TN];
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++) {
+      const _Float16* p = &As[buf][(wm * TM * 32 + tm * 32 + lr) * 32 + 16 * lh];
+      fa[tm].lo = *reinterpret_cast<const half8_t*>(p);
+      fa[tm].hi = *reinterpret_cast<const half8_t*>(p + 8);
+    }
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+      const int cl = wn * TN * 32 + tn * 32 + lr;
+      const _Float16* p = &Ws[buf][cl * 32 + 16 * lh];
+      fw[tn].lo = *reinterpret_cast<const half8_t*>(p);
+      fw[tn].hi = *reinterpret_cast<const half8_t*>(p + 8);
+      d[tn] = Ss[buf][cl];
+    }
+    f32x16_t p[TM][TN];
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        p[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[tm].lo, fw[tn].lo, zero, 0, 0, 0);
+        p[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[tm].hi, fw[tn].hi, p[tm][tn], 0, 0, 0);
+      }
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[tm][tn][r] = __builtin_fmaf(p[tm][tn][r], d[tn], acc[tm][tn][r]);
+  };
+
+  // Pipeline: LDS buffer (b & 1) holds block b; registers r0/r1 hold the
+  // global reads of blocks b+1 and b+2 (alternating).
+  Reg r0, r1;
+  gload(r0, 0);
+  if (nb > 1) gload(r1, 1);
+  lstore(r0, 0);
+  if (nb > 2) gload(r0, 2);
+  __syncthreads();
+  for (int b = 0; b < nb; b += 2) {
+    compute(0);
+    if (b + 1 < nb) {
+      lstore(r1, 1);
+      if (b + 3 < nb) gload(r1, b + 3);
+    }
+    __syncthreads();
+    if (b + 1 >= nb) break;
+    compute(1);
+    if (b + 2 < nb) {
+      lstore(r0, 0);
+      if (b + 4 < nb) gload(r0, b + 4);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++) {
+    const int mb = m0 + wm * TM * 32 + tm * 32;
+    float rs[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+      rs[r] = row_scale[row < M ? row : M - 1];
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        const int col = n0 + wn * TN * 32 + tn * 32 + lr;
+        if (row < M && col < N) Y[(int64_t)row * N + col] = acc[tm][tn][r] * rs[r];
+      }
+    }
+  }
+}
+
+// Split-path variant: a workgroup of NW waves covers NW*TM*32 rows x TN*32
+// columns.  Each wave streams its own A fragments straight from global
+// memory (through the vector L1), while the workgroup's small W tile of each
+// K-block (TN*32 rows x 64 B) and its block scales are staged once in a
+// double-buffered LDS ring and read by all NW waves.  Operand traffic is
+// split between the L1 path (A, 32 MAC per byte for TN = 2) and the LDS path
+// (W, 16*TM MAC per byte), instead of all of it going through one.
+template <int NW, int TM, int TN>
+__global__ __launch_bounds__(NW* SG_WAVE) void k_gemm_q8_sp(const _Float16* __restrict__ A, int a_rows,
+                                                            const _Float16* __restrict__ W,
+                                                            const float* __restrict__ St,
+                                                            const float* __restrict__ row_scale,
+                                                            float* __restrict__ Y, int M, int N, int K) {
+  constexpr int NT = NW * SG_WAVE;
+  constexpr int BN = TN * 32, BMW = TM * 32;
+  constexpr int W_V = BN * 32 / 4;  // 8-byte pieces of the W tile (BN rows x 32 halfs)
+  constexpr int WPT = (W_V + NT - 1) / NT;
+  __shared__ __attribute__((aligned(16))) _Float16 Ws[2][BN * 32];
+  __shared__ float Ss[2][BN];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lh = lane >> 5;
+  int bx, by;
+  xcd_tile(bx, by);
+  const int n0 = bx * BN;
+  const int mw = by * NW * BMW + wave * BMW;  // this wave's first row
+  const int nb = K >> 5;
+  const int64_t a_bstride = (int64_t)a_rows * 32, w_bstride = (int64_t)N * 32;
+
+  // W piece v of the tile: row n0 + v/8, halfs 4*(v%8) .. +4.
+  const _Float16* wsrc[WPT];
+#pragma unroll
+  for (int i = 0; i < WPT; i++) {
+    const int v = tid + i * NT;
+    const int row = n0 + (v >> 3) < N ? n0 + (v >> 3) : N - 1;
+    wsrc[i] = W + (int64_t)row * 32 + 4 * (v & 7);
+  }
+  const int s_col = n0 + tid < N ? n0 + tid : N - 1;
+  struct WReg {
+    half4_t w[WPT];
+    float s;
+  };
+  auto wload = [&](WReg& r, int b) {
+#pragma unroll
+    for (int i = 0; i < WPT; i++)
+      if (tid + i * NT < W_V) r.w[i] = *reinterpret_cast<const half4_t*>(wsrc[i] + b * w_bstride);
+    if (tid < BN) r.s = St[(int64_t)b * N + s_col];
+  };
+  // LDS W layout: row r (64 B = four 16-byte chunks c) stores chunk c at slot
+  // c ^ ((r >> 2) & 3), so a 16-lane fragment read (16 consecutive rows, one
+  // chunk) touches 16 distinct bank groups.
+  auto wslot = [](int r, int c) { return r * 32 + ((c ^ ((r >> 2) & 3)) << 3); };
+  auto wstore = [&](const WReg& r, int buf) {
+#pragma unroll
+    for (int i = 0; i < WPT; i++) {
+      const int v = tid + i * NT;  // piece v: row v/8, chunk (v%8)/2, half (v%2)
+      if (v < W_V) *reinterpret_cast<half4_t*>(&Ws[buf][wslot(v >> 3, (v & 7) >> 1) + 4 * (v & 1)]) = r.w[i];
+    }
+    if (tid < BN) Ss[buf][tid] = r.s;
+  };
+
+  const _Float16* ap[TM];
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++) ap[tm] = A + (int64_t)(mw + tm * 32 + lr) * 32 + 16 * lh;
+  auto aload = [&](Frag (&f)[TM], int b) {
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++) {
+      const _Float16* p = ap[tm] + b * a_bstride;
+      f[tm].lo = *reinterpret_cast<const half8_t*>(p);
+      f[tm].hi = *reinterpret_cast<const half8_t*>(p + 8);
+    }
+  };
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[tm][tn][r] = 0.0f;
+
+  auto compute = [&](const Frag (&fa)[TM], int buf) {
+    const f32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    Frag fw[TN];
+    float d[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+      const int row = tn * 32 + lr;
+      fw[tn].lo = *reinterpret_cast<const half8_t*>(&Ws[buf][wslot(row, 2 * lh)]);
+      fw[tn].hi = *reinterpret_cast<const half8_t*>(&Ws[buf][wslot(row, 2 * lh + 1)]);
+      d[tn] = Ss[buf][row];
+    }
+    f32x16_t p[TM][TN];
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        p[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[tm].lo, fw[tn].lo, zero, 0, 0, 0);
+        p[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[tm].hi, fw[tn].hi, p[tm][tn], 0, 0, 0);
+      }
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++)
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[tm][tn][r] = __builtin_fmaf(p[tm][tn][r], d[tn], acc[tm][tn][r]);
+  };
+
+  // W ring: LDS buffer (b & 1) holds block b; w0/w1 carry blocks b+1, b+2.
+  // A: registers fa0/fa1 alternate, one block ahead.
+  WReg w0, w1;
+  Frag fa0[TM], fa1[TM];
+  wload(w0, 0);
+  if (nb > 1) wload(w1, 1);
+  aload(fa0, 0);
+  wstore(w0, 0);
+  if (nb > 2) wload(w0, 2);
+  __syncthreads();
+  for (int b = 0; b < nb; b += 2) {
+    if (b + 1 < nb) aload(fa1, b + 1);
+    compute(fa0, 0);
+    if (b + 1 < nb) {
+      wstore(w1, 1);
+      if (b + 3 < nb) wload(w1, b + 3);
+    }
+    __syncthreads();
+    if (b + 1 >= nb) break;
+    if (b + 2 < nb) aload(fa0, b + 2);
+    compute(fa1, 1);
+    if (b + 2 < nb) {
+      wstore(w0, 0);
+      if (b + 4 < nb) wload(w0, b + 4);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int tm = 0; tm < TM; tm++) {
+    const int mb = mw + tm * 32;
+    float rs[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+      rs[r] = row_scale[row < M ? row : M - 1];
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+#pragma unroll
+      for (int tn = 0; tn < TN; tn++) {
+        const int col = n0 + tn * 32 + lr;
+        if (row < M && col < N) Y[(int64_t)row * N + col] = acc[tm][tn][r] * rs[r];
+      }
+    }
+  }
+}
+
+template <int NW, int TM, int TN>
+hipError_t launch_sp(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
+                     int M, int N, int K, hipStream_t s) {
+  constexpr int BM = NW * TM * 32, BN = TN * 32;
+  const int gm = (M + BM - 1) / BM;
+  if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
+  dim3 grid((N + BN - 1) / BN, gm);
+  hipLaunchKernelGGL((k_gemm_q8_sp<NW, TM, TN>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y, M, N, K);
+  return hipGetLastError();
+}
+
+template <int WM, int WN, int TM, int TN>
+hipError_t launch_lds(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
+                      int M, int N, int K, hipStream_t s) {
+  constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
+  const int gm = (M + BM - 1) / BM;
+  if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
+  dim3 grid((N + BN - 1) / BN, gm);
+  hipLaunchKernelGGL((k_gemm_q8_lds<WM, WN, TM, TN>), grid, dim3(WM * WN * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y,
                      M, N, K);
+  return hipGetLastError();
+}
+
+template <int WM, int WN, int TM, int TN, bool SUMS>
+hipError_t launch(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
+                  int32_t* sums, int M, int N, int K, hipStream_t s) {
+  constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
+  const int gm = (M + BM - 1) / BM;
+  if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;  // A must cover the padded rows
+  dim3 grid((N + BN - 1) / BN, gm);
+  hipLaunchKernelGGL((k_gemm_q8<WM, WN, TM, TN, SUMS>), grid, dim3(WM * WN * SG_WAVE), 0, s, A, a_rows, W, St, rs,
+                     Y, sums, M, N, K);
   return hipGetLastError();
 }
 
@@ -134,16 +542,16 @@ hipError_t launch(const _Float16* A, const _Float16* W, const float* St, const f
 
 namespace sgk {
 
-hipError_t gemm_q8(const _Float16* A, const _Float16* W, const float* St, const float* row_scale, float* Y,
-                   int32_t* sums, int M, int N, int K, hipStream_t s) {
+hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* row_scale,
+                   float* Y, int32_t* sums, int M, int N, int K, hipStream_t s) {
   if (M <= 0 || N <= 0) return hipSuccess;
   if (K <= 0 || K % 32) return hipErrorInvalidValue;
-  if (sums) return launch<1, 1, 1, 1, true>(A, W, St, row_scale, Y, sums, M, N, K, s);
-  // Large M: 128x128 workgroup tiles (4 waves of 64x64).  Small problems use
-  // 64x64 tiles so that the grid still covers the 256 compute units.
-  const int64_t tiles128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-  if (tiles128 >= 512) return launch<2, 2, 2, 2, false>(A, W, St, row_scale, Y, nullptr, M, N, K, s);
-  return launch<2, 2, 1, 1, false>(A, W, St, row_scale, Y, nullptr, M, N, K, s);
+  if (sums) return launch<1, 1, 1, 1, true>(A, a_rows, W, St, row_scale, Y, sums, M, N, K, s);
+  // Large M: split-path workgroups of 8 waves (256 rows x 64 columns).
+  // Small M: 64x64 register-direct tiles so the grid still covers the 256
+  // compute units (tile sweeps on MI355X at the model's shapes).
+  if (M >= 8192) return launch_sp<8, 1, 2>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+  return launch<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
 }
 
 }  // namespace sgk

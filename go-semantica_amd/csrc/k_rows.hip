@@ -21,14 +21,14 @@ __device__ __forceinline__ uint16_t rd_u16(const uint8_t* p) { return (uint16_t)
 // One thread per Q8_0 block: 2-byte fp16 scale + 32 int8 values
 // (GGUF Q8_0 layout; extractQ8_0Scales model_int8.go:543-569 reads the same bytes).
 __global__ void k_repack_q8_0(const uint8_t* __restrict__ raw, int rows, int cols, _Float16* __restrict__ w16,
-                              float* __restrict__ st, int ld_st, int row_off) {
+                              float* __restrict__ st, int ld, int row_off) {
   const int nb = cols / 32;
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= (int64_t)rows * nb) return;
   const int r = (int)(id / nb), b = (int)(id % nb);
   const uint8_t* blk = raw + id * 34;
-  st[(int64_t)b * ld_st + row_off + r] = sg_f16_ieee(rd_u16(blk));
-  _Float16* dst = w16 + (int64_t)(row_off + r) * cols + b * 32;
+  st[(int64_t)b * ld + row_off + r] = sg_f16_ieee(rd_u16(blk));
+  _Float16* dst = w16 + ((int64_t)b * ld + row_off + r) * 32;
 #pragma unroll
   for (int i = 0; i < 32; i += 8) {
     half8_t v;
@@ -52,9 +52,12 @@ __global__ void k_repack_embd(const uint8_t* __restrict__ raw, int vocab, int d,
   for (int i = 0; i < 32; i++) dst[i] = (int8_t)blk[2 + i];
 }
 
-__global__ void k_i8_to_f16(const int8_t* __restrict__ x, _Float16* __restrict__ y, int64_t n) {
+__global__ void k_i8_to_f16_blocked(const int8_t* __restrict__ x, int M, int K, _Float16* __restrict__ y,
+                                    int a_rows) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) y[i] = (_Float16)(float)x[i];
+  if (i >= (int64_t)M * K) return;
+  const int m = (int)(i / K), k = (int)(i % K);
+  y[((int64_t)(k >> 5) * a_rows + m) * 32 + (k & 31)] = (_Float16)(float)x[i];
 }
 
 __global__ void k_fill(float* __restrict__ p, float v, int64_t n) {
@@ -141,7 +144,8 @@ template <bool F16>
 __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__ x, int ldx, int rows, int cols,
                                                        const int32_t* __restrict__ row_seq,
                                                        const float* __restrict__ amax, _Float16* __restrict__ qf,
-                                                       int8_t* __restrict__ qi, float* __restrict__ row_scale) {
+                                                       int a_rows, int8_t* __restrict__ qi,
+                                                       float* __restrict__ row_scale) {
   const int c4n = cols >> 2;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (gid >= (int64_t)rows * c4n) return;
@@ -164,16 +168,16 @@ __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__
     }
     qv[t] = q;
   }
-  const int64_t o = (int64_t)row * cols + 4 * c4;
-  if (F16) {
+  if (F16) {  // block-major GEMM operand: [k/32][a_rows][32]
     half4_t h;
 #pragma unroll
     for (int t = 0; t < 4; t++) h[t] = (_Float16)(float)qv[t];
-    *reinterpret_cast<half4_t*>(qf + o) = h;
+    const int k = 4 * c4;
+    *reinterpret_cast<half4_t*>(qf + ((int64_t)(k >> 5) * a_rows + row) * 32 + (k & 31)) = h;
   } else {
     char4 c;
     c.x = (signed char)qv[0]; c.y = (signed char)qv[1]; c.z = (signed char)qv[2]; c.w = (signed char)qv[3];
-    *reinterpret_cast<char4*>(qi + o) = c;
+    *reinterpret_cast<char4*>(qi + (int64_t)row * cols + 4 * c4) = c;
   }
 }
 
@@ -393,10 +397,10 @@ inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1)
 
 namespace sgk {
 
-hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, float* st, int ld_st, int row_off,
+hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, float* st, int ld, int row_off,
                        hipStream_t s) {
   const int64_t n = (int64_t)rows * (cols / 32);
-  hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(n, 256)), dim3(256), 0, s, raw, rows, cols, w16, st, ld_st,
+  hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(n, 256)), dim3(256), 0, s, raw, rows, cols, w16, st, ld,
                      row_off);
   return hipGetLastError();
 }
@@ -407,9 +411,11 @@ hipError_t repack_embd(const uint8_t* raw, int vocab, int d, int8_t* q, float* s
   return hipGetLastError();
 }
 
-hipError_t i8_to_f16(const int8_t* x, _Float16* y, int64_t n, hipStream_t s) {
+hipError_t i8_to_f16_blocked(const int8_t* x, int M, int K, _Float16* y, int a_rows, hipStream_t s) {
+  const int64_t n = (int64_t)M * K;
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_i8_to_f16, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, y, n);
+  if (K % 32 || a_rows < M) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_i8_to_f16_blocked, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, M, K, y, a_rows);
   return hipGetLastError();
 }
 
@@ -449,16 +455,17 @@ hipError_t embed_only(const int32_t* tokens, int T, const int8_t* eq, const floa
 }
 
 hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
-                    _Float16* f16, int8_t* i8, float* row_scale, hipStream_t s) {
+                    _Float16* f16, int a_rows, int8_t* i8, float* row_scale, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   if (cols % 4 || ldx % 4) return hipErrorInvalidValue;
+  if (f16 && (cols % 32 || a_rows < rows)) return hipErrorInvalidValue;
   const int64_t n = (int64_t)rows * (cols / 4);
   if (f16)
     hipLaunchKernelGGL(k_quantize<true>, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, s, x, ldx, rows, cols,
-                       row_seq, amax, f16, nullptr, row_scale);
+                       row_seq, amax, f16, a_rows, nullptr, row_scale);
   else
     hipLaunchKernelGGL(k_quantize<false>, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, s, x, ldx, rows, cols,
-                       row_seq, amax, nullptr, i8, row_scale);
+                       row_seq, amax, nullptr, 0, i8, row_scale);
   return hipGetLastError();
 }
 

@@ -205,7 +205,7 @@ struct sg_ctx {
 struct sg_q8_weight {
   sg_ctx* ctx = nullptr;
   int N = 0, K = 0;
-  _Float16* w = nullptr;  // [N][K]
+  _Float16* w = nullptr;  // block-major [K/32][N][32]
   float* st = nullptr;    // [K/32][N]
 };
 
@@ -372,6 +372,7 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
   float* gu = m->gu.as<float>();
   float* g = m->g.as<float>();
   _Float16* a16 = m->a16.as<_Float16>();
+  const int ar = sgk::gemm_pad_rows(T);
   float* sx = m->sx.as<float>();
   float* amax = m->amax.as<float>();
   auto site = [&](int l, int k) { return amax + ((size_t)4 * l + k) * ns; };
@@ -391,24 +392,24 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
   for (int l = 0; l < L; l++) {
     if (l == stop) break;
     const LayerDev& ly = m->layers[l];
-    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 0), a16, nullptr, sx, s));
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), sgk::gemm_q8(a16, ly.wqkv, ly.sqkv, sx, qkv, nullptr, T, nqkv, d, s));
+    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 0), a16, ar, nullptr, sx, s));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), sgk::gemm_q8(a16, ar, ly.wqkv, ly.sqkv, sx, qkv, nullptr, T, nqkv, d, s));
     SG_LAUNCH(SG_K_NORM, t * (qd + kvd) * 8.0,
               sgk::qknorm_rope(qkv, nqkv, qkv + qd, nqkv, ly.q_norm, ly.k_norm, c.num_heads, c.num_kv_heads, T,
                                meta.row_pos, m->cos_t, m->sin_t, eps, s));
     SG_LAUNCH(SG_K_ATTENTION, attn_flops,
               sgk::attention(qkv, nqkv, qkv + qd, qkv + qd + kvd, nqkv, att, qd, meta.seq_off, meta.items,
                              meta.n_items, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale, site(l, 1), s));
-    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), sgk::quantize(att, qd, T, qd, meta.row_seq, site(l, 1), a16, nullptr, sx, s));
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), sgk::gemm_q8(a16, ly.wo, ly.so, sx, o, nullptr, T, d, qd, s));
+    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), sgk::quantize(att, qd, T, qd, meta.row_seq, site(l, 1), a16, ar, nullptr, sx, s));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), sgk::gemm_q8(a16, ar, ly.wo, ly.so, sx, o, nullptr, T, d, qd, s));
     SG_LAUNCH(SG_K_NORM, t * d * 16.0,
               sgk::post_res_norm(o, h, ly.post_attn, ly.ffn_norm, eps, T, d, xn, meta.row_seq, site(l, 2), s));
-    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 2), a16, nullptr, sx, s));
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(2 * ff, d), sgk::gemm_q8(a16, ly.wgu, ly.sgu, sx, gu, nullptr, T, 2 * ff, d, s));
+    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 2), a16, ar, nullptr, sx, s));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(2 * ff, d), sgk::gemm_q8(a16, ar, ly.wgu, ly.sgu, sx, gu, nullptr, T, 2 * ff, d, s));
     SG_LAUNCH(SG_K_GELU, t * ff * 12.0,
               sgk::gelu_mul(g, ff, gu, 2 * ff, gu + ff, 2 * ff, T, ff, meta.row_seq, site(l, 3), s));
-    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(ff), sgk::quantize(g, ff, T, ff, meta.row_seq, site(l, 3), a16, nullptr, sx, s));
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), sgk::gemm_q8(a16, ly.wd, ly.sd, sx, o, nullptr, T, d, ff, s));
+    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(ff), sgk::quantize(g, ff, T, ff, meta.row_seq, site(l, 3), a16, ar, nullptr, sx, s));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), sgk::gemm_q8(a16, ar, ly.wd, ly.sd, sx, o, nullptr, T, d, ff, s));
     const bool last = l + 1 == L;
     SG_LAUNCH(SG_K_NORM, t * d * 16.0,
               sgk::post_res_norm(o, h, ly.post_ffw, last ? m->out_norm : m->layers[l + 1].attn_norm, eps, T, d, xn,
@@ -451,7 +452,7 @@ int ensure_workspace(sg_model* m, int T, int n_seq) {
   SG_TRY(m->o.ensure(sizeof(float) * t * c.embed_dim));
   SG_TRY(m->gu.ensure(sizeof(float) * t * 2 * c.interm_dim));
   SG_TRY(m->g.ensure(sizeof(float) * t * c.interm_dim));
-  SG_TRY(m->a16.ensure(sizeof(_Float16) * t * a_cols));
+  SG_TRY(m->a16.ensure(sizeof(_Float16) * (size_t)sgk::gemm_pad_rows(T) * a_cols));
   SG_TRY(m->sx.ensure(sizeof(float) * t));
   SG_TRY(m->amax.ensure(sizeof(float) * 4 * (size_t)c.num_layers * n_seq));
   SG_TRY(m->err.ensure(64));
@@ -711,7 +712,7 @@ int sg_quantize_act(sg_ctx* ctx, const float* x, int32_t rows, int32_t cols, con
   float* row_scale = amax + n_seq;
   SG_HIP(sgk::fill_f32(amax, 0.0f, n_seq, s));
   SG_HIP(sgk::absmax_rows(x, cols, rows, cols, meta.row_seq, amax, s));
-  SG_HIP(sgk::quantize(x, cols, rows, cols, meta.row_seq, amax, nullptr, q_out, row_scale, s));
+  SG_HIP(sgk::quantize(x, cols, rows, cols, meta.row_seq, amax, nullptr, 0, q_out, row_scale, s));
   SG_HIP(sgk::seq_scales(amax, n_seq, scale_out, s));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;
@@ -725,18 +726,17 @@ static int matmul_common(sg_ctx* ctx, float* dst, int32_t* sums, const sg_q8_wei
   std::lock_guard<std::mutex> lk(ctx->mu);
   SG_TRY(set_device(ctx));
   hipStream_t s = pick(ctx, stream);
-  const int64_t n = (int64_t)batch * w->K;
-  SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)n));
-  SG_HIP(sgk::i8_to_f16(x, ctx->f16.as<_Float16>(), n, s));
+  const int ar = sgk::gemm_pad_rows(batch);
+  SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)ar * w->K));
+  SG_HIP(sgk::i8_to_f16_blocked(x, batch, w->K, ctx->f16.as<_Float16>(), ar, s));
   if (sums) {
     SG_TRY(ctx->amax.ensure(sizeof(float) * (size_t)batch));
     float* ones = ctx->amax.as<float>();
     SG_HIP(sgk::fill_f32(ones, 1.0f, batch, s));
-    float* scratch_y = nullptr;
     DevBuf y;
     SG_TRY(y.ensure(sizeof(float) * (size_t)batch * w->N));
-    scratch_y = y.as<float>();
-    hipError_t e = sgk::gemm_q8(ctx->f16.as<_Float16>(), w->w, w->st, ones, scratch_y, sums, batch, w->N, w->K, s);
+    hipError_t e = sgk::gemm_q8(ctx->f16.as<_Float16>(), ar, w->w, w->st, ones, y.as<float>(), sums, batch, w->N,
+                                w->K, s);
     hipError_t e2 = hipStreamSynchronize(s);
     y.release();
     SG_HIP(e);
@@ -744,7 +744,7 @@ static int matmul_common(sg_ctx* ctx, float* dst, int32_t* sums, const sg_q8_wei
     return SG_OK;
   }
   if (!row_scale) return fail(SG_ERR_INVALID, "row_scale is NULL");
-  SG_HIP(sgk::gemm_q8(ctx->f16.as<_Float16>(), w->w, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s));
+  SG_HIP(sgk::gemm_q8(ctx->f16.as<_Float16>(), ar, w->w, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;
 }

@@ -9,14 +9,22 @@ struct sg_item { int32_t seq, q0; };  // one attention work item: 32 query rows 
 
 namespace sgk {
 
+// GEMM operands are block-major fp16 [K/32][rows][32]; activation buffers hold
+// gemm_pad_rows(M) rows per K-block so that every workgroup tile reads
+// allocated memory (rows past M are never stored).
+constexpr int kGemmRowPad = 256;
+inline int gemm_pad_rows(int M) { return (M + kGemmRowPad - 1) / kGemmRowPad * kGemmRowPad; }
+
 // ---- load-time repack (k_rows.hip) ----
-// Raw Q8_0 rows [rows][cols/32][34 B] -> fp16 integer weights w16[(row_off+r)*cols + k]
-// and fp32 block scales (IEEE converter) transposed st[b*ld_st + row_off + r].
-hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, float* st, int ld_st,
-                       int row_off, hipStream_t s);
+// Raw Q8_0 rows [rows][cols/32][34 B] -> block-major fp16 integer weights
+// w16[b][row_off + r][32] (ld rows per block) and fp32 block scales (IEEE
+// converter) st[b][row_off + r] (ld per block).
+hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, float* st, int ld, int row_off,
+                       hipStream_t s);
 // token_embd: int8 values q[v][d] and per-block scales (gguf halving converter) sc[v][d/32].
 hipError_t repack_embd(const uint8_t* raw, int vocab, int d, int8_t* q, float* sc, hipStream_t s);
-hipError_t i8_to_f16(const int8_t* x, _Float16* y, int64_t n, hipStream_t s);
+// int8 x[M][K] -> block-major fp16 y[K/32][a_rows][32].
+hipError_t i8_to_f16_blocked(const int8_t* x, int M, int K, _Float16* y, int a_rows, hipStream_t s);
 hipError_t fill_f32(float* p, float v, int64_t n, hipStream_t s);
 
 // ---- per-row kernels (k_rows.hip) ----
@@ -25,9 +33,10 @@ hipError_t embed_norm(const int32_t* tokens, int T, const int8_t* eq, const floa
                       float sqrt_d, const float* w, float eps, const int32_t* row_seq, float* h, float* xn,
                       float* amax, int32_t* err, hipStream_t s);
 // Per-sequence symmetric quantization of x[rows][cols] (stride ldx) using amax[row_seq[r]].
-// Writes fp16-encoded integers (f16 != null) or int8 (i8 != null) [rows][cols] and row_scale[rows].
+// Writes fp16-encoded integers block-major f16[cols/32][a_rows][32] (f16 != null, the
+// GEMM operand) or int8 row-major i8[rows][cols] (i8 != null), and row_scale[rows].
 hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
-                    _Float16* f16, int8_t* i8, float* row_scale, hipStream_t s);
+                    _Float16* f16, int a_rows, int8_t* i8, float* row_scale, hipStream_t s);
 hipError_t absmax_rows(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, float* amax,
                        hipStream_t s);
 hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s);
@@ -52,8 +61,10 @@ hipError_t embed_only(const int32_t* tokens, int T, const int8_t* eq, const floa
 // ---- GEMM (k_gemm.hip) ----
 // Y[M][N] = (sum_b float(P_b) * St[b][n]) * row_scale[m]; A fp16 [M][K], W fp16 [N][K].
 // sums != null additionally dumps the exact block sums int32 [M][N][K/32].
-hipError_t gemm_q8(const _Float16* A, const _Float16* W, const float* St, const float* row_scale, float* Y,
-                   int32_t* sums, int M, int N, int K, hipStream_t s);
+// A block-major [K/32][a_rows][32] (a_rows >= gemm_pad_rows(M)), W block-major [K/32][N][32],
+// St [K/32][N].
+hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* row_scale,
+                   float* Y, int32_t* sums, int M, int N, int K, hipStream_t s);
 
 // ---- attention (k_attention.hip) ----
 hipError_t attention(const float* q, int ldq, const float* k, const float* v, int ldkv, float* out, int ldo,
