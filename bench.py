@@ -37,6 +37,9 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, host CPUs)")
     ap.add_argument("--cpu-seqs", type=int, default=0, help="0: 6 x cpu threads")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="after the timed region, run a plain fp32 copy kernel (y = -x) of this many MiB "
+                         "three times, so a counter run can scale FETCH_SIZE/WRITE_SIZE to bytes")
     return ap.parse_args()
 
 
@@ -93,6 +96,15 @@ def main():
     dt = time.perf_counter() - t0
     prof = model.profile_read()
     model.profile_enable(False)
+
+    if a.copy_calib_mib:
+        n = a.copy_calib_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     emb = d_out.cpu().numpy()
     assert np.all(np.isfinite(emb)) and np.allclose(np.sum(emb.astype(np.float64) ** 2, axis=1), 1.0, atol=1e-4)

@@ -100,22 +100,27 @@ __global__ __launch_bounds__(kThreads) void k_embed_norm(const int32_t* __restri
   constexpr int D = NPL * 8;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7;
-  if (row >= T) return;
-  float x[NPL];
-  gather_row<NPL>(tokens, row, eq, es, vocab, sqrt_d, j, x, err);
-  float* hr = h + (int64_t)row * D;
-#pragma unroll
-  for (int i = 0; i < NPL; i++) hr[8 * i + j] = x[i];
-  sg_rmsnorm8<NPL>(x, w, j, eps);
-  float* yr = xn + (int64_t)row * D;
+  const bool valid = row < T;
   float m = 0.0f;
+  if (valid) {
+    float x[NPL];
+    gather_row<NPL>(tokens, row, eq, es, vocab, sqrt_d, j, x, err);
+    float* hr = h + (int64_t)row * D;
 #pragma unroll
-  for (int i = 0; i < NPL; i++) {
-    yr[8 * i + j] = x[i];
-    m = fmaxf(m, fabsf(x[i]));
+    for (int i = 0; i < NPL; i++) hr[8 * i + j] = x[i];
+    sg_rmsnorm8<NPL>(x, w, j, eps);
+    float* yr = xn + (int64_t)row * D;
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+      yr[8 * i + j] = x[i];
+      m = fmaxf(m, fabsf(x[i]));
+    }
   }
-  m = sg_max8(m);
-  if (j == 0 && amax) sg_atomic_max_nonneg(amax + row_seq[row], m);
+  if (amax) {
+    m = sg_max8(m);
+    const int r0 = blockIdx.x * kRowsPerBlock;
+    sg_block_seq_max<kThreads>(m, valid && j == 0, row, r0, min(r0 + kRowsPerBlock, T) - 1, row_seq, amax);
+  }
 }
 
 template <int NPL>
@@ -197,22 +202,25 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(float* dst, const float* s
   constexpr int D = NPL * 8;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7;
-  if (row >= rows) return;
-  float x[NPL];
-  const float* sr = src + (int64_t)row * D;
-#pragma unroll
-  for (int i = 0; i < NPL; i++) x[i] = sr[8 * i + j];
-  sg_rmsnorm8<NPL>(x, w, j, eps);
-  float* dr = dst + (int64_t)row * D;
+  const bool valid = row < rows;
   float m = 0.0f;
+  if (valid) {
+    float x[NPL];
+    const float* sr = src + (int64_t)row * D;
 #pragma unroll
-  for (int i = 0; i < NPL; i++) {
-    dr[8 * i + j] = x[i];
-    m = fmaxf(m, fabsf(x[i]));
+    for (int i = 0; i < NPL; i++) x[i] = sr[8 * i + j];
+    sg_rmsnorm8<NPL>(x, w, j, eps);
+    float* dr = dst + (int64_t)row * D;
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+      dr[8 * i + j] = x[i];
+      m = fmaxf(m, fabsf(x[i]));
+    }
   }
   if (amax) {
     m = sg_max8(m);
-    if (j == 0) sg_atomic_max_nonneg(amax + row_seq[row], m);
+    const int r0 = blockIdx.x * kRowsPerBlock;
+    sg_block_seq_max<kThreads>(m, valid && j == 0, row, r0, min(r0 + kRowsPerBlock, rows) - 1, row_seq, amax);
   }
 }
 
@@ -228,29 +236,32 @@ __global__ __launch_bounds__(kThreads) void k_post_res_norm(const float* __restr
   constexpr int D = NPL * 8;
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7;
-  if (row >= T) return;
-  float x[NPL];
-  const float* orow = o + (int64_t)row * D;
-#pragma unroll
-  for (int i = 0; i < NPL; i++) x[i] = orow[8 * i + j];
-  if (w_post) sg_rmsnorm8<NPL>(x, w_post, j, eps);
-  float* hr = h + (int64_t)row * D;
-#pragma unroll
-  for (int i = 0; i < NPL; i++) {
-    x[i] = x[i] + hr[8 * i + j];
-    hr[8 * i + j] = x[i];
-  }
-  if (w_next) sg_rmsnorm8<NPL>(x, w_next, j, eps);
-  float* yr = xn + (int64_t)row * D;
+  const bool valid = row < T;
   float m = 0.0f;
+  if (valid) {
+    float x[NPL];
+    const float* orow = o + (int64_t)row * D;
 #pragma unroll
-  for (int i = 0; i < NPL; i++) {
-    yr[8 * i + j] = x[i];
-    m = fmaxf(m, fabsf(x[i]));
+    for (int i = 0; i < NPL; i++) x[i] = orow[8 * i + j];
+    if (w_post) sg_rmsnorm8<NPL>(x, w_post, j, eps);
+    float* hr = h + (int64_t)row * D;
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+      x[i] = x[i] + hr[8 * i + j];
+      hr[8 * i + j] = x[i];
+    }
+    if (w_next) sg_rmsnorm8<NPL>(x, w_next, j, eps);
+    float* yr = xn + (int64_t)row * D;
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+      yr[8 * i + j] = x[i];
+      m = fmaxf(m, fabsf(x[i]));
+    }
   }
   if (amax) {
     m = sg_max8(m);
-    if (j == 0) sg_atomic_max_nonneg(amax + row_seq[row], m);
+    const int r0 = blockIdx.x * kRowsPerBlock;
+    sg_block_seq_max<kThreads>(m, valid && j == 0, row, r0, min(r0 + kRowsPerBlock, T) - 1, row_seq, amax);
   }
 }
 
@@ -305,37 +316,38 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope(float* __restrict__ q,
 // ------------------------------------------------------------ GELU * up --
 
 // GELUQuickSIMD (activation.go:47-95) then VecMulF32 (matmul.go:238-259):
-// g = geluquick(gate) * up, one row per block, plus the row's max|g|.
+// g = geluquick(gate) * up over kGeluRows rows per workgroup (the float4
+// slots of those rows are dealt to the threads in turn), plus the sequences'
+// max|g|.  A workgroup inside one sequence folds its maximum with one atomic;
+// one straddling two sequences folds each row's maximum separately.
+constexpr int kGeluRows = 8;
 __global__ __launch_bounds__(kThreads) void k_gelu_mul(float* __restrict__ g, int ldd, const float* __restrict__ gate,
-                                                       int ldg, const float* __restrict__ up, int ldu, int cols,
-                                                       const int32_t* __restrict__ row_seq,
+                                                       int ldg, const float* __restrict__ up, int ldu, int rows,
+                                                       int cols, const int32_t* __restrict__ row_seq,
                                                        float* __restrict__ amax) {
-  __shared__ float red[kThreads / SG_WAVE];
-  const int row = blockIdx.x;
-  const float* gr = gate + (int64_t)row * ldg;
-  const float* ur = up + (int64_t)row * ldu;
-  float* dr = g + (int64_t)row * ldd;
+  const int r0 = blockIdx.x * kGeluRows;
+  const int nr = min(kGeluRows, rows - r0);
+  const int c4n = cols >> 2;
+  const bool one_seq = amax && row_seq[r0] == row_seq[r0 + nr - 1];
   float m = 0.0f;
-  for (int c4 = threadIdx.x; c4 < (cols >> 2); c4 += kThreads) {
-    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(gr + 4 * c4);
-    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(ur + 4 * c4);
+  for (int idx = threadIdx.x; idx < nr * c4n; idx += kThreads) {
+    const int row = r0 + idx / c4n, c4 = idx % c4n;
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(gate + (int64_t)row * ldg + 4 * c4);
+    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(up + (int64_t)row * ldu + 4 * c4);
     f32x4_t r;
+    float mr = 0.0f;
 #pragma unroll
     for (int t = 0; t < 4; t++) {
       r[t] = sg_gelu_quick(a[t]) * b[t];
-      m = fmaxf(m, fabsf(r[t]));
+      mr = fmaxf(mr, fabsf(r[t]));
     }
-    *reinterpret_cast<f32x4_t*>(dr + 4 * c4) = r;
+    *reinterpret_cast<f32x4_t*>(g + (int64_t)row * ldd + 4 * c4) = r;
+    if (one_seq)
+      m = fmaxf(m, mr);
+    else if (amax)
+      sg_atomic_max_nonneg(amax + row_seq[row], mr);
   }
-  if (!amax) return;
-  m = sg_wave_max(m);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float mm = red[0];
-    for (int i = 1; i < kThreads / SG_WAVE; i++) mm = fmaxf(mm, red[i]);
-    sg_atomic_max_nonneg(amax + row_seq[row], mm);
-  }
+  if (one_seq) sg_block_seq_max<kThreads>(m, false, r0, r0, r0 + nr - 1, row_seq, amax);
 }
 
 
@@ -505,7 +517,8 @@ hipError_t gelu_mul(float* g, int ldd, const float* gate, int ldg, const float* 
                     const int32_t* row_seq, float* amax, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   if (cols % 4 || ldd % 4 || ldg % 4 || ldu % 4) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_gelu_mul, dim3(rows), dim3(kThreads), 0, s, g, ldd, gate, ldg, up, ldu, cols, row_seq, amax);
+  hipLaunchKernelGGL(k_gelu_mul, dim3(blocks_for(rows, kGeluRows)), dim3(kThreads), 0, s, g, ldd, gate, ldg, up, ldu,
+                     rows, cols, row_seq, amax);
   return hipGetLastError();
 }
 

@@ -108,6 +108,40 @@ __device__ __forceinline__ float sg_wave_max(float a) {
   return a;
 }
 
+// Monotone float max for non-negative values via the uint bit pattern.
+__device__ __forceinline__ void sg_atomic_max_nonneg(float* addr, float v) {
+  atomicMax(reinterpret_cast<unsigned int*>(addr), __float_as_uint(v));
+}
+
+// Folds per-row maxima into the per-sequence maxima amax[row_seq[row]] for
+// the rows [r_first, r_last] a workgroup of NT threads owns.  Rows are packed
+// sequence by sequence (row_seq is non-decreasing), so when the first and the
+// last row share a sequence the whole workgroup reduces to ONE atomic; a
+// workgroup that straddles sequences issues one atomic per row from the
+// row's owner thread.  Thousands of same-address atomics (one per row)
+// serialise in L2, hence the reduction.  m: the caller's row maximum (0 for
+// threads without a row), non-negative.  Every thread of the workgroup must
+// call this (it holds a barrier).
+template <int NT>
+__device__ __forceinline__ void sg_block_seq_max(float m, bool owner, int row, int r_first, int r_last,
+                                                 const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
+  __shared__ float red[NT / 64];
+  const int s0 = row_seq[r_first];
+  if (s0 == row_seq[r_last]) {
+    m = sg_wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float mm = red[0];
+#pragma unroll
+      for (int i = 1; i < NT / 64; i++) mm = fmaxf(mm, red[i]);
+      sg_atomic_max_nonneg(amax + s0, mm);
+    }
+  } else if (owner) {
+    sg_atomic_max_nonneg(amax + row_seq[row], m);
+  }
+}
+
 // RMSNorm of one row held by an 8-lane group, internal/kernels/norm.go:8-36.
 // Lane j of the group holds x[i] = row[8*i + j] (NPL = n/8 values): that is
 // exactly lane j of dotProductAVX2Asm's YMM accumulator, which runs
@@ -131,7 +165,3 @@ __device__ __forceinline__ void sg_rmsnorm8(float (&x)[NPL], const float* __rest
   }
 }
 
-// Monotone float max for non-negative values via the uint bit pattern.
-__device__ __forceinline__ void sg_atomic_max_nonneg(float* addr, float v) {
-  atomicMax(reinterpret_cast<unsigned int*>(addr), __float_as_uint(v));
-}
