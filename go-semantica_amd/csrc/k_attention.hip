@@ -25,205 +25,275 @@
 // fastExp argument and, through fastExp's polynomial error, the weights by
 // ~1e-5).
 //
-// Work split: one workgroup = one (sequence, 32-query block, kv head), 6
-// waves = 2 sub-blocks of 16 queries x G=3 query heads, so every K/V tile
-// staged in LDS serves all heads that share it.  Scores are computed
-// transposed (S^T = K Q^T, v_mfma_f32_16x16x32_f16): a lane owns one query
-// and 4 keys of each 16-key subtile, and those registers are exactly the B
-// operand slots of O^T = V^T P^T -- no shuffles between the two products.
+// Operands arrive already split (the QK-norm/RoPE kernel writes Q and K hi/lo,
+// k_v_split_t writes V^T hi/lo), so every workgroup only copies fp16 tiles.
+//
+// Work split.  The G query heads that share a kv head are stacked into
+// G*ceil(S/32) chunks of 32 (head, query) rows.  A workgroup is 4 waves, one
+// chunk each, one wave per SIMD; all four stream the same 32-key K and V^T
+// tiles through LDS.  A wave holds its chunk's Q^T (split, 128 VGPRs) and its
+// O^T accumulators (256 dims x 32 queries, 128 AGPRs) for the whole run.
+// Scores are computed transposed, S^T = K Q^T on v_mfma_f32_32x32x16_f16: a
+// lane owns one query and 16 keys of the tile, so row max and row sum are
+// lane-local plus one exchange, and those 16 registers are exactly the B
+// operand of O^T += V^T P^T once V^T's keys are stored in the matching order
+// (k_v_split_t swaps the middle two 4-key groups of every 16 keys).
 #include "sg_device.h"
 #include "sg_kernels.h"
 
 namespace {
 
-constexpr int BK = 32;          // keys per tile
-constexpr int QW = 16;          // queries per wave
-constexpr int QB = 32 / QW;     // query sub-blocks per workgroup
-constexpr int KPAD = 8, VPAD = 8;
-constexpr float kQKScale = 8.0f;
+constexpr int kHD = 256;            // head_dim
+constexpr int kBK = 32;             // keys per tile
+constexpr int kWaves = 4;           // chunks (waves) per workgroup
+constexpr int kKStride = kHD + 8;   // LDS K row, halves (conflict-free 16-B reads)
+constexpr int kVStride = kBK + 8;   // LDS V^T row, halves
+constexpr float kQKScale = sgk::kAttnQKScale;
 constexpr float kPScale = 1024.0f, kPUnscale = 1.0f / 1024.0f;
 
-struct hl16 {
-  _Float16 hi, lo;
-};
-__device__ __forceinline__ hl16 split_f16(float x) {
-  const _Float16 hi = (_Float16)x;
-  return hl16{hi, (_Float16)(x - (float)hi)};
+__device__ __forceinline__ f32x16_t mfma32(half8_t a, half8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ f32x4_t mfma16(half8_t a, half8_t b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
+// Position of key k (0..31) inside a V^T tile row: bits 2 and 3 swapped, so
+// that lane half h reads keys {4h..4h+3, 8+4h..8+4h+3} (+16 for the second
+// 16-key step) as 8 contiguous halves -- the keys its S^T registers hold.
+__device__ __forceinline__ int vt_pos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
-template <int HD, int G>
-__global__ __launch_bounds__(G* QB* SG_WAVE) void k_attention(const float* __restrict__ q, int ldq,
-                                                              const float* __restrict__ k,
-                                                              const float* __restrict__ v, int ldkv,
-                                                              float* __restrict__ out, int ldo,
-                                                              const int32_t* __restrict__ seq_off,
-                                                              const sg_item* __restrict__ items, float scale,
-                                                              float* __restrict__ amax) {
-  __shared__ _Float16 Kh[BK][HD + KPAD], Kl[BK][HD + KPAD];
-  __shared__ _Float16 Vh[HD][BK + VPAD], Vl[HD][BK + VPAD];  // V^T
-  constexpr int NT = G * QB * SG_WAVE;
-  constexpr int NC = HD / 32;  // 32-dim chunks (k of the QK^T MFMA)
-  constexpr int ND = HD / 16;  // 16-dim output tiles of P.V
+__global__ __launch_bounds__(kWaves * SG_WAVE, 1) void k_attn(
+    const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
+    const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vth, const _Float16* __restrict__ vtl,
+    int ldvt, float* __restrict__ out, int ldo, const int32_t* __restrict__ seq_off,
+    const int32_t* __restrict__ voff, const sg_item* __restrict__ items, int G, float sscale,
+    float* __restrict__ amax) {
+  __shared__ _Float16 Ks[2][kBK][kKStride];  // [hi/lo][key][dim]
+  __shared__ _Float16 Vs[2][kHD][kVStride];  // [hi/lo][dim][key, vt_pos order]
+  __shared__ float red[kWaves];
 
   const sg_item it = items[blockIdx.x];
   const int kvh = blockIdx.y;
   const int r0 = seq_off[it.seq];
   const int S = seq_off[it.seq + 1] - r0;
+  const int vo = voff[it.seq];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int lq = lane & 15, lg = lane >> 4;  // column (query) and row group of the 16x16 tiles
-  const int head = kvh * G + (w % G);
-  const int qrow = it.q0 + (w / G) * QW + lq;
-  const bool qvalid = qrow < S;
+  const int ln = lane & 31, h = lane >> 5;
+  const int nqb = (S + 31) >> 5;
+  const int c = it.c0 + w;
+  const bool active = c < G * nqb;  // wave-uniform
+  const int g = active ? c / nqb : 0;
+  const int q0 = active ? (c % nqb) * 32 : 0;
+  const int head = kvh * G + g;
+  const int qrow = q0 + ln;
+  const bool qvalid = active && qrow < S;
 
-  // Q^T as the B operand: lane owns query qrow, dims 32c + 8*lg .. +8 (scaled by 8, split).
-  half8_t qh[NC], ql[NC];
+  // Q^T as the B operand: lane (query ln, half h), k-step ks: dims 16ks+8h..+8.
+  half8_t bqh[kHD / 16], bql[kHD / 16];
   {
-    const float* qp = q + (int64_t)(r0 + (qvalid ? qrow : S - 1)) * ldq + head * HD + 8 * lg;
+    const int64_t qo = (int64_t)(r0 + min(qrow, S - 1)) * ldq + head * kHD + 8 * h;
 #pragma unroll
-    for (int c = 0; c < NC; c++) {
-      const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(qp + 32 * c);
-      const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(qp + 32 * c + 4);
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const hl16 a = split_f16(x0[t] * kQKScale), b = split_f16(x1[t] * kQKScale);
-        qh[c][t] = a.hi;
-        ql[c][t] = a.lo;
-        qh[c][t + 4] = b.hi;
-        ql[c][t + 4] = b.lo;
-      }
+    for (int ks = 0; ks < kHD / 16; ks++) {
+      bqh[ks] = *reinterpret_cast<const half8_t*>(qh + qo + 16 * ks);
+      bql[ks] = *reinterpret_cast<const half8_t*>(ql + qo + 16 * ks);
     }
   }
 
-  const float* kbase = k + (int64_t)r0 * ldkv + kvh * HD;
-  const float* vbase = v + (int64_t)r0 * ldkv + kvh * HD;
-
+  // Tile staging through registers: 2048 16-B chunks per tile, 8 per thread.
+  // K chunk u: hi/lo u>>2, key (tid>>5) + 8(u&3), dims 8(tid&31)..+8.
+  // V^T chunk u: hi/lo u>>2, dim (tid>>2) + 64(u&3), keys 8(tid&3)..+8.
+  half8_t stg[8];
+  const _Float16* kbase_h = kh + kvh * kHD + 8 * (tid & 31);
+  const _Float16* kbase_l = kl + kvh * kHD + 8 * (tid & 31);
   auto load_k = [&](int kt) {
-    for (int idx = tid; idx < BK * HD / 4; idx += NT) {
-      const int key = idx / (HD / 4), d4 = idx % (HD / 4);
-      const int kr = kt + key < S ? kt + key : S - 1;
-      const f32x4_t x = *reinterpret_cast<const f32x4_t*>(kbase + (int64_t)kr * ldkv + 4 * d4);
-      half4_t h, l;
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const hl16 p = split_f16(x[t] * kQKScale);
-        h[t] = p.hi;
-        l[t] = p.lo;
-      }
-      *reinterpret_cast<half4_t*>(&Kh[key][4 * d4]) = h;
-      *reinterpret_cast<half4_t*>(&Kl[key][4 * d4]) = l;
+    for (int u = 0; u < 8; u++) {
+      const int key = (tid >> 5) + 8 * (u & 3);
+      const int64_t row = r0 + min(kt + key, S - 1);
+      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 2) ? kbase_l : kbase_h) + row * ldk);
     }
   };
-  auto load_v = [&](int kt) {
-    for (int idx = tid; idx < BK * HD / 4; idx += NT) {
-      const int key = idx % BK, d4 = idx / BK;
-      const int kr = kt + key < S ? kt + key : S - 1;
-      const f32x4_t x = *reinterpret_cast<const f32x4_t*>(vbase + (int64_t)kr * ldkv + 4 * d4);
+  auto store_k = [&]() {
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
-        const hl16 p = split_f16(x[t]);
-        Vh[4 * d4 + t][key] = p.hi;
-        Vl[4 * d4 + t][key] = p.lo;
-      }
+    for (int u = 0; u < 8; u++)
+      *reinterpret_cast<half8_t*>(&Ks[u >> 2][(tid >> 5) + 8 * (u & 3)][8 * (tid & 31)]) = stg[u];
+  };
+  const int64_t vrow0 = (int64_t)(kvh * kHD + (tid >> 2)) * ldvt + vo + 8 * (tid & 3);
+  auto load_v = [&](int kt) {
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int64_t o = vrow0 + (int64_t)(64 * (u & 3)) * ldvt + kt;
+      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 2) ? vtl : vth) + o);
     }
+  };
+  auto store_v = [&]() {
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      *reinterpret_cast<half8_t*>(&Vs[u >> 2][(tid >> 2) + 64 * (u & 3)][8 * (tid & 3)]) = stg[u];
   };
 
-  // Scores of key subtile st of the staged tile, split product (scaled by 64).
-  // S^T subtile: lane holds query lq, keys 16*st + 4*lg + r (r = 0..3).
-  auto scores = [&](int st) {
-    f32x4_t acc = {0, 0, 0, 0};
+  // S^T tile (32 keys x 32 queries), scaled by 64: lane holds query ln and
+  // keys 8(r/4) + 4h + r%4 of the tile in register r.
+  auto scores = [&]() {
+    f32x16_t acc = {};
 #pragma unroll
-    for (int c = 0; c < NC; c++) {
-      const half8_t ah = *reinterpret_cast<const half8_t*>(&Kh[16 * st + lq][32 * c + 8 * lg]);
-      const half8_t al = *reinterpret_cast<const half8_t*>(&Kl[16 * st + lq][32 * c + 8 * lg]);
-      acc = mfma16(ah, qh[c], acc);
-      acc = mfma16(ah, ql[c], acc);
-      acc = mfma16(al, qh[c], acc);
+    for (int ks = 0; ks < kHD / 16; ks++) {
+      const half8_t ah = *reinterpret_cast<const half8_t*>(&Ks[0][ln][16 * ks + 8 * h]);
+      const half8_t al = *reinterpret_cast<const half8_t*>(&Ks[1][ln][16 * ks + 8 * h]);
+      acc = mfma32(ah, bqh[ks], acc);
+      acc = mfma32(ah, bql[ks], acc);
+      acc = mfma32(al, bqh[ks], acc);
     }
     return acc;
   };
-  const float sscale = scale / (kQKScale * kQKScale);
+  auto key_of = [&](int kt, int r) { return kt + 8 * (r >> 2) + 4 * h + (r & 3); };
 
   // ---- pass 1: row max ----
   float m = -INFINITY;
-  for (int kt = 0; kt < S; kt += BK) {
+  load_k(0);
+  for (int kt = 0; kt < S; kt += kBK) {
+    __syncthreads();  // every wave is done with the previous tile
+    store_k();
     __syncthreads();
-    load_k(kt);
-    __syncthreads();
+    if (kt + kBK < S) load_k(kt + kBK);  // in flight during the MFMAs
+    if (active) {
+      const f32x16_t acc = scores();
 #pragma unroll
-    for (int st = 0; st < 2; st++) {
-      const f32x4_t acc = scores(st);
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        if (kt + 16 * st + 4 * lg + r < S) m = fmaxf(m, acc[r] * sscale);
+      for (int r = 0; r < 16; r++)
+        if (key_of(kt, r) < S) m = fmaxf(m, acc[r] * sscale);
     }
   }
-  m = fmaxf(m, __shfl_xor(m, 16));
   m = fmaxf(m, __shfl_xor(m, 32));
 
   // ---- pass 2: e = fastExp(s - m), row sums, O^T += V^T P^T ----
-  f32x4_t o[ND];
+  f32x16_t o[kHD / 32];
 #pragma unroll
-  for (int dt = 0; dt < ND; dt++) o[dt] = f32x4_t{0, 0, 0, 0};
+  for (int mt = 0; mt < kHD / 32; mt++) o[mt] = f32x16_t{};
   float lsum = 0.0f;
-  for (int kt = 0; kt < S; kt += BK) {
-    __syncthreads();
-    load_k(kt);
-    load_v(kt);
-    __syncthreads();
-    half8_t ph, pl;  // slots 0..3: keys 4lg+r of subtile 0; slots 4..7: 16+4lg+r
+  load_k(0);
+  __syncthreads();  // pass 1's last tile is consumed
+  store_k();
+  __syncthreads();
+  for (int kt = 0; kt < S; kt += kBK) {
+    load_v(kt);  // in flight during the score MFMAs
+    half8_t ph[2], pl[2];
+    if (active) {
+      const f32x16_t acc = scores();
 #pragma unroll
-    for (int st = 0; st < 2; st++) {
-      const f32x4_t acc = scores(st);
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float e = kt + 16 * st + 4 * lg + r < S ? sg_fast_exp(acc[r] * sscale - m) : 0.0f;
+      for (int r = 0; r < 16; r++) {
+        const float e = key_of(kt, r) < S ? sg_fast_exp(acc[r] * sscale - m) : 0.0f;
         lsum = lsum + e;
         const hl16 p = split_f16(e * kPScale);
-        ph[4 * st + r] = p.hi;
-        pl[4 * st + r] = p.lo;
+        ph[r >> 3][r & 7] = p.hi;
+        pl[r >> 3][r & 7] = p.lo;
       }
     }
+    store_v();
+    __syncthreads();  // V^T tile staged; K tile free
+    const bool more = kt + kBK < S;
+    if (more) load_k(kt + kBK);  // in flight during the P.V MFMAs
+    if (active) {
 #pragma unroll
-    for (int dt = 0; dt < ND; dt++) {
-      const _Float16* vh = &Vh[16 * dt + lq][0];
-      const _Float16* vl = &Vl[16 * dt + lq][0];
-      const half4_t h0 = *reinterpret_cast<const half4_t*>(vh + 4 * lg);
-      const half4_t h1 = *reinterpret_cast<const half4_t*>(vh + 16 + 4 * lg);
-      const half4_t l0 = *reinterpret_cast<const half4_t*>(vl + 4 * lg);
-      const half4_t l1 = *reinterpret_cast<const half4_t*>(vl + 16 + 4 * lg);
-      const half8_t ah = {h0[0], h0[1], h0[2], h0[3], h1[0], h1[1], h1[2], h1[3]};
-      const half8_t al = {l0[0], l0[1], l0[2], l0[3], l1[0], l1[1], l1[2], l1[3]};
-      o[dt] = mfma16(ah, ph, o[dt]);
-      o[dt] = mfma16(ah, pl, o[dt]);
-      o[dt] = mfma16(al, ph, o[dt]);
+      for (int mt = 0; mt < kHD / 32; mt++) {
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+          const half8_t ah = *reinterpret_cast<const half8_t*>(&Vs[0][32 * mt + ln][16 * st + 8 * h]);
+          const half8_t al = *reinterpret_cast<const half8_t*>(&Vs[1][32 * mt + ln][16 * st + 8 * h]);
+          o[mt] = mfma32(ah, ph[st], o[mt]);
+          o[mt] = mfma32(ah, pl[st], o[mt]);
+          o[mt] = mfma32(al, ph[st], o[mt]);
+        }
+      }
     }
+    if (more) store_k();  // nobody reads Ks between the two barriers
+    __syncthreads();      // K tile staged; V^T tile free
   }
-  lsum = lsum + __shfl_xor(lsum, 16);
   lsum = lsum + __shfl_xor(lsum, 32);
   const float f = (1.0f / lsum) * kPUnscale;
 
-  // O^T tile dt: lane holds query lq, dims 16*dt + 4*lg + r.
+  // O^T tile mt: lane holds query ln, dims 32mt + 8(r/4) + 4h + r%4.
   float mx = 0.0f;
   if (qvalid) {
-    float* op = out + (int64_t)(r0 + qrow) * ldo + head * HD + 4 * lg;
+    float* op = out + (int64_t)(r0 + qrow) * ldo + head * kHD + 4 * h;
 #pragma unroll
-    for (int dt = 0; dt < ND; dt++) {
-      f32x4_t y;
+    for (int mt = 0; mt < kHD / 32; mt++) {
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        y[r] = o[dt][r] * f;
-        mx = fmaxf(mx, fabsf(y[r]));
+      for (int rb = 0; rb < 4; rb++) {
+        f32x4_t y;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          y[j] = o[mt][4 * rb + j] * f;
+          mx = fmaxf(mx, fabsf(y[j]));
+        }
+        *reinterpret_cast<f32x4_t*>(op + 32 * mt + 8 * rb) = y;
       }
-      *reinterpret_cast<f32x4_t*>(op + 16 * dt) = y;
     }
   }
-  if (amax) {
+  if (amax) {  // all chunks of a workgroup belong to one sequence
     mx = sg_wave_max(mx);
-    if (lane == 0) sg_atomic_max_nonneg(amax + it.seq, mx);
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    if (tid == 0) {
+      float mm = red[0];
+#pragma unroll
+      for (int i = 1; i < kWaves; i++) mm = fmaxf(mm, red[i]);
+      sg_atomic_max_nonneg(amax + it.seq, mm);
+    }
+  }
+}
+
+// V [T][ldv] fp32 (kv head blockIdx.y at column 256*kvh) -> V^T hi/lo fp16
+// [HKV*256][ldvt]: sequence s occupies columns voff[s] .. voff[s] + 32*ceil(S/32),
+// keys in vt_pos order inside every 32-key tile, zeros past S.
+__global__ __launch_bounds__(256) void k_v_split_t(const float* __restrict__ v, int ldv,
+                                                   const int32_t* __restrict__ seq_off,
+                                                   const int32_t* __restrict__ voff,
+                                                   const sg_item* __restrict__ vtiles, _Float16* __restrict__ vth,
+                                                   _Float16* __restrict__ vtl, int ldvt) {
+  __shared__ _Float16 th[2][kHD][kVStride];
+  const sg_item t = vtiles[blockIdx.x];
+  const int kvh = blockIdx.y;
+  const int r0 = seq_off[t.seq], S = seq_off[t.seq + 1] - r0, k0 = t.c0;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < 8; u++) {  // 32 keys x 64 float4
+    const int idx = tid + 256 * u;
+    const int key = idx >> 6, d4 = idx & 63;
+    f32x4_t x = {0, 0, 0, 0};
+    if (k0 + key < S) x = *reinterpret_cast<const f32x4_t*>(v + (int64_t)(r0 + k0 + key) * ldv + kvh * kHD + 4 * d4);
+    const int p = vt_pos(key);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const hl16 s = split_f16(x[j]);
+      th[0][4 * d4 + j][p] = s.hi;
+      th[1][4 * d4 + j][p] = s.lo;
+    }
+  }
+  __syncthreads();
+  const int64_t col = voff[t.seq] + k0;
+#pragma unroll
+  for (int u = 0; u < 8; u++) {  // 2 x 256 rows x 4 chunks of 8 keys
+    const int idx = tid + 256 * u;
+    const int hl = idx >> 10, dim = (idx >> 2) & 255, c8 = idx & 3;
+    _Float16* dst = (hl ? vtl : vth) + (int64_t)(kvh * kHD + dim) * ldvt + col + 8 * c8;
+    *reinterpret_cast<half8_t*>(dst) = *reinterpret_cast<const half8_t*>(&th[hl][dim][8 * c8]);
+  }
+}
+
+// Rows of x (fp32) -> hi/lo fp16 of x*scale.
+__global__ __launch_bounds__(256) void k_split_rows(const float* __restrict__ x, int ldx, int cols, float scale,
+                                                    _Float16* __restrict__ hi, _Float16* __restrict__ lo,
+                                                    int ldo) {
+  const int row = blockIdx.x;
+  for (int c4 = threadIdx.x; c4 < cols / 4; c4 += 256) {
+    const f32x4_t a = *reinterpret_cast<const f32x4_t*>(x + (int64_t)row * ldx + 4 * c4);
+    half4_t vh, vl;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const hl16 s = split_f16(a[j] * scale);
+      vh[j] = s.hi;
+      vl[j] = s.lo;
+    }
+    *reinterpret_cast<half4_t*>(hi + (int64_t)row * ldo + 4 * c4) = vh;
+    *reinterpret_cast<half4_t*>(lo + (int64_t)row * ldo + 4 * c4) = vl;
   }
 }
 
@@ -231,21 +301,33 @@ __global__ __launch_bounds__(G* QB* SG_WAVE) void k_attention(const float* __res
 
 namespace sgk {
 
-hipError_t attention(const float* q, int ldq, const float* k, const float* v, int ldkv, float* out, int ldo,
-                     const int32_t* seq_off, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
+hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles,
+                     int n_vtiles, int HKV, _Float16* vth, _Float16* vtl, int ldvt, hipStream_t s) {
+  if (n_vtiles <= 0) return hipSuccess;
+  if ((ldv & 3) || (ldvt & 7)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_v_split_t, dim3(n_vtiles, HKV), dim3(256), 0, s, v, ldv, seq_off, voff, vtiles, vth, vtl,
+                     ldvt);
+  return hipGetLastError();
+}
+
+hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, _Float16* hi, _Float16* lo, int ldo,
+                      hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if ((ldx & 3) || (cols & 3) || (ldo & 3)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_split_rows, dim3(rows), dim3(256), 0, s, x, ldx, cols, scale, hi, lo, ldo);
+  return hipGetLastError();
+}
+
+hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
+                     const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo, const int32_t* seq_off,
+                     const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
                      float* amax, hipStream_t s) {
   if (n_items <= 0) return hipSuccess;
-  if (hd != 256 || HKV <= 0 || H % HKV) return hipErrorInvalidValue;
-  if ((ldq | ldkv | ldo) & 3) return hipErrorInvalidValue;
-  const int G = H / HKV;
-  dim3 grid(n_items, HKV);
-  switch (G) {
-    case 1: hipLaunchKernelGGL((k_attention<256, 1>), grid, dim3(1 * QB * 64), 0, s, q, ldq, k, v, ldkv, out, ldo, seq_off, items, scale, amax); break;
-    case 2: hipLaunchKernelGGL((k_attention<256, 2>), grid, dim3(2 * QB * 64), 0, s, q, ldq, k, v, ldkv, out, ldo, seq_off, items, scale, amax); break;
-    case 3: hipLaunchKernelGGL((k_attention<256, 3>), grid, dim3(3 * QB * 64), 0, s, q, ldq, k, v, ldkv, out, ldo, seq_off, items, scale, amax); break;
-    case 4: hipLaunchKernelGGL((k_attention<256, 4>), grid, dim3(4 * QB * 64), 0, s, q, ldq, k, v, ldkv, out, ldo, seq_off, items, scale, amax); break;
-    default: return hipErrorInvalidValue;
-  }
+  if (hd != kHD || HKV <= 0 || H % HKV) return hipErrorInvalidValue;
+  if ((ldq | ldk | ldvt) & 7 || (ldo & 3)) return hipErrorInvalidValue;
+  const float sscale = scale / (kQKScale * kQKScale);
+  hipLaunchKernelGGL(k_attn, dim3(n_items, HKV), dim3(kWaves * SG_WAVE), 0, s, qh, ql, ldq, kh, kl, ldk, vth, vtl,
+                     ldvt, out, ldo, seq_off, voff, items, H / HKV, sscale, amax);
   return hipGetLastError();
 }
 

@@ -277,7 +277,10 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope(float* __restrict__ q,
                                                           const float* __restrict__ kw, int H, int HKV, int T,
                                                           const int32_t* __restrict__ row_pos,
                                                           const float* __restrict__ cos_t,
-                                                          const float* __restrict__ sin_t, float eps) {
+                                                          const float* __restrict__ sin_t, float eps,
+                                                          _Float16* __restrict__ qs_h, _Float16* __restrict__ qs_l,
+                                                          int ldqs, _Float16* __restrict__ ks_h,
+                                                          _Float16* __restrict__ ks_l, int ldks) {
   constexpr int NPL = 32, HALF = 128;
   const int g = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7;
@@ -309,8 +312,26 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope(float* __restrict__ q,
     x[i] = a - b;
     x[i + NPL / 2] = cc + dd;
   }
+  if (!qs_h) {
 #pragma unroll
-  for (int i = 0; i < NPL; i++) p[8 * i + j] = x[i];
+    for (int i = 0; i < NPL; i++) p[8 * i + j] = x[i];
+    return;
+  }
+  // Attention operands: hi/lo fp16 of x * kAttnQKScale.
+  _Float16 *dh, *dl;
+  if (hh < H) {
+    dh = qs_h + (int64_t)t * ldqs + hh * 256;
+    dl = qs_l + (int64_t)t * ldqs + hh * 256;
+  } else {
+    dh = ks_h + (int64_t)t * ldks + (hh - H) * 256;
+    dl = ks_l + (int64_t)t * ldks + (hh - H) * 256;
+  }
+#pragma unroll
+  for (int i = 0; i < NPL; i++) {
+    const hl16 sp = split_f16(x[i] * sgk::kAttnQKScale);
+    dh[8 * i + j] = sp.hi;
+    dl[8 * i + j] = sp.lo;
+  }
 }
 
 // ------------------------------------------------------------ GELU * up --
@@ -496,11 +517,13 @@ hipError_t rmsnorm(float* dst, const float* src, const float* w, int rows, int n
 }
 
 hipError_t qknorm_rope(float* q, int ldq, float* k, int ldk, const float* qw, const float* kw, int H, int HKV, int T,
-                       const int32_t* row_pos, const float* cos_t, const float* sin_t, float eps, hipStream_t s) {
+                       const int32_t* row_pos, const float* cos_t, const float* sin_t, float eps, _Float16* qs_h,
+                       _Float16* qs_l, int ldqs, _Float16* ks_h, _Float16* ks_l, int ldks, hipStream_t s) {
   if (T <= 0) return hipSuccess;
+  if (qs_h && (!qs_l || !ks_h || !ks_l)) return hipErrorInvalidValue;
   const int64_t groups = (int64_t)T * (H + HKV);
   hipLaunchKernelGGL(k_qknorm_rope, dim3(blocks_for(groups, kRowsPerBlock)), dim3(kThreads), 0, s, q, ldq, k, ldk,
-                     qw, kw, H, HKV, T, row_pos, cos_t, sin_t, eps);
+                     qw, kw, H, HKV, T, row_pos, cos_t, sin_t, eps, qs_h, qs_l, ldqs, ks_h, ks_l, ldks);
   return hipGetLastError();
 }
 

@@ -13,6 +13,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -104,48 +105,87 @@ struct HostBuf {
 
 // Per-call sequence metadata built on the host from CSR offsets.
 struct Meta {
-  int T = 0, n_seq = 0, n_items = 0;
+  int T = 0, n_seq = 0, n_items = 0, n_vtiles = 0;
+  int Tp = 0;         // V^T columns: every sequence padded to whole 32-key tiles
   double sum_sq = 0;  // sum over sequences of S^2 (attention work)
   // device views into one buffer
   int32_t* row_seq = nullptr;
   int32_t* row_pos = nullptr;
   int32_t* seq_off = nullptr;
-  sg_item* items = nullptr;
+  int32_t* voff = nullptr;   // [n_seq + 1] V^T column of each sequence
+  sg_item* items = nullptr;  // attention workgroups (sequence, first chunk)
+  sg_item* vtiles = nullptr; // V^T split tiles (sequence, first key)
 };
 
-size_t meta_bytes(int T, int n_seq, int n_items) {
-  return sizeof(int32_t) * ((size_t)2 * T + n_seq + 1) + sizeof(sg_item) * (size_t)n_items + 64;
-}
+// Attention workgroups of one sequence: G*ceil(S/32) chunks, kAttnChunks each.
+int seq_groups(int S, int G) { return (G * ((S + 31) / 32) + sgk::kAttnChunks - 1) / sgk::kAttnChunks; }
 
-int count_items(const int32_t* off, int n_seq) {
-  int n = 0;
-  for (int i = 0; i < n_seq; i++) n += (off[i + 1] - off[i] + 31) / 32;
-  return n;
-}
-
-// Fills `host` with [row_seq | row_pos | seq_off | items] and copies it to
-// `dev` on stream s (the copy is complete when this returns).
-int stage_meta(const int32_t* off, int n_seq, HostBuf& host, DevBuf& dev, hipStream_t s, Meta& m) {
+// Fills `host` with [row_seq | row_pos | seq_off | voff | items | vtiles] and
+// copies it to `dev` on stream s (the copy is complete when this returns).
+// G: query heads per kv head.
+//
+// Workgroup order.  Workgroup i of a launch runs on XCD i % 8 (the dispatcher
+// deals workgroups round-robin over the eight XCDs, each with its own L2), so
+// sequences are binned to XCDs (largest first, onto the least-loaded bin) and
+// the list interleaves the bins: all workgroups of a sequence then share one
+// L2 copy of its K and V^T.
+int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev, hipStream_t s, Meta& m) {
+  constexpr int kXcd = 8;
   const int T = off[n_seq];
-  const int n_items = count_items(off, n_seq);
-  const size_t bytes = meta_bytes(T, n_seq, n_items);
+  int n_items = 0, n_vt = 0;
+  for (int i = 0; i < n_seq; i++) {
+    n_items += seq_groups(off[i + 1] - off[i], G);
+    n_vt += (off[i + 1] - off[i] + 31) / 32;
+  }
+  const size_t bytes = sizeof(int32_t) * ((size_t)2 * T + 2 * (n_seq + 1)) +
+                       sizeof(sg_item) * ((size_t)n_items + n_vt) + 64;
   SG_TRY(host.ensure(bytes));
   SG_TRY(dev.ensure(bytes));
   int32_t* h = host.as<int32_t>();
   int32_t* rs = h;
   int32_t* rp = rs + T;
   int32_t* so = rp + T;
-  sg_item* it = reinterpret_cast<sg_item*>(so + n_seq + 1);
-  int k = 0;
+  int32_t* vo = so + n_seq + 1;
+  sg_item* it = reinterpret_cast<sg_item*>(vo + n_seq + 1);
+  sg_item* vt = it + n_items;
+  int nv = 0;
+  vo[0] = 0;
   for (int i = 0; i < n_seq; i++) {
+    const int S = off[i + 1] - off[i];
     so[i] = off[i];
+    vo[i + 1] = vo[i] + sgk::attn_key_pad(S);
     for (int r = off[i]; r < off[i + 1]; r++) {
       rs[r] = i;
       rp[r] = r - off[i];
     }
-    for (int q0 = 0; q0 < off[i + 1] - off[i]; q0 += 32) it[k++] = sg_item{i, q0};
+    for (int k0 = 0; k0 < S; k0 += 32) vt[nv++] = sg_item{i, k0};
   }
   so[n_seq] = off[n_seq];
+  {
+    std::vector<int> order(n_seq);
+    for (int i = 0; i < n_seq; i++) order[i] = i;
+    auto work = [&](int i) { return (double)seq_groups(off[i + 1] - off[i], G) * (off[i + 1] - off[i]); };
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return work(a) > work(b); });
+    std::vector<std::vector<sg_item>> bin(kXcd);
+    double load[kXcd] = {};
+    for (int i : order) {
+      int b = 0;
+      for (int x = 1; x < kXcd; x++)
+        if (load[x] < load[b]) b = x;
+      load[b] += work(i);
+      for (int c0 = 0, n = seq_groups(off[i + 1] - off[i], G); c0 < n * sgk::kAttnChunks; c0 += sgk::kAttnChunks)
+        bin[b].push_back(sg_item{i, c0});
+    }
+    size_t pos[kXcd] = {};
+    for (int k = 0; k < n_items; k++) {
+      int b = k % kXcd;
+      if (pos[b] == bin[b].size()) {  // this bin ran dry: take from the fullest one
+        for (int x = 0; x < kXcd; x++)
+          if (bin[x].size() - pos[x] > bin[b].size() - pos[b]) b = x;
+      }
+      it[k] = bin[b][pos[b]++];
+    }
+  }
   SG_HIP(hipMemcpyAsync(dev.p, host.p, bytes, hipMemcpyHostToDevice, s));
   SG_HIP(hipStreamSynchronize(s));
   int32_t* d = dev.as<int32_t>();
@@ -154,10 +194,14 @@ int stage_meta(const int32_t* off, int n_seq, HostBuf& host, DevBuf& dev, hipStr
   m.sum_sq = 0;
   for (int i = 0; i < n_seq; i++) m.sum_sq += (double)(off[i + 1] - off[i]) * (off[i + 1] - off[i]);
   m.n_items = n_items;
+  m.n_vtiles = n_vt;
+  m.Tp = vo[n_seq];
   m.row_seq = d;
   m.row_pos = d + T;
   m.seq_off = d + 2 * T;
-  m.items = reinterpret_cast<sg_item*>(d + 2 * T + n_seq + 1);
+  m.voff = d + 2 * T + n_seq + 1;
+  m.items = reinterpret_cast<sg_item*>(d + 2 * T + 2 * (n_seq + 1));
+  m.vtiles = m.items + n_items;
   return SG_OK;
 }
 
@@ -199,7 +243,7 @@ struct sg_ctx {
   hipStream_t stream = nullptr;
   std::mutex mu;  // guards the scratch below for the kernel seam
   HostBuf meta_h;
-  DevBuf meta_d, f16, amax, tab;
+  DevBuf meta_d, f16, amax, tab, split;
 };
 
 struct sg_q8_weight {
@@ -279,6 +323,7 @@ struct sg_model {
   std::vector<LayerDev> layers;
   // forward workspace (grown on demand)
   DevBuf h, xn, qkv, att, o, gu, g, a16, sx, amax, meta_d, tokens, out, err;
+  DevBuf qs, ks, vt;  // attention operands, hi/lo fp16 (Q, K row-major; V^T)
   HostBuf meta_h, io_h;
   std::mutex mu;
 
@@ -292,7 +337,8 @@ struct sg_model {
   }
   ~sg_model() {
     for (void* p : allocs) (void)hipFree(p);
-    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &gu, &g, &a16, &sx, &amax, &meta_d, &tokens, &out, &err}) b->release();
+    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &gu, &g, &a16, &sx, &amax, &meta_d, &tokens, &out, &err, &qs, &ks, &vt})
+      b->release();
     meta_h.release();
     io_h.release();
   }
@@ -373,6 +419,12 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
   float* g = m->g.as<float>();
   _Float16* a16 = m->a16.as<_Float16>();
   const int ar = sgk::gemm_pad_rows(T);
+  _Float16* qs_h = m->qs.as<_Float16>();
+  _Float16* qs_l = qs_h + (size_t)T * qd;
+  _Float16* ks_h = m->ks.as<_Float16>();
+  _Float16* ks_l = ks_h + (size_t)T * kvd;
+  _Float16* vt_h = m->vt.as<_Float16>();
+  _Float16* vt_l = vt_h + (size_t)kvd * meta.Tp;
   float* sx = m->sx.as<float>();
   float* amax = m->amax.as<float>();
   auto site = [&](int l, int k) { return amax + ((size_t)4 * l + k) * ns; };
@@ -396,10 +448,14 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
     SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), sgk::gemm_q8(a16, ar, ly.wqkv, ly.sqkv, sx, qkv, nullptr, T, nqkv, d, s));
     SG_LAUNCH(SG_K_NORM, t * (qd + kvd) * 8.0,
               sgk::qknorm_rope(qkv, nqkv, qkv + qd, nqkv, ly.q_norm, ly.k_norm, c.num_heads, c.num_kv_heads, T,
-                               meta.row_pos, m->cos_t, m->sin_t, eps, s));
+                               meta.row_pos, m->cos_t, m->sin_t, eps, qs_h, qs_l, qd, ks_h, ks_l, kvd, s));
+    SG_LAUNCH(SG_K_NORM, t * kvd * 8.0,
+              sgk::v_split_t(qkv + qd + kvd, nqkv, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles,
+                             c.num_kv_heads, vt_h, vt_l, meta.Tp, s));
     SG_LAUNCH(SG_K_ATTENTION, attn_flops,
-              sgk::attention(qkv, nqkv, qkv + qd, qkv + qd + kvd, nqkv, att, qd, meta.seq_off, meta.items,
-                             meta.n_items, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale, site(l, 1), s));
+              sgk::attention(qs_h, qs_l, qd, ks_h, ks_l, kvd, vt_h, vt_l, meta.Tp, att, qd, meta.seq_off, meta.voff,
+                             meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale,
+                             site(l, 1), s));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), sgk::quantize(att, qd, T, qd, meta.row_seq, site(l, 1), a16, ar, nullptr, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), sgk::gemm_q8(a16, ar, ly.wo, ly.so, sx, o, nullptr, T, d, qd, s));
     SG_LAUNCH(SG_K_NORM, t * d * 16.0,
@@ -440,7 +496,7 @@ int check_forward_args(const sg_model* m, const int32_t* off, int n_seq, int out
   return SG_OK;
 }
 
-int ensure_workspace(sg_model* m, int T, int n_seq) {
+int ensure_workspace(sg_model* m, int T, int n_seq, int Tp) {
   const sg_model_config& c = m->cfg;
   const size_t t = (size_t)T;
   const int amax_cols = c.embed_dim > c.interm_dim ? c.embed_dim : c.interm_dim;
@@ -455,6 +511,9 @@ int ensure_workspace(sg_model* m, int T, int n_seq) {
   SG_TRY(m->a16.ensure(sizeof(_Float16) * (size_t)sgk::gemm_pad_rows(T) * a_cols));
   SG_TRY(m->sx.ensure(sizeof(float) * t));
   SG_TRY(m->amax.ensure(sizeof(float) * 4 * (size_t)c.num_layers * n_seq));
+  SG_TRY(m->qs.ensure(2 * sizeof(_Float16) * t * m->qd));
+  SG_TRY(m->ks.ensure(2 * sizeof(_Float16) * t * m->kvd));
+  SG_TRY(m->vt.ensure(2 * sizeof(_Float16) * (size_t)m->kvd * Tp));
   SG_TRY(m->err.ensure(64));
   return SG_OK;
 }
@@ -464,9 +523,9 @@ int forward_device_locked(sg_model* m, const int32_t* d_tokens, const int32_t* o
   SG_TRY(check_forward_args(m, off, n_seq, out_dim));
   SG_TRY(set_device(m->ctx));
   const int T = off[n_seq];
-  SG_TRY(ensure_workspace(m, T, n_seq));
   Meta meta;
-  SG_TRY(stage_meta(off, n_seq, m->meta_h, m->meta_d, s, meta));
+  SG_TRY(stage_meta(off, n_seq, m->cfg.num_heads / m->cfg.num_kv_heads, m->meta_h, m->meta_d, s, meta));
+  SG_TRY(ensure_workspace(m, T, n_seq, meta.Tp));
   SG_TRY(run_forward(m, d_tokens, meta, out_dim, d_out, s, stop));
   SG_TRY(m->io_h.ensure(64));
   SG_HIP(hipMemcpyAsync(m->io_h.p, m->err.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
@@ -512,6 +571,7 @@ void sg_shutdown(sg_ctx* c) {
   c->f16.release();
   c->amax.release();
   c->tab.release();
+  c->split.release();
   (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -706,7 +766,7 @@ int sg_quantize_act(sg_ctx* ctx, const float* x, int32_t rows, int32_t cols, con
   SG_TRY(set_device(ctx));
   hipStream_t s = pick(ctx, stream);
   Meta meta;
-  SG_TRY(stage_meta(off, n_seq, ctx->meta_h, ctx->meta_d, s, meta));
+  SG_TRY(stage_meta(off, n_seq, 1, ctx->meta_h, ctx->meta_d, s, meta));
   SG_TRY(ctx->amax.ensure(sizeof(float) * ((size_t)n_seq + (size_t)rows)));
   float* amax = ctx->amax.as<float>();
   float* row_scale = amax + n_seq;
@@ -781,7 +841,7 @@ int sg_qknorm_rope(sg_ctx* ctx, float* q, int32_t ldq, float* k, int32_t ldk, co
   SG_TRY(set_device(ctx));
   hipStream_t s = pick(ctx, stream);
   Meta meta;
-  SG_TRY(stage_meta(off, n_seq, ctx->meta_h, ctx->meta_d, s, meta));
+  SG_TRY(stage_meta(off, n_seq, 1, ctx->meta_h, ctx->meta_d, s, meta));
   std::vector<float> ct, st;
   rope_tables(head_dim, rope_base, max_seq_len, ct, st);
   SG_TRY(ctx->tab.ensure(sizeof(float) * (ct.size() + st.size())));
@@ -789,7 +849,7 @@ int sg_qknorm_rope(sg_ctx* ctx, float* q, int32_t ldq, float* k, int32_t ldk, co
   SG_HIP(hipMemcpy(tc, ct.data(), sizeof(float) * ct.size(), hipMemcpyHostToDevice));
   SG_HIP(hipMemcpy(tc + ct.size(), st.data(), sizeof(float) * st.size(), hipMemcpyHostToDevice));
   SG_HIP(sgk::qknorm_rope(q, ldq, k, ldk, q_norm, k_norm, n_heads, n_kv_heads, meta.T, meta.row_pos, tc,
-                          tc + ct.size(), eps, s));
+                          tc + ct.size(), eps, nullptr, nullptr, 0, nullptr, nullptr, 0, s));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;
 }
@@ -805,10 +865,23 @@ int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const flo
   SG_TRY(set_device(ctx));
   hipStream_t s = pick(ctx, stream);
   Meta meta;
-  SG_TRY(stage_meta(off, n_seq, ctx->meta_h, ctx->meta_d, s, meta));
+  SG_TRY(stage_meta(off, n_seq, n_heads / n_kv_heads, ctx->meta_h, ctx->meta_d, s, meta));
   const float scale = 1.0f / (float)std::sqrt((double)head_dim);
-  SG_HIP(sgk::attention(q, ldq, k, v, ldkv, out, n_heads * head_dim, meta.seq_off, meta.items, meta.n_items, n_heads,
-                        n_kv_heads, head_dim, scale, nullptr, s));
+  // Split operands as the forward's producers write them.
+  const size_t T = (size_t)meta.T, qd = (size_t)n_heads * head_dim, kvd = (size_t)n_kv_heads * head_dim;
+  SG_TRY(ctx->split.ensure(2 * sizeof(_Float16) * (T * qd + T * kvd + kvd * (size_t)meta.Tp)));
+  _Float16* qs_h = ctx->split.as<_Float16>();
+  _Float16* qs_l = qs_h + T * qd;
+  _Float16* ks_h = qs_l + T * qd;
+  _Float16* ks_l = ks_h + T * kvd;
+  _Float16* vt_h = ks_l + T * kvd;
+  _Float16* vt_l = vt_h + kvd * (size_t)meta.Tp;
+  SG_HIP(sgk::split_rows(q, ldq, meta.T, (int)qd, sgk::kAttnQKScale, qs_h, qs_l, (int)qd, s));
+  SG_HIP(sgk::split_rows(k, ldkv, meta.T, (int)kvd, sgk::kAttnQKScale, ks_h, ks_l, (int)kvd, s));
+  SG_HIP(sgk::v_split_t(v, ldkv, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles, n_kv_heads, vt_h, vt_l,
+                        meta.Tp, s));
+  SG_HIP(sgk::attention(qs_h, qs_l, (int)qd, ks_h, ks_l, (int)kvd, vt_h, vt_l, meta.Tp, out, (int)qd, meta.seq_off,
+                        meta.voff, meta.items, meta.n_items, n_heads, n_kv_heads, head_dim, scale, nullptr, s));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;
 }
@@ -850,7 +923,7 @@ int sg_pool_l2(sg_ctx* ctx, float* out, const float* x, int32_t ldx, int32_t out
   SG_TRY(set_device(ctx));
   hipStream_t s = pick(ctx, stream);
   Meta meta;
-  SG_TRY(stage_meta(off, n_seq, ctx->meta_h, ctx->meta_d, s, meta));
+  SG_TRY(stage_meta(off, n_seq, 1, ctx->meta_h, ctx->meta_d, s, meta));
   SG_HIP(sgk::pool_l2(out, x, ldx, out_dim, meta.seq_off, n_seq, s));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;

@@ -108,6 +108,16 @@ __device__ __forceinline__ float sg_wave_max(float a) {
   return a;
 }
 
+// Split of an fp32 value into two fp16 terms, x ~= hi + lo with
+// hi = fp16(x) and lo = fp16(x - hi) (x - hi is exact in fp32).
+struct hl16 {
+  _Float16 hi, lo;
+};
+__device__ __forceinline__ hl16 split_f16(float x) {
+  const _Float16 hi = (_Float16)x;
+  return hl16{hi, (_Float16)(x - (float)hi)};
+}
+
 // Monotone float max for non-negative values via the uint bit pattern.
 __device__ __forceinline__ void sg_atomic_max_nonneg(float* addr, float v) {
   atomicMax(reinterpret_cast<unsigned int*>(addr), __float_as_uint(v));

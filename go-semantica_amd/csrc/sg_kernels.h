@@ -5,7 +5,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-struct sg_item { int32_t seq, q0; };  // one attention work item: 32 query rows of a sequence
+// One unit of per-sequence work: attention workgroup (sequence, first 32-row
+// chunk) or V^T split tile (sequence, first key).
+struct sg_item { int32_t seq, c0; };
 
 namespace sgk {
 
@@ -43,9 +45,12 @@ hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s);
 // RMSNorm rows in the reference's order; amax (optional) collects per-sequence max|y|.
 hipError_t rmsnorm(float* dst, const float* src, const float* w, int rows, int n, float eps,
                    const int32_t* row_seq, float* amax, hipStream_t s);
-// QK-norm + RoPE, in place; head_dim 256.
+// QK-norm + RoPE; head_dim 256.  In place (fp32) when qs_h is null, else
+// written as the attention operands: hi/lo fp16 of x * kAttnQKScale into
+// qs_h/qs_l [T][ldqs] and ks_h/ks_l [T][ldks] (q and k are only read).
 hipError_t qknorm_rope(float* q, int ldq, float* k, int ldk, const float* qw, const float* kw, int H, int HKV,
                        int T, const int32_t* row_pos, const float* cos_t, const float* sin_t, float eps,
+                       _Float16* qs_h, _Float16* qs_l, int ldqs, _Float16* ks_h, _Float16* ks_l, int ldks,
                        hipStream_t s);
 // h = RMSNorm(o; w_post) + h ; xn = RMSNorm(h; w_next) ; amax (optional) per sequence of max|xn|.
 hipError_t post_res_norm(const float* o, float* h, const float* w_post, const float* w_next, float eps, int T,
@@ -67,8 +72,22 @@ hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float
                    float* Y, int32_t* sums, int M, int N, int K, hipStream_t s);
 
 // ---- attention (k_attention.hip) ----
-hipError_t attention(const float* q, int ldq, const float* k, const float* v, int ldkv, float* out, int ldo,
-                     const int32_t* seq_off, const sg_item* items, int n_items, int H, int HKV, int hd,
-                     float scale, float* amax, hipStream_t s);
+constexpr float kAttnQKScale = 8.0f;  // Q and K are split after scaling by 8 (exact)
+constexpr int kAttnChunks = 4;        // 32-row (head, query) chunks per attention workgroup
+// Columns of V^T a sequence of S keys occupies (whole 32-key tiles).
+inline int attn_key_pad(int S) { return (S + 31) / 32 * 32; }
+// V fp32 [T][ldv] -> V^T hi/lo fp16 [HKV*256][ldvt] (sequence s at column voff[s],
+// keys permuted within 32-key tiles, zero past S); vtiles: (seq, key0) per 32 keys.
+hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles,
+                     int n_vtiles, int HKV, _Float16* vth, _Float16* vtl, int ldvt, hipStream_t s);
+// rows x cols of x -> hi/lo fp16 of x*scale (row stride ldo).
+hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, _Float16* hi, _Float16* lo, int ldo,
+                      hipStream_t s);
+// out[T][ldo] = attention over the split operands; items: (seq, first chunk)
+// per workgroup, chunk c of a sequence = (head c / ceil(S/32), rows 32*(c % ceil(S/32))).
+hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
+                     const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo, const int32_t* seq_off,
+                     const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
+                     float* amax, hipStream_t s);
 
 }  // namespace sgk

@@ -51,11 +51,15 @@ def _check_envelope(got, oracle_model, toks, off, dim, tag, threads=16):
     env = [_stats(refs[n], refs["vnni"]) for n in REF_ORDERS]
     e_mad = np.max([e[0] for e in env], axis=0)
     e_dc = np.max([e[1] for e in env], axis=0)
-    say(f"{tag}: gpu-vs-vnni max-abs max {g_mad.max():.2e} med {np.median(g_mad):.2e} 1-cos max {g_dc.max():.2e} | "
-        f"reference spread max-abs max {e_mad.max():.2e} med {np.median(e_mad):.2e} 1-cos max {e_dc.max():.2e}")
+    say(f"{tag}: gpu-vs-vnni max-abs max {g_mad.max():.2e} mean {g_mad.mean():.2e} 1-cos max {g_dc.max():.2e} "
+        f"mean {g_dc.mean():.2e} | reference spread max-abs max {e_mad.max():.2e} mean {e_mad.mean():.2e} "
+        f"1-cos max {e_dc.max():.2e} mean {e_dc.mean():.2e}")
+    # The spread comes from int8 re-quantization flips, whose number per
+    # sequence is random; a systematic error would sit far above these bounds.
     assert g_mad.max() <= 2.0 * e_mad.max() + 1e-4
-    assert np.median(g_mad) <= 2.0 * np.median(e_mad) + 1e-4
-    assert g_dc.max() <= 3.0 * e_dc.max() + 1e-6
+    assert g_mad.mean() <= 2.0 * e_mad.mean() + 1e-4
+    assert g_dc.max() <= 4.0 * e_dc.max() + 1e-6
+    assert g_dc.mean() <= 3.0 * e_dc.mean() + 1e-6
     assert g_dc.max() <= 1e-3
     assert np.allclose(np.sum(np.asarray(got, np.float64) ** 2, axis=1), 1.0, atol=1e-5)
 
@@ -118,7 +122,8 @@ def test_layer_taps_vs_oracle(full_gpu, full_oracle):
 
 def test_tiny_forward_envelope(tiny_gpu, tiny_model, oracle):
     from semantica_gpu import synth
-    lens = [1, 7, 32, 33, 128, 300]
+    # edge lengths (1, partial and exact 32-row tiles) plus 18 seeded ragged ones
+    lens = [1, 7, 32, 33, 128, 300] + [int(x) for x in synth.lengths_log_uniform(18, 2, 300, seed=11)]
     off = synth.offsets_from_lengths(lens)
     toks = synth.token_ids(int(off[-1]), tiny_model.config["vocab_size"], seed=7)
     say(f"tiny forward lens={lens}")
