@@ -7,7 +7,9 @@ sequences, token IDs already resident in HBM, embeddings left in HBM.
 `value` is embeddings/sec over the K timed steps.  `roofline` is the Q8_0
 GEMM (the dominant kernel class): algorithmic int8 ops (2*M*N*K per launch)
 over the HIP-event time of those launches inside the timed region, against
-MI355X's dense int8 peak.  `cpu_baseline` is the CPU oracle (a restatement
+MI355X's dense int8 peak.  `traffic` is read from profiles/gemm_traffic.json (FETCH_SIZE and
+WRITE_SIZE counter passes, scaled by a copy kernel of known size).
+`cpu_baseline` is the CPU oracle (a restatement
 of the reference's Go path; the reference itself cannot run here) timed on
 this host on a bounded sample of the same workload.
 """
@@ -124,6 +126,12 @@ def main():
             k["GB_s"] = round(p["work"] / (p["ms"] * 1e-3) / 1e9, 1)
         kernels[name] = k
 
+    traffic = None  # HBM bytes per GEMM launch from the committed rocprofv3 counter passes
+    tp = os.path.join(ROOT, "profiles", "gemm_traffic.json")
+    if os.path.exists(tp):
+        with open(tp) as f:
+            traffic = json.load(f)["traffic_bytes_per_launch"]
+
     line = {
         "metric": METRIC,
         "value": round(B * a.steps / dt, 2),
@@ -141,7 +149,7 @@ def main():
                    "batch": B, "seq_len": S, "tokens": "U[2,262144) seed 0",
                    "weights": "random Q8_0 (int8 U[-127,127], fp16 |N(0,1e-3)|) seed 5; norms U[0.5,1.5] seed 2"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS,
-                     "unit": "TFLOP/s", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                     "unit": "TFLOP/s", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": traffic,
                      "kernel": "k_gemm_q8 (all Q8_0 GEMM launches; int8 TOP/s)",
                      "avg_launch_ms": round(g["ms"] / max(g["launches"], 1), 4)},
         "kernels": kernels,
