@@ -353,12 +353,22 @@ __global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8_lds(const _Float16*
 // double-buffered LDS ring and read by all NW waves.  Operand traffic is
 // split between the L1 path (A, 32 MAC per byte for TN = 2) and the LDS path
 // (W, 16*TM MAC per byte), instead of all of it going through one.
-template <int NW, int TM, int TN>
+// GELU: the FFN's gate/up GEMM with GELUQuickSIMD * up in the epilogue
+// (model_int8.go:520-535).  W holds gate and up rows interleaved in groups
+// of 32 (rows 64j..64j+31 = gate 32j.., rows 64j+32.. = up 32j..), so the
+// two 32-column subtiles of a wave are gate and up of the same features.
+// Each value is rounded exactly as the unfused path rounds it (gate and up
+// stored as acc * row_scale, then k_gelu_mul's arithmetic), so Y = g [M][N/2]
+// is bit-identical; the sequences' max|g| is folded into amax (row_seq).
+template <int NW, int TM, int TN, bool GELU>
 __global__ __launch_bounds__(NW* SG_WAVE) void k_gemm_q8_sp(const _Float16* __restrict__ A, int a_rows,
                                                             const _Float16* __restrict__ W,
                                                             const float* __restrict__ St,
                                                             const float* __restrict__ row_scale,
-                                                            float* __restrict__ Y, int M, int N, int K) {
+                                                            float* __restrict__ Y, int M, int N, int K,
+                                                            const int32_t* __restrict__ row_seq,
+                                                            float* __restrict__ amax) {
+  static_assert(!GELU || TN == 2, "the fused GELU epilogue pairs one gate and one up subtile");
   constexpr int NT = NW * SG_WAVE;
   constexpr int BN = TN * 32, BMW = TM * 32;
   constexpr int W_V = BN * 32 / 4;  // 8-byte pieces of the W tile (BN rows x 32 halfs)
@@ -482,35 +492,76 @@ __global__ __launch_bounds__(NW* SG_WAVE) void k_gemm_q8_sp(const _Float16* __re
     __syncthreads();
   }
 
+  if constexpr (GELU) {
+    __shared__ float red[NW];
+    const int Nh = N >> 1, col = (n0 >> 1) + lr;
+    const int r_first = by * NW * BMW, r_last = min(r_first + NW * BMW, M) - 1;
+    const bool one_seq = amax && row_seq[r_first] == row_seq[r_last];  // workgroup-uniform
+    float mx = 0.0f;
 #pragma unroll
-  for (int tm = 0; tm < TM; tm++) {
-    const int mb = mw + tm * 32;
-    float rs[16];
+    for (int tm = 0; tm < TM; tm++) {
+      const int mb = mw + tm * 32;
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
-      rs[r] = row_scale[row < M ? row : M - 1];
+      for (int r = 0; r < 16; r++) {
+        const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+        const float rsr = row_scale[row < M ? row : M - 1];
+        const float gate = acc[tm][0][r] * rsr, up = acc[tm][1][r] * rsr;
+        const float g = sg_gelu_quick(gate) * up;
+        const bool ok = row < M && col < Nh;
+        if (ok) Y[(int64_t)row * Nh + col] = g;
+        float a = ok ? fabsf(g) : 0.0f;
+        if (one_seq) {
+          mx = fmaxf(mx, a);
+        } else if (amax) {  // rows of several sequences: one maximum per row
+#pragma unroll
+          for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
+          if (lr == 0 && row < M) sg_atomic_max_nonneg(amax + row_seq[row], a);
+        }
+      }
     }
+    if (one_seq) {
+      mx = sg_wave_max(mx);
+      if (lane == 0) red[wave] = mx;
+      __syncthreads();
+      if (tid == 0) {
+        float mm = red[0];
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+        for (int i = 1; i < NW; i++) mm = fmaxf(mm, red[i]);
+        sg_atomic_max_nonneg(amax + row_seq[r_first], mm);
+      }
+    }
+  } else {
 #pragma unroll
-      for (int tn = 0; tn < TN; tn++) {
-        const int col = n0 + tn * 32 + lr;
-        if (row < M && col < N) Y[(int64_t)row * N + col] = acc[tm][tn][r] * rs[r];
+    for (int tm = 0; tm < TM; tm++) {
+      const int mb = mw + tm * 32;
+      float rs[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+        rs[r] = row_scale[row < M ? row : M - 1];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++) {
+          const int col = n0 + tn * 32 + lr;
+          if (row < M && col < N) Y[(int64_t)row * N + col] = acc[tm][tn][r] * rs[r];
+        }
       }
     }
   }
 }
 
-template <int NW, int TM, int TN>
+template <int NW, int TM, int TN, bool GELU = false>
 hipError_t launch_sp(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
-                     int M, int N, int K, hipStream_t s) {
+                     int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
   constexpr int BM = NW * TM * 32, BN = TN * 32;
   const int gm = (M + BM - 1) / BM;
   if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
   dim3 grid((N + BN - 1) / BN, gm);
-  hipLaunchKernelGGL((k_gemm_q8_sp<NW, TM, TN>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y, M, N, K);
+  hipLaunchKernelGGL((k_gemm_q8_sp<NW, TM, TN, GELU>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y, M, N,
+                     K, row_seq, amax);
   return hipGetLastError();
 }
 
@@ -552,6 +603,15 @@ hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float
   // compute units (tile sweeps on MI355X at the model's shapes).
   if (M >= 8192) return launch_sp<8, 1, 2>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   return launch<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
+}
+
+hipError_t gemm_q8_gelu(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* row_scale,
+                        float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s) {
+  if (M <= 0 || Nh <= 0) return hipSuccess;
+  if (K <= 0 || K % 32 || Nh % 32) return hipErrorInvalidValue;
+  if (amax && !row_seq) return hipErrorInvalidValue;
+  if (M >= 8192) return launch_sp<8, 1, 2, true>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
+  return launch_sp<4, 1, 2, true>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
 }
 
 }  // namespace sgk

@@ -21,14 +21,15 @@ __device__ __forceinline__ uint16_t rd_u16(const uint8_t* p) { return (uint16_t)
 // One thread per Q8_0 block: 2-byte fp16 scale + 32 int8 values
 // (GGUF Q8_0 layout; extractQ8_0Scales model_int8.go:543-569 reads the same bytes).
 __global__ void k_repack_q8_0(const uint8_t* __restrict__ raw, int rows, int cols, _Float16* __restrict__ w16,
-                              float* __restrict__ st, int ld, int row_off) {
+                              float* __restrict__ st, int ld, int row_off, int grp, int gstride) {
   const int nb = cols / 32;
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= (int64_t)rows * nb) return;
   const int r = (int)(id / nb), b = (int)(id % nb);
+  const int dr = row_off + (r / grp) * gstride + r % grp;
   const uint8_t* blk = raw + id * 34;
-  st[(int64_t)b * ld + row_off + r] = sg_f16_ieee(rd_u16(blk));
-  _Float16* dst = w16 + ((int64_t)b * ld + row_off + r) * 32;
+  st[(int64_t)b * ld + dr] = sg_f16_ieee(rd_u16(blk));
+  _Float16* dst = w16 + ((int64_t)b * ld + dr) * 32;
 #pragma unroll
   for (int i = 0; i < 32; i += 8) {
     half8_t v;
@@ -431,10 +432,11 @@ inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1)
 namespace sgk {
 
 hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, float* st, int ld, int row_off,
-                       hipStream_t s) {
+                       int grp, int gstride, hipStream_t s) {
   const int64_t n = (int64_t)rows * (cols / 32);
+  if (grp <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(n, 256)), dim3(256), 0, s, raw, rows, cols, w16, st, ld,
-                     row_off);
+                     row_off, grp, gstride);
   return hipGetLastError();
 }
 

@@ -322,7 +322,7 @@ struct sg_model {
   float *cos_t = nullptr, *sin_t = nullptr;
   std::vector<LayerDev> layers;
   // forward workspace (grown on demand)
-  DevBuf h, xn, qkv, att, o, gu, g, a16, sx, amax, meta_d, tokens, out, err;
+  DevBuf h, xn, qkv, att, o, g, a16, sx, amax, meta_d, tokens, out, err;
   DevBuf qs, ks, vt;  // attention operands, hi/lo fp16 (Q, K row-major; V^T)
   HostBuf meta_h, io_h;
   std::mutex mu;
@@ -337,7 +337,7 @@ struct sg_model {
   }
   ~sg_model() {
     for (void* p : allocs) (void)hipFree(p);
-    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &gu, &g, &a16, &sx, &amax, &meta_d, &tokens, &out, &err, &qs, &ks, &vt})
+    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a16, &sx, &amax, &meta_d, &tokens, &out, &err, &qs, &ks, &vt})
       b->release();
     meta_h.release();
     io_h.release();
@@ -358,13 +358,14 @@ int upload_f32(sg_model* m, float** dst, const float* src, int n) {
 
 // Copies one raw Q8_0 matrix through `stage` and repacks it into rows
 // [row_off, row_off+rows) of w16 / columns of st.
+// grp/gstride: row grouping of repack_q8_0 (0: rows stay contiguous).
 int upload_q8(const void* raw, int rows, int cols, DevBuf& stage, _Float16* w16, float* st, int ld_st, int row_off,
-              hipStream_t s) {
+              hipStream_t s, int grp = 0, int gstride = 0) {
   if (!raw) return fail(SG_ERR_INVALID, "missing Q8_0 tensor");
   const size_t bytes = (size_t)rows * (cols / 32) * 34;
   SG_TRY(stage.ensure(bytes));
   SG_HIP(hipMemcpyAsync(stage.p, raw, bytes, hipMemcpyHostToDevice, s));
-  SG_HIP(sgk::repack_q8_0(stage.as<uint8_t>(), rows, cols, w16, st, ld_st, row_off, s));
+  SG_HIP(sgk::repack_q8_0(stage.as<uint8_t>(), rows, cols, w16, st, ld_st, row_off, grp ? grp : rows, gstride, s));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;
 }
@@ -415,7 +416,6 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
   float* qkv = m->qkv.as<float>();
   float* att = m->att.as<float>();
   float* o = m->o.as<float>();
-  float* gu = m->gu.as<float>();
   float* g = m->g.as<float>();
   _Float16* a16 = m->a16.as<_Float16>();
   const int ar = sgk::gemm_pad_rows(T);
@@ -461,9 +461,8 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
     SG_LAUNCH(SG_K_NORM, t * d * 16.0,
               sgk::post_res_norm(o, h, ly.post_attn, ly.ffn_norm, eps, T, d, xn, meta.row_seq, site(l, 2), s));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 2), a16, ar, nullptr, sx, s));
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(2 * ff, d), sgk::gemm_q8(a16, ar, ly.wgu, ly.sgu, sx, gu, nullptr, T, 2 * ff, d, s));
-    SG_LAUNCH(SG_K_GELU, t * ff * 12.0,
-              sgk::gelu_mul(g, ff, gu, 2 * ff, gu + ff, 2 * ff, T, ff, meta.row_seq, site(l, 3), s));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(2 * ff, d),
+              sgk::gemm_q8_gelu(a16, ar, ly.wgu, ly.sgu, sx, g, T, ff, d, meta.row_seq, site(l, 3), s));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(ff), sgk::quantize(g, ff, T, ff, meta.row_seq, site(l, 3), a16, ar, nullptr, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), sgk::gemm_q8(a16, ar, ly.wd, ly.sd, sx, o, nullptr, T, d, ff, s));
     const bool last = l + 1 == L;
@@ -506,7 +505,6 @@ int ensure_workspace(sg_model* m, int T, int n_seq, int Tp) {
   SG_TRY(m->qkv.ensure(sizeof(float) * t * m->nqkv));
   SG_TRY(m->att.ensure(sizeof(float) * t * m->qd));
   SG_TRY(m->o.ensure(sizeof(float) * t * c.embed_dim));
-  SG_TRY(m->gu.ensure(sizeof(float) * t * 2 * c.interm_dim));
   SG_TRY(m->g.ensure(sizeof(float) * t * c.interm_dim));
   SG_TRY(m->a16.ensure(sizeof(_Float16) * (size_t)sgk::gemm_pad_rows(T) * a_cols));
   SG_TRY(m->sx.ensure(sizeof(float) * t));
@@ -636,8 +634,10 @@ int sg_model_load(sg_ctx* ctx, const sg_model_desc* desc, sg_model** out) {
         (r = upload_q8(ld.attn_k, kvd, d, stage, ly.wqkv, ly.sqkv, nqkv, qd, s)) ||
         (r = upload_q8(ld.attn_v, kvd, d, stage, ly.wqkv, ly.sqkv, nqkv, qd + kvd, s)) ||
         (r = upload_q8(ld.attn_output, d, qd, stage, ly.wo, ly.so, d, 0, s)) ||
-        (r = upload_q8(ld.ffn_gate, ff, d, stage, ly.wgu, ly.sgu, 2 * ff, 0, s)) ||
-        (r = upload_q8(ld.ffn_up, ff, d, stage, ly.wgu, ly.sgu, 2 * ff, ff, s)) ||
+        // gate and up interleaved in groups of 32 rows for the fused GELU GEMM
+        (r = upload_q8(ld.ffn_gate, ff, d, stage, ly.wgu, ly.sgu, 2 * ff, 0, s, sgk::kGeluGroup, 2 * sgk::kGeluGroup)) ||
+        (r = upload_q8(ld.ffn_up, ff, d, stage, ly.wgu, ly.sgu, 2 * ff, sgk::kGeluGroup, s, sgk::kGeluGroup,
+                       2 * sgk::kGeluGroup)) ||
         (r = upload_q8(ld.ffn_down, d, ff, stage, ly.wd, ly.sd, d, 0, s)))
       return done(r);
     if (!ld.attn_norm || !ld.ffn_norm) return done(fail(SG_ERR_INVALID, "layer %d: attn_norm/ffn_norm required", l));
@@ -816,6 +816,37 @@ int sg_matmul_q8_0_int8(sg_ctx* ctx, float* dst, const sg_q8_weight* w, const in
 
 int sg_q8_block_sums(sg_ctx* ctx, int32_t* out, const sg_q8_weight* w, const int8_t* x, int32_t batch, void* stream) {
   return matmul_common(ctx, nullptr, out, w, x, nullptr, batch, stream);
+}
+
+int sg_ffn_gate_up(sg_ctx* ctx, float* dst, const sg_q8_weight* w_gate, const sg_q8_weight* w_up, const int8_t* x,
+                   const float* row_scale, int32_t batch, void* stream) {
+  if (!ctx || !dst || !w_gate || !w_up || !x || !row_scale) return fail(SG_ERR_INVALID, "NULL argument");
+  if (w_gate->N != w_up->N || w_gate->K != w_up->K || w_gate->N % sgk::kGeluGroup)
+    return fail(SG_ERR_INVALID, "gate and up must have the same shape, out_dim a multiple of 32");
+  if (batch < 0) return fail(SG_ERR_INVALID, "batch < 0");
+  if (batch == 0) return SG_OK;
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  SG_TRY(set_device(ctx));
+  hipStream_t s = pick(ctx, stream);
+  const int N = w_gate->N, K = w_gate->K, ar = sgk::gemm_pad_rows(batch);
+  // Interleave gate and up rows in groups of 32 (the model does this at load).
+  // Block-major [K/32][N][32]: each 32-row group of one block is one 2-KB
+  // chunk (128 B of scales), and chunks of gate and up alternate.
+  const size_t wch = (size_t)sgk::kGeluGroup * 32 * sizeof(_Float16), sch = sgk::kGeluGroup * sizeof(float);
+  const size_t nch = (size_t)(K / 32) * (N / sgk::kGeluGroup);
+  SG_TRY(ctx->split.ensure(2 * nch * (wch + sch)));
+  uint8_t* wi = ctx->split.as<uint8_t>();
+  uint8_t* si = wi + 2 * nch * wch;
+  SG_HIP(hipMemcpy2DAsync(wi, 2 * wch, w_gate->w, wch, wch, nch, hipMemcpyDeviceToDevice, s));
+  SG_HIP(hipMemcpy2DAsync(wi + wch, 2 * wch, w_up->w, wch, wch, nch, hipMemcpyDeviceToDevice, s));
+  SG_HIP(hipMemcpy2DAsync(si, 2 * sch, w_gate->st, sch, sch, nch, hipMemcpyDeviceToDevice, s));
+  SG_HIP(hipMemcpy2DAsync(si + sch, 2 * sch, w_up->st, sch, sch, nch, hipMemcpyDeviceToDevice, s));
+  SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)ar * K));
+  SG_HIP(sgk::i8_to_f16_blocked(x, batch, K, ctx->f16.as<_Float16>(), ar, s));
+  SG_HIP(sgk::gemm_q8_gelu(ctx->f16.as<_Float16>(), ar, reinterpret_cast<const _Float16*>(wi),
+                           reinterpret_cast<const float*>(si), row_scale, dst, batch, N, K, nullptr, nullptr, s));
+  SG_HIP(hipStreamSynchronize(s));
+  return SG_OK;
 }
 
 int sg_rmsnorm(sg_ctx* ctx, float* dst, const float* src, const float* weight, int32_t rows, int32_t n, float eps,

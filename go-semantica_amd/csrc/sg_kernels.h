@@ -19,10 +19,11 @@ inline int gemm_pad_rows(int M) { return (M + kGemmRowPad - 1) / kGemmRowPad * k
 
 // ---- load-time repack (k_rows.hip) ----
 // Raw Q8_0 rows [rows][cols/32][34 B] -> block-major fp16 integer weights
-// w16[b][row_off + r][32] (ld rows per block) and fp32 block scales (IEEE
-// converter) st[b][row_off + r] (ld per block).
+// w16[b][dst(r)][32] (ld rows per block) and fp32 block scales (IEEE
+// converter) st[b][dst(r)] (ld per block), dst(r) = row_off + (r / grp) * gstride
+// + r % grp (grp = rows, gstride = 0: plain row_off + r).
 hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, float* st, int ld, int row_off,
-                       hipStream_t s);
+                       int grp, int gstride, hipStream_t s);
 // token_embd: int8 values q[v][d] and per-block scales (gguf halving converter) sc[v][d/32].
 hipError_t repack_embd(const uint8_t* raw, int vocab, int d, int8_t* q, float* sc, hipStream_t s);
 // int8 x[M][K] -> block-major fp16 y[K/32][a_rows][32].
@@ -70,6 +71,15 @@ hipError_t embed_only(const int32_t* tokens, int T, const int8_t* eq, const floa
 // St [K/32][N].
 hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* row_scale,
                    float* Y, int32_t* sums, int M, int N, int K, hipStream_t s);
+// FFN gate/up GEMM with GELUQuick(gate) * up in the epilogue: W holds 2*Nh rows,
+// gate and up interleaved in groups of 32 (see repack_q8_0's grouping);
+// G[M][Nh] is bit-identical to the unfused GEMMs + gelu_mul; amax (optional,
+// with row_seq) collects the sequences' max|g|.
+hipError_t gemm_q8_gelu(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* row_scale,
+                        float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s);
+// Gate/up interleaving used by gemm_q8_gelu: source row r of a matrix goes to
+// row row_off + (r / 32) * 64 + r % 32 (gate: row_off 0, up: row_off 32).
+constexpr int kGeluGroup = 32;
 
 // ---- attention (k_attention.hip) ----
 constexpr float kAttnQKScale = 8.0f;  // Q and K are split after scaling by 8 (exact)

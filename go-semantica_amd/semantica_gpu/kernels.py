@@ -74,6 +74,13 @@ def matmul_q8_0(ctx, dst, w: Q8Weight, x, row_scale, stream=None):
                                            _stream(stream)))
 
 
+def ffn_gate_up(ctx, dst, w_gate: Q8Weight, w_up: Q8Weight, x, row_scale, stream=None):
+    """geluquick(x @ w_gate) * (x @ w_up) in one GEMM (model_int8.go:520-535)."""
+    _check_dev(dst, x, row_scale)
+    _lib.check(ctx.lib.sg_ffn_gate_up(ctx.handle, _vp(dst), w_gate.handle, w_up.handle, _vp(x), _vp(row_scale),
+                                      x.shape[0], _stream(stream)))
+
+
 def block_sums(ctx, out, w: Q8Weight, x, stream=None):
     _check_dev(out, x)
     _lib.check(ctx.lib.sg_q8_block_sums(ctx.handle, _vp(out), w.handle, _vp(x), x.shape[0], _stream(stream)))

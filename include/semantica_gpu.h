@@ -173,6 +173,15 @@ int sg_matmul_q8_0_int8(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const in
 int sg_q8_block_sums(sg_ctx *ctx, int32_t *out, const sg_q8_weight *w, const int8_t *x,
                      int32_t batch, void *stream);
 
+/* The FFN's first half as one GEMM (model_int8.go:520-535: MatMulQ8_0INT8 with
+ * ffn_gate and with ffn_up, GELUQuickSIMD on the gate output, VecMulF32 by up):
+ * dst[b][n] = geluquick(gate[b][n]) * up[b][n], where gate and up are exactly
+ * what sg_matmul_q8_0_int8 returns for w_gate and w_up (same shapes, out_dim a
+ * multiple of 32); bit-identical to those two calls followed by
+ * sg_gelu_quick_mul. */
+int sg_ffn_gate_up(sg_ctx *ctx, float *dst, const sg_q8_weight *w_gate, const sg_q8_weight *w_up,
+                   const int8_t *x, const float *row_scale, int32_t batch, void *stream);
+
 /* RMSNorm per row (internal/kernels/norm.go:8-36), AVX2 8-lane order.
  * dst may equal src.  n must be a multiple of 8. */
 int sg_rmsnorm(sg_ctx *ctx, float *dst, const float *src, const float *weight,

@@ -75,6 +75,39 @@ def test_gemm_fp32_config1(gpu_ctx, oracle, N, K):
     assert rel_err(got, avx2) <= 1e-5
 
 
+@pytest.mark.parametrize("M", [1, 33, 2048, 8200])
+def test_ffn_gate_up_fused_bit_exact(gpu_ctx, oracle, M):
+    """The fused gate/up GEMM with GELUQuick * up in its epilogue equals the
+    unfused GEMMs followed by the GELU kernel bit for bit, and the first rows
+    equal the oracle's block-serial GEMMs + geluquick * up."""
+    import torch
+    from semantica_gpu import kernels, synth
+    N, K = 1152, 768
+    rng = np.random.default_rng(M)
+    say(f"ffn gate/up fused M={M} N={N} K={K}")
+    raw_g, raw_u = synth.q8_0_random(rng, N, K), synth.q8_0_random(rng, N, K)
+    xq = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    rs = rng.uniform(1e-3, 2e-2, M).astype(np.float32)
+    wg, wu = kernels.Q8Weight(gpu_ctx, raw_g, N, K), kernels.Q8Weight(gpu_ctx, raw_u, N, K)
+    gate = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    up = torch.empty_like(gate)
+    ref = torch.empty_like(gate)
+    got = torch.empty_like(gate)
+    kernels.matmul_q8_0(gpu_ctx, gate, wg, dev(xq), dev(rs))
+    kernels.matmul_q8_0(gpu_ctx, up, wu, dev(xq), dev(rs))
+    kernels.gelu_quick_mul(gpu_ctx, ref, gate, up)
+    kernels.ffn_gate_up(gpu_ctx, got, wg, wu, dev(xq), dev(rs))
+    wg.close()
+    wu.close()
+    g_host, r_host = host(got), host(ref)
+    assert np.array_equal(g_host.view(np.uint32), r_host.view(np.uint32))
+    m = min(M, 64)
+    og = oracle.matmul(raw_g, xq[:m], rs[:m], N, oracle.ORDER_BLOCK_SERIAL)
+    ou = oracle.matmul(raw_u, xq[:m], rs[:m], N, oracle.ORDER_BLOCK_SERIAL)
+    want = oracle.gelu_quick(og) * ou
+    assert np.array_equal(g_host[:m].view(np.uint32), want.view(np.uint32))
+
+
 def test_gemm_ragged_m_and_extremes(gpu_ctx, oracle):
     """M not a multiple of any tile; blocks at +-127 extremes; per-row scales."""
     import torch
