@@ -397,32 +397,52 @@ __global__ __launch_bounds__(kThreads) void k_absmax_rows(const float* __restric
 // MeanPoolingPartial (attention.go:423-445): per column, serial sum over the
 // sequence's rows then * (1/float32(S)); l2Normalize (runtime/model.go:808-820):
 // serial sum of squares, norm = float32(sqrt(float64(ss))), v /= norm.
-__global__ __launch_bounds__(kThreads) void k_pool_l2(float* __restrict__ out, const float* __restrict__ x, int ldx,
-                                                      int out_dim, const int32_t* __restrict__ seq_off) {
-  __shared__ float pooled[1024];
-  __shared__ float nrm;
-  const int sq = blockIdx.x;
+// MeanPoolingPartial (attention.go:423-445): p[c] = (sum_s x[s][c]) * (1/S),
+// the sum running over s in order for each column.  A workgroup owns 64
+// columns of one sequence; 64-row slabs are staged through LDS by all 256
+// threads (coalesced, many loads in flight), then 64 threads extend their
+// column's serial sum.  Writes the unnormalized means to out.
+constexpr int kPoolCols = 64, kPoolRows = 64;
+__global__ __launch_bounds__(kThreads) void k_pool_mean(float* __restrict__ out, const float* __restrict__ x, int ldx,
+                                                        int out_dim, const int32_t* __restrict__ seq_off) {
+  __shared__ float tile[kPoolRows][kPoolCols + 1];
+  const int sq = blockIdx.x, c0 = blockIdx.y * kPoolCols;
   const int r0 = seq_off[sq], S = seq_off[sq + 1] - r0;
-  const float sc = 1.0f / (float)S;
-  for (int c = threadIdx.x; c < out_dim; c += kThreads) {
-    float acc = 0.0f;
-    const float* p = x + (int64_t)r0 * ldx + c;
-    for (int s = 0; s < S; s++) acc = acc + p[(int64_t)s * ldx];
-    pooled[c] = acc * sc;
+  const int lc = threadIdx.x % kPoolCols, rq = threadIdx.x / kPoolCols;  // rq: 0..3
+  const int c = min(c0 + lc, out_dim - 1);
+  float acc = 0.0f;
+  for (int s0 = 0; s0 < S; s0 += kPoolRows) {
+    const int n = min(kPoolRows, S - s0);
+#pragma unroll
+    for (int i = 0; i < kPoolRows / 4; i++) {
+      const int rr = rq * (kPoolRows / 4) + i;
+      tile[rr][lc] = x[(int64_t)(r0 + s0 + min(rr, n - 1)) * ldx + c];
+    }
+    __syncthreads();
+    if (rq == 0)
+      for (int i = 0; i < n; i++) acc = acc + tile[i][lc];
+    __syncthreads();
   }
-  __syncthreads();
+  if (rq == 0 && c0 + lc < out_dim) out[(int64_t)sq * out_dim + c0 + lc] = acc * (1.0f / (float)S);
+}
+
+// l2Normalize (runtime/model.go:808-820) of each pooled row in place: serial
+// fp32 sum of squares, n = sqrt, v / n; an all-zero row is left as is.
+__global__ __launch_bounds__(kThreads) void k_l2_rows(float* __restrict__ out, int out_dim) {
+  __shared__ float nrm;
+  float* v = out + (int64_t)blockIdx.x * out_dim;
   if (threadIdx.x == 0) {
     float ss = 0.0f;
     for (int c = 0; c < out_dim; c++) {
-      const float t = pooled[c] * pooled[c];
+      const float t = v[c] * v[c];
       ss = ss + t;
     }
     nrm = ss == 0.0f ? 0.0f : sg_sqrt(ss);
   }
   __syncthreads();
   const float n = nrm;
-  for (int c = threadIdx.x; c < out_dim; c += kThreads)
-    out[(int64_t)sq * out_dim + c] = n == 0.0f ? pooled[c] : pooled[c] / n;
+  if (n != 0.0f)
+    for (int c = threadIdx.x; c < out_dim; c += kThreads) v[c] = v[c] / n;
 }
 
 inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
@@ -551,7 +571,9 @@ hipError_t pool_l2(float* out, const float* x, int ldx, int out_dim, const int32
                    hipStream_t s) {
   if (n_seq <= 0) return hipSuccess;
   if (out_dim > 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_pool_l2, dim3(n_seq), dim3(kThreads), 0, s, out, x, ldx, out_dim, seq_off);
+  hipLaunchKernelGGL(k_pool_mean, dim3(n_seq, blocks_for(out_dim, kPoolCols)), dim3(kThreads), 0, s, out, x, ldx,
+                     out_dim, seq_off);
+  hipLaunchKernelGGL(k_l2_rows, dim3(n_seq), dim3(kThreads), 0, s, out, out_dim);
   return hipGetLastError();
 }
 
