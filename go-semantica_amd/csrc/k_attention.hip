@@ -147,6 +147,8 @@ __global__ __launch_bounds__(kWaves * SG_WAVE, 1) void k_attn(
   auto key_of = [&](int kt, int r) { return kt + 8 * (r >> 2) + 4 * h + (r & 3); };
 
   // ---- pass 1: row max ----
+  // Max of the raw (x64) scores; scaling by the power of two sscale commutes
+  // with max exactly.  Keys past S only occur in a sequence's last tile.
   float m = -INFINITY;
   load_k(0);
   for (int kt = 0; kt < S; kt += kBK) {
@@ -156,12 +158,16 @@ __global__ __launch_bounds__(kWaves * SG_WAVE, 1) void k_attn(
     if (kt + kBK < S) load_k(kt + kBK);  // in flight during the MFMAs
     if (active) {
       const f32x16_t acc = scores();
+      if (kt + kBK <= S) {
 #pragma unroll
-      for (int r = 0; r < 16; r++)
-        if (key_of(kt, r) < S) m = fmaxf(m, acc[r] * sscale);
+        for (int r = 0; r < 16; r++) m = fmaxf(m, acc[r]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; r++) m = key_of(kt, r) < S ? fmaxf(m, acc[r]) : m;
+      }
     }
   }
-  m = fmaxf(m, __shfl_xor(m, 32));
+  m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
 
   // ---- pass 2: e = fastExp(s - m), row sums, O^T += V^T P^T ----
   f32x16_t o[kHD / 32];
@@ -177,9 +183,11 @@ __global__ __launch_bounds__(kWaves * SG_WAVE, 1) void k_attn(
     half8_t ph[2], pl[2];
     if (active) {
       const f32x16_t acc = scores();
+      const bool full = kt + kBK <= S;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const float e = key_of(kt, r) < S ? sg_fast_exp(acc[r] * sscale - m) : 0.0f;
+        float e = sg_fast_exp_nonpos(acc[r] * sscale - m);
+        if (!full) e = key_of(kt, r) < S ? e : 0.0f;
         lsum = lsum + e;
         const hl16 p = split_f16(e * kPScale);
         ph[r >> 3][r & 7] = p.hi;
