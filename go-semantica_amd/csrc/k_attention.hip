@@ -29,15 +29,16 @@
 // k_v_split_t writes V^T hi/lo), so every workgroup only copies fp16 tiles.
 //
 // Work split.  The G query heads that share a kv head are stacked into
-// G*ceil(S/32) chunks of 32 (head, query) rows.  A workgroup is 4 waves, one
-// chunk each, one wave per SIMD; all four stream the same 32-key K and V^T
-// tiles through LDS.  A wave holds its chunk's Q^T (split, 128 VGPRs) and its
-// O^T accumulators (256 dims x 32 queries, 128 AGPRs) for the whole run.
-// Scores are computed transposed, S^T = K Q^T on v_mfma_f32_32x32x16_f16: a
-// lane owns one query and 16 keys of the tile, so row max and row sum are
-// lane-local plus one exchange, and those 16 registers are exactly the B
-// operand of O^T += V^T P^T once V^T's keys are stored in the matching order
-// (k_v_split_t swaps the middle two 4-key groups of every 16 keys).
+// G*ceil(S/16) chunks of 16 (head, query) rows.  A workgroup is 8 waves, one
+// chunk each, two waves per SIMD (so one wave's softmax VALU overlaps the
+// other's MFMAs); all eight stream the same 32-key K and V^T tiles through
+// LDS.  A wave holds its chunk's Q^T (split, 64 VGPRs) and its O^T
+// accumulators (256 dims x 16 queries, 64 VGPRs) for the whole run.  Scores
+// are computed transposed, S^T = K Q^T on v_mfma_f32_16x16x32_f16: a lane owns
+// one query and 8 keys of the tile, so row max and row sum are lane-local
+// plus two exchanges, and those 8 registers are exactly the B operand of
+// O^T += V^T P^T (one 32-key MFMA step) once V^T's keys are stored in the
+// matching order (vt_pos; k_v_split_t writes that order).
 #include "sg_device.h"
 #include "sg_kernels.h"
 
@@ -45,22 +46,26 @@ namespace {
 
 constexpr int kHD = 256;            // head_dim
 constexpr int kBK = 32;             // keys per tile
-constexpr int kWaves = 4;           // chunks (waves) per workgroup
+constexpr int kQW = 16;             // (head, query) rows per wave
+constexpr int kWaves = sgk::kAttnChunks;
+constexpr int kNT = kWaves * SG_WAVE;
 constexpr int kKStride = kHD + 8;   // LDS K row, halves (conflict-free 16-B reads)
 constexpr int kVStride = kBK + 8;   // LDS V^T row, halves
 constexpr float kQKScale = sgk::kAttnQKScale;
 constexpr float kPScale = 1024.0f, kPUnscale = 1.0f / 1024.0f;
+static_assert(sgk::kAttnChunkRows == kQW, "host chunking must match the kernel");
 
-__device__ __forceinline__ f32x16_t mfma32(half8_t a, half8_t b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x4_t mfma16(half8_t a, half8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Position of key k (0..31) inside a V^T tile row: bits 2 and 3 swapped, so
-// that lane half h reads keys {4h..4h+3, 8+4h..8+4h+3} (+16 for the second
-// 16-key step) as 8 contiguous halves -- the keys its S^T registers hold.
-__device__ __forceinline__ int vt_pos(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
+// Position of key k (0..31) inside a V^T tile row.  Lane group g (lane/16)
+// holds the S^T entries of keys 4g..4g+3 (first 16-key subtile) and
+// 16+4g..16+4g+3 (second); as the B operand of a 32-key MFMA step its slots
+// are k = 8g..8g+7, so V^T stores key k at 8*((k&15)>>2) + 4*(k>>4) + (k&3).
+__device__ __forceinline__ int vt_pos(int k) { return ((k & 12) << 1) | ((k & 16) >> 2) | (k & 3); }
 
-__global__ __launch_bounds__(kWaves * SG_WAVE, 1) void k_attn(
+__global__ __launch_bounds__(kNT, 2) void k_attn(
     const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
     const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vth, const _Float16* __restrict__ vtl,
     int ldvt, float* __restrict__ out, int ldo, const int32_t* __restrict__ seq_off,
@@ -76,75 +81,75 @@ __global__ __launch_bounds__(kWaves * SG_WAVE, 1) void k_attn(
   const int S = seq_off[it.seq + 1] - r0;
   const int vo = voff[it.seq];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int ln = lane & 31, h = lane >> 5;
-  const int nqb = (S + 31) >> 5;
+  const int ln = lane & 15, g4 = lane >> 4;
+  const int nqb = (S + kQW - 1) / kQW;
   const int c = it.c0 + w;
   const bool active = c < G * nqb;  // wave-uniform
-  const int g = active ? c / nqb : 0;
-  const int q0 = active ? (c % nqb) * 32 : 0;
-  const int head = kvh * G + g;
+  const int hg = active ? c / nqb : 0;
+  const int q0 = active ? (c % nqb) * kQW : 0;
+  const int head = kvh * G + hg;
   const int qrow = q0 + ln;
   const bool qvalid = active && qrow < S;
 
-  // Q^T as the B operand: lane (query ln, half h), k-step ks: dims 16ks+8h..+8.
-  half8_t bqh[kHD / 16], bql[kHD / 16];
+  // Q^T as the B operand: lane (query ln, group g4), k-step c: dims 32c+8g4..+8.
+  half8_t bqh[kHD / 32], bql[kHD / 32];
   {
-    const int64_t qo = (int64_t)(r0 + min(qrow, S - 1)) * ldq + head * kHD + 8 * h;
+    const int64_t qo = (int64_t)(r0 + min(qrow, S - 1)) * ldq + head * kHD + 8 * g4;
 #pragma unroll
-    for (int ks = 0; ks < kHD / 16; ks++) {
-      bqh[ks] = *reinterpret_cast<const half8_t*>(qh + qo + 16 * ks);
-      bql[ks] = *reinterpret_cast<const half8_t*>(ql + qo + 16 * ks);
+    for (int ks = 0; ks < kHD / 32; ks++) {
+      bqh[ks] = *reinterpret_cast<const half8_t*>(qh + qo + 32 * ks);
+      bql[ks] = *reinterpret_cast<const half8_t*>(ql + qo + 32 * ks);
     }
   }
 
-  // Tile staging through registers: 2048 16-B chunks per tile, 8 per thread.
-  // K chunk u: hi/lo u>>2, key (tid>>5) + 8(u&3), dims 8(tid&31)..+8.
-  // V^T chunk u: hi/lo u>>2, dim (tid>>2) + 64(u&3), keys 8(tid&3)..+8.
-  half8_t stg[8];
+  // Tile staging through registers: 2048 16-B chunks per tile, 4 per thread.
+  // K chunk u: hi/lo u>>1, key (tid>>5) + 16(u&1), dims 8(tid&31)..+8.
+  // V^T chunk u: hi/lo u>>1, dim (tid>>2) + 128(u&1), keys 8(tid&3)..+8.
+  half8_t stg[4];
   const _Float16* kbase_h = kh + kvh * kHD + 8 * (tid & 31);
   const _Float16* kbase_l = kl + kvh * kHD + 8 * (tid & 31);
   auto load_k = [&](int kt) {
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const int key = (tid >> 5) + 8 * (u & 3);
+    for (int u = 0; u < 4; u++) {
+      const int key = (tid >> 5) + 16 * (u & 1);
       const int64_t row = r0 + min(kt + key, S - 1);
-      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 2) ? kbase_l : kbase_h) + row * ldk);
+      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 1) ? kbase_l : kbase_h) + row * ldk);
     }
   };
   auto store_k = [&]() {
 #pragma unroll
-    for (int u = 0; u < 8; u++)
-      *reinterpret_cast<half8_t*>(&Ks[u >> 2][(tid >> 5) + 8 * (u & 3)][8 * (tid & 31)]) = stg[u];
+    for (int u = 0; u < 4; u++)
+      *reinterpret_cast<half8_t*>(&Ks[u >> 1][(tid >> 5) + 16 * (u & 1)][8 * (tid & 31)]) = stg[u];
   };
   const int64_t vrow0 = (int64_t)(kvh * kHD + (tid >> 2)) * ldvt + vo + 8 * (tid & 3);
   auto load_v = [&](int kt) {
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const int64_t o = vrow0 + (int64_t)(64 * (u & 3)) * ldvt + kt;
-      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 2) ? vtl : vth) + o);
+    for (int u = 0; u < 4; u++) {
+      const int64_t o = vrow0 + (int64_t)(128 * (u & 1)) * ldvt + kt;
+      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 1) ? vtl : vth) + o);
     }
   };
   auto store_v = [&]() {
 #pragma unroll
-    for (int u = 0; u < 8; u++)
-      *reinterpret_cast<half8_t*>(&Vs[u >> 2][(tid >> 2) + 64 * (u & 3)][8 * (tid & 3)]) = stg[u];
+    for (int u = 0; u < 4; u++)
+      *reinterpret_cast<half8_t*>(&Vs[u >> 1][(tid >> 2) + 128 * (u & 1)][8 * (tid & 3)]) = stg[u];
   };
 
-  // S^T tile (32 keys x 32 queries), scaled by 64: lane holds query ln and
-  // keys 8(r/4) + 4h + r%4 of the tile in register r.
-  auto scores = [&]() {
-    f32x16_t acc = {};
+  // S^T subtile st (keys 16st..16st+15 of the tile x 16 queries), scaled by
+  // 64: lane holds query ln and keys 16st + 4g4 + r in register r.
+  auto scores = [&](int st) {
+    f32x4_t acc = {0, 0, 0, 0};
 #pragma unroll
-    for (int ks = 0; ks < kHD / 16; ks++) {
-      const half8_t ah = *reinterpret_cast<const half8_t*>(&Ks[0][ln][16 * ks + 8 * h]);
-      const half8_t al = *reinterpret_cast<const half8_t*>(&Ks[1][ln][16 * ks + 8 * h]);
-      acc = mfma32(ah, bqh[ks], acc);
-      acc = mfma32(ah, bql[ks], acc);
-      acc = mfma32(al, bqh[ks], acc);
+    for (int ks = 0; ks < kHD / 32; ks++) {
+      const half8_t ah = *reinterpret_cast<const half8_t*>(&Ks[0][16 * st + ln][32 * ks + 8 * g4]);
+      const half8_t al = *reinterpret_cast<const half8_t*>(&Ks[1][16 * st + ln][32 * ks + 8 * g4]);
+      acc = mfma16(ah, bqh[ks], acc);
+      acc = mfma16(ah, bql[ks], acc);
+      acc = mfma16(al, bqh[ks], acc);
     }
     return acc;
   };
-  auto key_of = [&](int kt, int r) { return kt + 8 * (r >> 2) + 4 * h + (r & 3); };
+  auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
 
   // ---- pass 1: row max ----
   // Max of the raw (x64) scores; scaling by the power of two sscale commutes
@@ -157,22 +162,26 @@ __global__ __launch_bounds__(kWaves * SG_WAVE, 1) void k_attn(
     __syncthreads();
     if (kt + kBK < S) load_k(kt + kBK);  // in flight during the MFMAs
     if (active) {
-      const f32x16_t acc = scores();
+      const f32x4_t a0 = scores(0), a1 = scores(1);
       if (kt + kBK <= S) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) m = fmaxf(m, acc[r]);
+        for (int r = 0; r < 4; r++) m = fmaxf(m, fmaxf(a0[r], a1[r]));
       } else {
 #pragma unroll
-        for (int r = 0; r < 16; r++) m = key_of(kt, r) < S ? fmaxf(m, acc[r]) : m;
+        for (int r = 0; r < 4; r++) {
+          m = key_of(kt, 0, r) < S ? fmaxf(m, a0[r]) : m;
+          m = key_of(kt, 1, r) < S ? fmaxf(m, a1[r]) : m;
+        }
       }
     }
   }
+  m = fmaxf(m, __shfl_xor(m, 16));
   m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
 
   // ---- pass 2: e = fastExp(s - m), row sums, O^T += V^T P^T ----
-  f32x16_t o[kHD / 32];
+  f32x4_t o[kHD / 16];
 #pragma unroll
-  for (int mt = 0; mt < kHD / 32; mt++) o[mt] = f32x16_t{};
+  for (int mt = 0; mt < kHD / 16; mt++) o[mt] = f32x4_t{0, 0, 0, 0};
   float lsum = 0.0f;
   load_k(0);
   __syncthreads();  // pass 1's last tile is consumed
@@ -180,18 +189,21 @@ __global__ __launch_bounds__(kWaves * SG_WAVE, 1) void k_attn(
   __syncthreads();
   for (int kt = 0; kt < S; kt += kBK) {
     load_v(kt);  // in flight during the score MFMAs
-    half8_t ph[2], pl[2];
+    half8_t ph, pl;  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
     if (active) {
-      const f32x16_t acc = scores();
+      const f32x4_t a0 = scores(0), a1 = scores(1);
       const bool full = kt + kBK <= S;
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        float e = sg_fast_exp_nonpos(acc[r] * sscale - m);
-        if (!full) e = key_of(kt, r) < S ? e : 0.0f;
-        lsum = lsum + e;
-        const hl16 p = split_f16(e * kPScale);
-        ph[r >> 3][r & 7] = p.hi;
-        pl[r >> 3][r & 7] = p.lo;
+      for (int st = 0; st < 2; st++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          float e = sg_fast_exp_nonpos((st ? a1[r] : a0[r]) * sscale - m);
+          if (!full) e = key_of(kt, st, r) < S ? e : 0.0f;
+          lsum = lsum + e;
+          const hl16 p = split_f16(e * kPScale);
+          ph[4 * st + r] = p.hi;
+          pl[4 * st + r] = p.lo;
+        }
       }
     }
     store_v();
@@ -200,39 +212,34 @@ __global__ __launch_bounds__(kWaves * SG_WAVE, 1) void k_attn(
     if (more) load_k(kt + kBK);  // in flight during the P.V MFMAs
     if (active) {
 #pragma unroll
-      for (int mt = 0; mt < kHD / 32; mt++) {
-#pragma unroll
-        for (int st = 0; st < 2; st++) {
-          const half8_t ah = *reinterpret_cast<const half8_t*>(&Vs[0][32 * mt + ln][16 * st + 8 * h]);
-          const half8_t al = *reinterpret_cast<const half8_t*>(&Vs[1][32 * mt + ln][16 * st + 8 * h]);
-          o[mt] = mfma32(ah, ph[st], o[mt]);
-          o[mt] = mfma32(ah, pl[st], o[mt]);
-          o[mt] = mfma32(al, ph[st], o[mt]);
-        }
+      for (int mt = 0; mt < kHD / 16; mt++) {
+        const half8_t ah = *reinterpret_cast<const half8_t*>(&Vs[0][16 * mt + ln][8 * g4]);
+        const half8_t al = *reinterpret_cast<const half8_t*>(&Vs[1][16 * mt + ln][8 * g4]);
+        o[mt] = mfma16(ah, ph, o[mt]);
+        o[mt] = mfma16(ah, pl, o[mt]);
+        o[mt] = mfma16(al, ph, o[mt]);
       }
     }
     if (more) store_k();  // nobody reads Ks between the two barriers
     __syncthreads();      // K tile staged; V^T tile free
   }
+  lsum = lsum + __shfl_xor(lsum, 16);
   lsum = lsum + __shfl_xor(lsum, 32);
   const float f = (1.0f / lsum) * kPUnscale;
 
-  // O^T tile mt: lane holds query ln, dims 32mt + 8(r/4) + 4h + r%4.
+  // O^T tile mt: lane holds query ln, dims 16mt + 4g4 + r.
   float mx = 0.0f;
   if (qvalid) {
-    float* op = out + (int64_t)(r0 + qrow) * ldo + head * kHD + 4 * h;
+    float* op = out + (int64_t)(r0 + qrow) * ldo + head * kHD + 4 * g4;
 #pragma unroll
-    for (int mt = 0; mt < kHD / 32; mt++) {
+    for (int mt = 0; mt < kHD / 16; mt++) {
+      f32x4_t y;
 #pragma unroll
-      for (int rb = 0; rb < 4; rb++) {
-        f32x4_t y;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          y[j] = o[mt][4 * rb + j] * f;
-          mx = fmaxf(mx, fabsf(y[j]));
-        }
-        *reinterpret_cast<f32x4_t*>(op + 32 * mt + 8 * rb) = y;
+      for (int j = 0; j < 4; j++) {
+        y[j] = o[mt][j] * f;
+        mx = fmaxf(mx, fabsf(y[j]));
       }
+      *reinterpret_cast<f32x4_t*>(op + 16 * mt) = y;
     }
   }
   if (amax) {  // all chunks of a workgroup belong to one sequence
@@ -334,7 +341,7 @@ hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Flo
   if (hd != kHD || HKV <= 0 || H % HKV) return hipErrorInvalidValue;
   if ((ldq | ldk | ldvt) & 7 || (ldo & 3)) return hipErrorInvalidValue;
   const float sscale = scale / (kQKScale * kQKScale);
-  hipLaunchKernelGGL(k_attn, dim3(n_items, HKV), dim3(kWaves * SG_WAVE), 0, s, qh, ql, ldq, kh, kl, ldk, vth, vtl,
+  hipLaunchKernelGGL(k_attn, dim3(n_items, HKV), dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vth, vtl,
                      ldvt, out, ldo, seq_off, voff, items, H / HKV, sscale, amax);
   return hipGetLastError();
 }

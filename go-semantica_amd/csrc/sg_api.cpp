@@ -117,8 +117,11 @@ struct Meta {
   sg_item* vtiles = nullptr; // V^T split tiles (sequence, first key)
 };
 
-// Attention workgroups of one sequence: G*ceil(S/32) chunks, kAttnChunks each.
-int seq_groups(int S, int G) { return (G * ((S + 31) / 32) + sgk::kAttnChunks - 1) / sgk::kAttnChunks; }
+// Attention workgroups of one sequence: G*ceil(S/16) chunks, kAttnChunks each.
+int seq_groups(int S, int G) {
+  const int chunks = G * ((S + sgk::kAttnChunkRows - 1) / sgk::kAttnChunkRows);
+  return (chunks + sgk::kAttnChunks - 1) / sgk::kAttnChunks;
+}
 
 // Fills `host` with [row_seq | row_pos | seq_off | voff | items | vtiles] and
 // copies it to `dev` on stream s (the copy is complete when this returns).

@@ -83,7 +83,8 @@ constexpr int kGeluGroup = 32;
 
 // ---- attention (k_attention.hip) ----
 constexpr float kAttnQKScale = 8.0f;  // Q and K are split after scaling by 8 (exact)
-constexpr int kAttnChunks = 4;        // 32-row (head, query) chunks per attention workgroup
+constexpr int kAttnChunkRows = 16;    // (head, query) rows per attention chunk (one wave)
+constexpr int kAttnChunks = 8;        // chunks per attention workgroup
 // Columns of V^T a sequence of S keys occupies (whole 32-key tiles).
 inline int attn_key_pad(int S) { return (S + 31) / 32 * 32; }
 // V fp32 [T][ldv] -> V^T hi/lo fp16 [HKV*256][ldvt] (sequence s at column voff[s],
@@ -94,7 +95,7 @@ hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int3
 hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, _Float16* hi, _Float16* lo, int ldo,
                       hipStream_t s);
 // out[T][ldo] = attention over the split operands; items: (seq, first chunk)
-// per workgroup, chunk c of a sequence = (head c / ceil(S/32), rows 32*(c % ceil(S/32))).
+// per workgroup, chunk c of a sequence = (head c / ceil(S/16), rows 16*(c % ceil(S/16))).
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
                      const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
