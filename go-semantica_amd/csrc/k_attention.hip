@@ -49,8 +49,12 @@ constexpr int kBK = 32;             // keys per tile
 constexpr int kQW = 16;             // (head, query) rows per wave
 constexpr int kWaves = sgk::kAttnChunks;
 constexpr int kNT = kWaves * SG_WAVE;
-constexpr int kKStride = kHD + 8;   // LDS K row, halves (conflict-free 16-B reads)
-constexpr int kVStride = kBK + 8;   // LDS V^T row, halves
+// LDS row strides (halves).  For 16x16x32 operand reads (16 rows x 4 lane
+// groups of 16 B per ds_read_b128) rows of 544 B and 96 B are conflict-free
+// on gfx950, while 528 B and 80 B rows cost 1.6x (measured with a one-CU
+// ds_read_b128 throughput probe).
+constexpr int kKStride = kHD + 16;
+constexpr int kVStride = kBK + 16;
 constexpr float kQKScale = sgk::kAttnQKScale;
 constexpr float kPScale = 1024.0f, kPUnscale = 1.0f / 1024.0f;
 static_assert(sgk::kAttnChunkRows == kQW, "host chunking must match the kernel");
