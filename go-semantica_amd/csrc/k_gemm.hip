@@ -353,6 +353,85 @@ __global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8_lds(const _Float16*
 // double-buffered LDS ring and read by all NW waves.  Operand traffic is
 // split between the L1 path (A, 32 MAC per byte for TN = 2) and the LDS path
 // (W, 16*TM MAC per byte), instead of all of it going through one.
+// Epilogue shared by the split-path kernels: Y = acc * row_scale (or, with
+// GELU, g = geluquick(gate) * up over the paired subtiles, with the
+// sequences' max|g| folded into amax).  Wave tile rows mw.., workgroup row
+// tile by, columns n0...
+template <int NW, int TM, int TN, bool GELU>
+__device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int mw, int by, int n0, int lr, int lh,
+                                              int lane, int wave, int tid, int M, int N,
+                                              const float* __restrict__ row_scale, float* __restrict__ Y,
+                                              const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
+  constexpr int BMW = TM * 32;
+  if constexpr (GELU) {
+    // Subtile pairs (2p, 2p+1) are gate and up of output columns
+    // (n0 / 2) + 32p + lr.
+    static_assert(TN % 2 == 0, "GELU pairs gate and up subtiles");
+    __shared__ float red[NW];
+    const int Nh = N >> 1;
+    const int r_first = by * NW * BMW, r_last = min(r_first + NW * BMW, M) - 1;
+    const bool one_seq = amax && row_seq[r_first] == row_seq[r_last];  // workgroup-uniform
+    float mx = 0.0f;
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++) {
+      const int mb = mw + tm * 32;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+        const float rsr = row_scale[row < M ? row : M - 1];
+        float a = 0.0f;
+#pragma unroll
+        for (int pr = 0; pr < TN / 2; pr++) {
+          const int col = (n0 >> 1) + 32 * pr + lr;
+          const float gate = acc[tm][2 * pr][r] * rsr, up = acc[tm][2 * pr + 1][r] * rsr;
+          const float g = sg_gelu_quick(gate) * up;
+          const bool ok = row < M && col < Nh;
+          if (ok) Y[(int64_t)row * Nh + col] = g;
+          a = ok ? fmaxf(a, fabsf(g)) : a;
+        }
+        if (one_seq) {
+          mx = fmaxf(mx, a);
+        } else if (amax) {  // rows of several sequences: one maximum per row
+#pragma unroll
+          for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
+          if (lr == 0 && row < M) sg_atomic_max_nonneg(amax + row_seq[row], a);
+        }
+      }
+    }
+    if (one_seq) {
+      mx = sg_wave_max(mx);
+      if (lane == 0) red[wave] = mx;
+      __syncthreads();
+      if (tid == 0) {
+        float mm = red[0];
+#pragma unroll
+        for (int i = 1; i < NW; i++) mm = fmaxf(mm, red[i]);
+        sg_atomic_max_nonneg(amax + row_seq[r_first], mm);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int tm = 0; tm < TM; tm++) {
+      const int mb = mw + tm * 32;
+      float rs[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+        rs[r] = row_scale[row < M ? row : M - 1];
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++) {
+          const int col = n0 + tn * 32 + lr;
+          if (row < M && col < N) Y[(int64_t)row * N + col] = acc[tm][tn][r] * rs[r];
+        }
+      }
+    }
+  }
+}
+
 // GELU: the FFN's gate/up GEMM with GELUQuickSIMD * up in the epilogue
 // (model_int8.go:520-535).  W holds gate and up rows interleaved in groups
 // of 32 (rows 64j..64j+31 = gate 32j.., rows 64j+32.. = up 32j..), so the
@@ -368,7 +447,6 @@ __global__ __launch_bounds__(NW* SG_WAVE) void k_gemm_q8_sp(const _Float16* __re
                                                             float* __restrict__ Y, int M, int N, int K,
                                                             const int32_t* __restrict__ row_seq,
                                                             float* __restrict__ amax) {
-  static_assert(!GELU || TN == 2, "the fused GELU epilogue pairs one gate and one up subtile");
   constexpr int NT = NW * SG_WAVE;
   constexpr int BN = TN * 32, BMW = TM * 32;
   constexpr int W_V = BN * 32 / 4;  // 8-byte pieces of the W tile (BN rows x 32 halfs)
@@ -492,65 +570,121 @@ __global__ __launch_bounds__(NW* SG_WAVE) void k_gemm_q8_sp(const _Float16* __re
     __syncthreads();
   }
 
-  if constexpr (GELU) {
-    __shared__ float red[NW];
-    const int Nh = N >> 1, col = (n0 >> 1) + lr;
-    const int r_first = by * NW * BMW, r_last = min(r_first + NW * BMW, M) - 1;
-    const bool one_seq = amax && row_seq[r_first] == row_seq[r_last];  // workgroup-uniform
-    float mx = 0.0f;
+  gemm_epilogue<NW, TM, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
+}
+
+// Direct-to-LDS variant.  Workgroup: 8 waves x 32 rows = 256 rows, 32*TN
+// columns.  Every K-block's A tile (each wave's own 32 rows), weight tile and
+// scales are copied global -> LDS by global_load_lds_dwordx4/dword (no
+// staging registers) into a ring of STAGES buffers, STAGES-1 blocks ahead.
+// Each wave issues exactly 4 copies per block (clamped, redundant past the
+// last block) so one constant s_waitcnt vmcnt covers "this wave's copies of
+// block b have landed"; a bare s_barrier then publishes every wave's copies.
+// (__syncthreads' fence would wait for all copies in flight.)  Rows are
+// stored in 64-byte lines with the 16-byte chunks XOR-swizzled by row, so
+// fragment reads are conflict-free; the swizzle is applied by choosing which
+// global chunk each lane copies.
+template <int TN, bool GELU, int STAGES>
+__global__ __launch_bounds__(512, 4) void k_gemm_q8_dl(const _Float16* __restrict__ A, int a_rows,
+                                                   const _Float16* __restrict__ W, const float* __restrict__ St,
+                                                   const float* __restrict__ row_scale, float* __restrict__ Y, int M,
+                                                   int N, int K, const int32_t* __restrict__ row_seq,
+                                                   float* __restrict__ amax) {
+  constexpr int NW = 8, BN = TN * 32;
+  constexpr int A_BYTES = NW * 32 * 64, W_BYTES = BN * 64, S_BYTES = BN * 4;
+  constexpr int STAGE = A_BYTES + W_BYTES + S_BYTES;
+  static_assert(STAGES >= 3 && STAGES <= 4, "wait counts below cover 3 or 4 stages");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[STAGES * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 31, lh = lane >> 5;
+  int bx, by;
+  xcd_tile(bx, by);
+  const int n0 = bx * BN;
+  const int mw = by * NW * 32 + wave * 32;
+  const int nb = K >> 5;
+  auto swz = [](int r, int c) { return c ^ ((r >> 2) & 3); };  // chunk slot of chunk c in row r
+
+  // Copy sources for this lane (block 0); block b adds b * (rows * 32) halves.
+  // A: two 1-KB copies per wave, lane -> row 16j + lane/4, slot lane%4.
+  const _Float16* asrc[2];
 #pragma unroll
-    for (int tm = 0; tm < TM; tm++) {
-      const int mb = mw + tm * 32;
+  for (int j = 0; j < 2; j++) {
+    const int r = 16 * j + (lane >> 2);
+    asrc[j] = A + (int64_t)(mw + r) * 32 + 8 * swz(r, lane & 3);
+  }
+  const int64_t a_bstride = (int64_t)a_rows * 32;
+  // W: 4*TN rows per wave (16*TN active lanes), lane -> row 4*TN*wave + lane/4.
+  constexpr int WLANES = 16 * TN;
+  const int wr = 4 * TN * wave + (lane >> 2);
+  const _Float16* wsrc = W + (int64_t)min(n0 + wr, N - 1) * 32 + 8 * swz(wr, lane & 3);
+  const int64_t w_bstride = (int64_t)N * 32;
+  // Scales: 4*TN per wave.
+  constexpr int SLANES = 4 * TN;
+  const float* ssrc = St + min(n0 + SLANES * wave + lane, N - 1);
+
+  auto issue = [&](int b, int st) {
+    unsigned char* base = lds + st * STAGE;
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
-        const float rsr = row_scale[row < M ? row : M - 1];
-        const float gate = acc[tm][0][r] * rsr, up = acc[tm][1][r] * rsr;
-        const float g = sg_gelu_quick(gate) * up;
-        const bool ok = row < M && col < Nh;
-        if (ok) Y[(int64_t)row * Nh + col] = g;
-        float a = ok ? fabsf(g) : 0.0f;
-        if (one_seq) {
-          mx = fmaxf(mx, a);
-        } else if (amax) {  // rows of several sequences: one maximum per row
+    for (int j = 0; j < 2; j++)
+      __builtin_amdgcn_global_load_lds(asrc[j] + b * a_bstride, base + wave * 2048 + j * 1024, 16, 0, 0);
+    if (lane < WLANES)
+      __builtin_amdgcn_global_load_lds(wsrc + b * w_bstride, base + A_BYTES + wave * (WLANES * 16), 16, 0, 0);
+    if (lane < SLANES)
+      __builtin_amdgcn_global_load_lds(ssrc + (int64_t)b * N, base + A_BYTES + W_BYTES + wave * (SLANES * 4), 4, 0,
+                                       0);
+  };
+
+  f32x16_t acc[1][TN];
 #pragma unroll
-          for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
-          if (lr == 0 && row < M) sg_atomic_max_nonneg(amax + row_seq[row], a);
-        }
-      }
-    }
-    if (one_seq) {
-      mx = sg_wave_max(mx);
-      if (lane == 0) red[wave] = mx;
-      __syncthreads();
-      if (tid == 0) {
-        float mm = red[0];
+  for (int tn = 0; tn < TN; tn++)
 #pragma unroll
-        for (int i = 1; i < NW; i++) mm = fmaxf(mm, red[i]);
-        sg_atomic_max_nonneg(amax + row_seq[r_first], mm);
-      }
-    }
-  } else {
+    for (int r = 0; r < 16; r++) acc[0][tn][r] = 0.0f;
+
 #pragma unroll
-    for (int tm = 0; tm < TM; tm++) {
-      const int mb = mw + tm * 32;
-      float rs[16];
+  for (int i = 0; i < STAGES - 1; i++) issue(min(i, nb - 1), i);
+  const f32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  for (int b = 0; b < nb; b++) {
+    const int st = b % STAGES;
+    if constexpr (STAGES == 3)
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(min(b + STAGES - 1, nb - 1), (b + STAGES - 1) % STAGES);
+    const unsigned char* base = lds + st * STAGE;
+    const unsigned char* arow = base + wave * 2048 + lr * 64;
+    Frag fa;
+    fa.lo = *reinterpret_cast<const half8_t*>(arow + 16 * swz(lr, 2 * lh));
+    fa.hi = *reinterpret_cast<const half8_t*>(arow + 16 * swz(lr, 2 * lh + 1));
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
-        rs[r] = row_scale[row < M ? row : M - 1];
-      }
+    for (int tn = 0; tn < TN; tn++) {
+      const int rr = 32 * tn + lr;
+      const unsigned char* wrow = base + A_BYTES + rr * 64;
+      const half8_t wlo = *reinterpret_cast<const half8_t*>(wrow + 16 * swz(rr, 2 * lh));
+      const half8_t whi = *reinterpret_cast<const half8_t*>(wrow + 16 * swz(rr, 2 * lh + 1));
+      const float d = *reinterpret_cast<const float*>(base + A_BYTES + W_BYTES + 4 * rr);
+      f32x16_t pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa.lo, wlo, zero, 0, 0, 0);
+      pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa.hi, whi, pp, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
-#pragma unroll
-        for (int tn = 0; tn < TN; tn++) {
-          const int col = n0 + tn * 32 + lr;
-          if (row < M && col < N) Y[(int64_t)row * N + col] = acc[tm][tn][r] * rs[r];
-        }
-      }
+      for (int r = 0; r < 16; r++) acc[0][tn][r] = __builtin_fmaf(pp[r], d, acc[0][tn][r]);
     }
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // redundant tail copies drained before exit
+  gemm_epilogue<NW, 1, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
+}
+
+template <int TN, bool GELU = false, int STAGES = 3>
+hipError_t launch_dl(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
+                     int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
+  constexpr int BM = 256, BN = TN * 32;
+  const int gm = (M + BM - 1) / BM;
+  if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
+  dim3 grid((N + BN - 1) / BN, gm);
+  hipLaunchKernelGGL((k_gemm_q8_dl<TN, GELU, STAGES>), grid, dim3(512), 0, s, A, a_rows, W, St, rs, Y, M, N, K,
+                     row_seq, amax);
+  return hipGetLastError();
 }
 
 template <int NW, int TM, int TN, bool GELU = false>
@@ -598,10 +732,11 @@ hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float
   if (M <= 0 || N <= 0) return hipSuccess;
   if (K <= 0 || K % 32) return hipErrorInvalidValue;
   if (sums) return launch<1, 1, 1, 1, true>(A, a_rows, W, St, row_scale, Y, sums, M, N, K, s);
-  // Large M: split-path workgroups of 8 waves (256 rows x 64 columns).
-  // Small M: 64x64 register-direct tiles so the grid still covers the 256
-  // compute units (tile sweeps on MI355X at the model's shapes).
-  if (M >= 8192) return launch_sp<8, 1, 2>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+  // Large M: direct-to-LDS workgroups of 8 waves (256 rows x 128 columns,
+  // 3-stage copy ring).  Small M: 64x64 register-direct tiles so the grid
+  // still covers the 256 compute units (tile sweeps on MI355X at the model's
+  // shapes).
+  if (M >= 8192) return launch_dl<4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   return launch<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
 }
 
@@ -610,7 +745,7 @@ hipError_t gemm_q8_gelu(const _Float16* A, int a_rows, const _Float16* W, const 
   if (M <= 0 || Nh <= 0) return hipSuccess;
   if (K <= 0 || K % 32 || Nh % 32) return hipErrorInvalidValue;
   if (amax && !row_seq) return hipErrorInvalidValue;
-  if (M >= 8192) return launch_sp<8, 1, 2, true>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
+  if (M >= 8192) return launch_dl<4, true, 3>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
   return launch_sp<4, 1, 2, true>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
 }
 

@@ -128,6 +128,29 @@ def test_gemm_ragged_m_and_extremes(gpu_ctx, oracle):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("N,K", [(1280, 768), (768, 1152)])
+def test_gemm_large_m(gpu_ctx, oracle, N, K):
+    """The large-M kernel (M >= 8192, ragged last tile): first and last rows
+    bit-exact to the block-serial order, every row within 1e-5 of AVX2's."""
+    import torch
+    from semantica_gpu import kernels, synth
+    M = 8200
+    rng = np.random.default_rng(N + K)
+    say(f"gemm large M={M} N={N} K={K}")
+    raw = synth.q8_0_random(rng, N, K)
+    xq = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    rs = rng.uniform(1e-3, 2.0, size=M).astype(np.float32)
+    w = kernels.Q8Weight(gpu_ctx, raw, N, K)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    kernels.matmul_q8_0(gpu_ctx, y, w, dev(xq), dev(rs))
+    got = host(y)
+    w.close()
+    for lo, hi in ((0, 128), (M - 128, M)):
+        ref = oracle.matmul(raw, xq[lo:hi], rs[lo:hi], N, oracle.ORDER_BLOCK_SERIAL)
+        assert np.array_equal(got[lo:hi].view(np.uint32), ref.view(np.uint32))
+    assert rel_err(got, oracle.matmul(raw, xq, rs, N, oracle.ORDER_AVX2)) <= 1e-5
+
+
 @pytest.mark.parametrize("cols", [768, 1152])
 def test_quantize_per_sequence_bit_exact(gpu_ctx, oracle, cols):
     import torch
