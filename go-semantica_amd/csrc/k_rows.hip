@@ -146,44 +146,45 @@ __global__ __launch_bounds__(kThreads) void k_embed_only(const int32_t* __restri
 // gathered into amax (one reference call quantizes one sequence):
 // scale = m/127 (fp32), inv = 1/scale (fp32),
 // q = clamp(round_half_away(float64(x)*float64(inv)), +-127); m == 0 -> scale 1, q 0.
+// One row per wave (4 rows per workgroup): the row's scale and reciprocal are
+// computed once, then the wave walks the row in coalesced float4 slots.
 template <bool F16>
 __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__ x, int ldx, int rows, int cols,
                                                        const int32_t* __restrict__ row_seq,
                                                        const float* __restrict__ amax, _Float16* __restrict__ qf,
                                                        int a_rows, int8_t* __restrict__ qi,
                                                        float* __restrict__ row_scale) {
-  const int c4n = cols >> 2;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= (int64_t)rows * c4n) return;
-  const int row = (int)(gid / c4n), c4 = (int)(gid % c4n);
+  const int row = blockIdx.x * (kThreads / SG_WAVE) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
   const float m = amax[row_seq[row]];
   float scale = 1.0f, inv = 0.0f;
   if (m != 0.0f) {
     scale = m / 127.0f;
     inv = 1.0f / scale;
   }
-  if (c4 == 0) row_scale[row] = scale;
-  const f32x4_t v = *reinterpret_cast<const f32x4_t*>(x + (int64_t)row * ldx + 4 * c4);
-  int qv[4];
+  if (lane == 0) row_scale[row] = scale;
+  const double dinv = (double)inv;
+  const float* xr = x + (int64_t)row * ldx;
+  for (int c4 = lane; c4 < (cols >> 2); c4 += SG_WAVE) {
+    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(xr + 4 * c4);
+    int qv[4];
 #pragma unroll
-  for (int t = 0; t < 4; t++) {
-    int q = 0;
-    if (m != 0.0f) {
-      q = (int)round((double)v[t] * (double)inv);
-      q = q > 127 ? 127 : (q < -127 ? -127 : q);
+    for (int t = 0; t < 4; t++) {
+      int q = (int)round((double)v[t] * dinv);  // m == 0: inv == 0 gives 0
+      qv[t] = q > 127 ? 127 : (q < -127 ? -127 : q);
     }
-    qv[t] = q;
-  }
-  if (F16) {  // block-major GEMM operand: [k/32][a_rows][32]
-    half4_t h;
+    if (F16) {  // block-major GEMM operand: [k/32][a_rows][32]
+      half4_t h;
 #pragma unroll
-    for (int t = 0; t < 4; t++) h[t] = (_Float16)(float)qv[t];
-    const int k = 4 * c4;
-    *reinterpret_cast<half4_t*>(qf + ((int64_t)(k >> 5) * a_rows + row) * 32 + (k & 31)) = h;
-  } else {
-    char4 c;
-    c.x = (signed char)qv[0]; c.y = (signed char)qv[1]; c.z = (signed char)qv[2]; c.w = (signed char)qv[3];
-    *reinterpret_cast<char4*>(qi + (int64_t)row * cols + 4 * c4) = c;
+      for (int t = 0; t < 4; t++) h[t] = (_Float16)(float)qv[t];
+      const int k = 4 * c4;
+      *reinterpret_cast<half4_t*>(qf + ((int64_t)(k >> 5) * a_rows + row) * 32 + (k & 31)) = h;
+    } else {
+      char4 c;
+      c.x = (signed char)qv[0]; c.y = (signed char)qv[1]; c.z = (signed char)qv[2]; c.w = (signed char)qv[3];
+      *reinterpret_cast<char4*>(qi + (int64_t)row * cols + 4 * c4) = c;
+    }
   }
 }
 
@@ -514,13 +515,13 @@ hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* 
   if (rows <= 0) return hipSuccess;
   if (cols % 4 || ldx % 4) return hipErrorInvalidValue;
   if (f16 && (cols % 32 || a_rows < rows)) return hipErrorInvalidValue;
-  const int64_t n = (int64_t)rows * (cols / 4);
+  const unsigned nblk = blocks_for(rows, kThreads / SG_WAVE);
   if (f16)
-    hipLaunchKernelGGL(k_quantize<true>, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, s, x, ldx, rows, cols,
-                       row_seq, amax, f16, a_rows, nullptr, row_scale);
+    hipLaunchKernelGGL(k_quantize<true>, dim3(nblk), dim3(kThreads), 0, s, x, ldx, rows, cols, row_seq, amax, f16,
+                       a_rows, nullptr, row_scale);
   else
-    hipLaunchKernelGGL(k_quantize<false>, dim3(blocks_for(n, kThreads)), dim3(kThreads), 0, s, x, ldx, rows, cols,
-                       row_seq, amax, nullptr, 0, i8, row_scale);
+    hipLaunchKernelGGL(k_quantize<false>, dim3(nblk), dim3(kThreads), 0, s, x, ldx, rows, cols, row_seq, amax,
+                       nullptr, 0, i8, row_scale);
   return hipGetLastError();
 }
 
