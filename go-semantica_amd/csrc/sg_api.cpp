@@ -22,12 +22,14 @@
 #include <string>
 #include <vector>
 
+#include "sg_internal.h"
 #include "sg_kernels.h"
 
 namespace {
-
 thread_local std::string g_err;
+}  // namespace
 
+namespace sgi {
 int fail(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -37,6 +39,11 @@ int fail(int code, const char* fmt, ...) {
   g_err = buf;
   return code;
 }
+}  // namespace sgi
+
+namespace {
+
+using sgi::fail;
 
 #define SG_HIP(call)                                                                                     \
   do {                                                                                                   \

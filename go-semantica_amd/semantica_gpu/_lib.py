@@ -94,6 +94,9 @@ _PROTOS = {
     "sg_abi_version": (ctypes.c_int, []),
     "sg_model_load": (ctypes.c_int, [_vp, ctypes.POINTER(ModelDesc), _pp]),
     "sg_model_free": (None, [_vp]),
+    "sg_gguf_read_config": (ctypes.c_int, [_vp, ctypes.c_size_t, ctypes.POINTER(ModelConfig)]),
+    "sg_model_load_gguf": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t, _pp]),
+    "sg_model_load_gguf_file": (ctypes.c_int, [_vp, ctypes.c_char_p, _pp]),
     "sg_forward": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "sg_forward_device": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "sg_forward_hidden": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),

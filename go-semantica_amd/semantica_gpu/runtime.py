@@ -9,6 +9,9 @@
                                                      (api.go:90-112) with token IDs in
                                                      place of texts (the tokenizer is host
                                                      code outside this library)
+  Model.from_gguf(ctx, image_or_path)             <- LoadModelFromBytes / LoadModel,
+                                                     internal/runtime/model.go:236-262
+  read_gguf_config(image)                         <- parseConfig, model.go:424-517
   resolve_dim / supported_dims                    <- ggufembed.ResolveDim / SupportedDims
                                                      (pkg/ggufembed/tasks.go:80-117)
 
@@ -93,6 +96,19 @@ def model_desc(model: SynthModel):
     return desc, keep
 
 
+_CONFIG_FIELDS = ("embed_dim", "num_layers", "num_heads", "num_kv_heads", "interm_dim", "max_seq_len",
+                  "vocab_size", "norm_eps", "rope_base")
+
+
+def read_gguf_config(image: bytes) -> dict:
+    """parseConfig (internal/runtime/model.go:424-517) over a GGUF v3 image."""
+    lib = _lib.load()
+    buf = ctypes.create_string_buffer(bytes(image), len(image))
+    cfg = _lib.ModelConfig()
+    _lib.check(lib.sg_gguf_read_config(buf, len(image), ctypes.byref(cfg)))
+    return {k: getattr(cfg, k) for k in _CONFIG_FIELDS}
+
+
 class Model:
     """Weights resident on one GPU (sg_model_load) and the batched forward."""
 
@@ -105,6 +121,28 @@ class Model:
         _lib.check(self.lib.sg_model_load(ctx.handle, ctypes.byref(desc), ctypes.byref(h)))
         del keep
         self.handle = h
+
+    @classmethod
+    def from_gguf(cls, ctx: Context, source) -> "Model":
+        """LoadModelFromBytes / LoadModel (model.go:236-262): a GGUF image (bytes)
+        or a file path (str / os.PathLike)."""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        self.lib = ctx.lib
+        h = ctypes.c_void_p()
+        if isinstance(source, (bytes, bytearray, memoryview)):
+            image = bytes(source)
+            buf = ctypes.create_string_buffer(image, len(image))
+            _lib.check(self.lib.sg_model_load_gguf(ctx.handle, buf, len(image), ctypes.byref(h)))
+            self.config = read_gguf_config(image)
+        else:
+            import os
+            path = os.fspath(source)
+            _lib.check(self.lib.sg_model_load_gguf_file(ctx.handle, path.encode(), ctypes.byref(h)))
+            with open(path, "rb") as f:
+                self.config = read_gguf_config(f.read())
+        self.handle = h
+        return self
 
     def close(self):
         if self.handle:

@@ -111,3 +111,108 @@ def lengths_log_uniform(n: int, lo: int, hi: int, seed: int) -> np.ndarray:
     """Config 4: S = round(exp(U[ln lo, ln hi]))."""
     u = np.random.default_rng(seed).uniform(np.log(lo), np.log(hi), size=n)
     return np.clip(np.round(np.exp(u)), lo, hi).astype(np.int32)
+
+
+# ---------------------------------------------------------------- GGUF images
+
+GGUF_DTYPE_F32, GGUF_DTYPE_Q8_0 = 0, 8
+_GGUF_MTYPE = {"u8": 0, "i8": 1, "u16": 2, "i16": 3, "u32": 4, "i32": 5, "f32": 6, "bool": 7, "str": 8,
+               "arr": 9, "u64": 10, "i64": 11, "f64": 12}
+_GGUF_FMT = {"u8": "<B", "i8": "<b", "u16": "<H", "i16": "<h", "u32": "<I", "i32": "<i", "f32": "<f",
+             "bool": "<?", "u64": "<Q", "i64": "<q", "f64": "<d"}
+
+
+def _gguf_str(s: str) -> bytes:
+    import struct
+    b = s.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def _gguf_value(kind: str, value) -> bytes:
+    import struct
+    if kind == "str":
+        return _gguf_str(value)
+    if kind.startswith("arr:"):
+        ek = kind[4:]
+        out = struct.pack("<IQ", _GGUF_MTYPE["arr" if ek.startswith("arr:") else ek], len(value))
+        return out + b"".join(_gguf_value(ek, v) for v in value)
+    return struct.pack(_GGUF_FMT[kind], value)
+
+
+def gguf_image(metadata: list, tensors: list, version: int = 3) -> bytes:
+    """A GGUF image in the layout internal/gguf/reader.go:98-178 reads.
+
+    metadata: [(key, kind, value)] with kind one of u8..f64, "str", "arr:<kind>".
+    tensors: [(name, dims (ne0 first), dtype, raw bytes)].  Tensor data starts
+    at the end of the infos rounded up to 32 bytes; each tensor is placed at a
+    32-byte aligned offset from there.
+    """
+    import struct
+    head = struct.pack("<IIQQ", 0x46554747, version, len(tensors), len(metadata))
+    kv = b"".join(_gguf_str(k) + struct.pack("<I", _GGUF_MTYPE["arr" if kind.startswith("arr:") else kind]) +
+                  _gguf_value(kind, v) for k, kind, v in metadata)
+    infos, blobs, off = [], [], 0
+    for name, dims, dtype, raw in tensors:
+        raw = bytes(raw)
+        infos.append(_gguf_str(name) + struct.pack("<I", len(dims)) + struct.pack(f"<{len(dims)}Q", *dims) +
+                     struct.pack("<IQ", dtype, off))
+        blobs.append(raw + b"\0" * ((-len(raw)) % 32))
+        off += len(blobs[-1])
+    body = head + kv + b"".join(infos)
+    return body + b"\0" * ((-len(body)) % 32) + b"".join(blobs)
+
+
+def model_gguf(model: SynthModel, **kw) -> bytes:
+    """model_gguf_parts assembled into one image."""
+    return gguf_image(*model_gguf_parts(model, **kw))
+
+
+def model_gguf_parts(model: SynthModel, arch: str = "gemma-embedding", norms_q8: bool = False, vocab_tokens=True,
+                     extra_metadata: list = ()):
+    """The synthetic model as a GGUF image with the tensor names and metadata keys
+    the reference loader reads (model.go:424-552, model_int8.go:54-119).  With
+    norms_q8 the norm vectors are stored as Q8_0 (scale 1/64, exact for values
+    that are multiples of 1/64 in [-1.98, 1.98])."""
+    c = model.config
+    p = arch + "."
+    md = [("general.architecture", "str", arch),
+          (p + "embedding_length", "u32", c["embed_dim"]), (p + "block_count", "u32", c["num_layers"]),
+          (p + "attention.head_count", "u32", c["num_heads"]),
+          (p + "attention.head_count_kv", "u32", c["num_kv_heads"]),
+          (p + "feed_forward_length", "u32", c["interm_dim"]), (p + "context_length", "u32", c["max_seq_len"]),
+          (p + "attention.layer_norm_rms_epsilon", "f32", c["norm_eps"]),
+          (p + "rope.freq_base", "f32", c["rope_base"])]
+    if vocab_tokens:
+        md.append(("tokenizer.ggml.tokens", "arr:str", [f"t{i}" for i in range(c["vocab_size"])]))
+    md += list(extra_metadata)
+
+    def norm(name, v):
+        v = np.asarray(v, np.float32)
+        if not norms_q8:
+            return (name, [v.size], GGUF_DTYPE_F32, v.astype("<f4").tobytes())
+        q = np.round(v * 64).astype(np.int8)
+        raw = q8_0_from_parts(np.full((1, v.size // 32), 1 / 64, np.float16), q.reshape(1, -1))
+        return (name, [v.size], GGUF_DTYPE_Q8_0, raw.tobytes())
+
+    d = c["embed_dim"]
+    ts = [("token_embd.weight", [d, c["vocab_size"]], GGUF_DTYPE_Q8_0, model.token_embd.tobytes())]
+    if model.output_norm is not None:
+        ts.append(norm("output_norm.weight", model.output_norm))
+    for i, ly in enumerate(model.layers):
+        for name in LAYER_Q8:
+            rows = ly[name].shape[0]
+            cols = ly[name].shape[1] * 32
+            ts.append((f"blk.{i}.{name}.weight", [cols, rows], GGUF_DTYPE_Q8_0, ly[name].tobytes()))
+        for name in LAYER_NORMS:
+            if ly.get(name) is not None:
+                ts.append(norm(f"blk.{i}.{name}.weight", ly[name]))
+    return md, ts
+
+
+def quantized_norms(model: SynthModel) -> SynthModel:
+    """Copy of the model whose norm vectors are multiples of 1/64 (exact in the
+    Q8_0 form model_gguf(norms_q8=True) writes)."""
+    layers = [{k: (np.round(v * 64) / 64).astype(np.float32) if k in LAYER_NORMS else v for k, v in ly.items()}
+              for ly in model.layers]
+    on = None if model.output_norm is None else (np.round(model.output_norm * 64) / 64).astype(np.float32)
+    return SynthModel(dict(model.config), model.token_embd, on, layers)

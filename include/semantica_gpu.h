@@ -13,6 +13,7 @@
 #ifndef SEMANTICA_GPU_H
 #define SEMANTICA_GPU_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -88,6 +89,23 @@ int sg_abi_version(void);
  * buffers may be freed after return (unlike the Go zero-copy views). */
 int sg_model_load(sg_ctx *ctx, const sg_model_desc *desc, sg_model **out);
 void sg_model_free(sg_model *model);
+
+/* ---- GGUF model images ---------------------------------------------------
+ * parseConfig (internal/runtime/model.go:424-517) over a GGUF v3 image
+ * (gguf/reader.go:98-178): fills *out from the metadata.  Host only; no
+ * device call. */
+int sg_gguf_read_config(const void *data, size_t size, sg_model_config *out);
+
+/* LoadModelFromBytes (model.go:250-262) for the INT8 path: parses the image,
+ * checks the tensors the forward reads (token_embd and the seven layer
+ * matrices Q8_0; attn_norm/ffn_norm F32 or Q8_0; q/k norms, post norms and
+ * output_norm optional) and calls sg_model_load.  The image may be released
+ * after return.  No tokenizer is built: the library takes token IDs. */
+int sg_model_load_gguf(sg_ctx *ctx, const void *data, size_t size, sg_model **out);
+
+/* LoadModel (model.go:236-248): the same from a file, memory-mapped for the
+ * duration of the call. */
+int sg_model_load_gguf_file(sg_ctx *ctx, const char *path, sg_model **out);
 
 /* Batched ForwardWithDim (internal/runtime/model.go:661-667 ->
  * forwardINT8WithDim model_int8.go:148-256) over n_seq packed sequences:

@@ -132,6 +132,40 @@ def test_tiny_forward_envelope(tiny_gpu, tiny_model, oracle):
         _check_envelope(tiny_gpu.forward_packed(toks, off, dim), om, toks, off, dim, f"tiny dim={dim}")
 
 
+def test_gguf_load_matches_descriptor_load(gpu_ctx, tiny_gpu, tiny_model, tmp_path):
+    """LoadModelFromBytes / LoadModel over the synthetic GGUF image give the
+    same weights as the descriptor load: embeddings identical bit for bit;
+    Q8_0-stored norms are dequantized like gguf.DequantizeQ8_0."""
+    from semantica_gpu import Model, SemanticaError, _lib, synth
+    lens = [5, 40, 1, 33]
+    off = synth.offsets_from_lengths(lens)
+    toks = synth.token_ids(int(off[-1]), tiny_model.config["vocab_size"], seed=3)
+    say("gguf load: bytes, file, Q8_0 norms, wrong dtype")
+    want = tiny_gpu.forward_packed(toks, off, 768)
+    image = synth.model_gguf(tiny_model)
+    m = Model.from_gguf(gpu_ctx, image)
+    assert m.config["vocab_size"] == 4096 and m.config["num_layers"] == 2
+    assert np.array_equal(m.forward_packed(toks, off, 768).view(np.uint32), want.view(np.uint32))
+    m.close()
+    path = tmp_path / "tiny.gguf"
+    path.write_bytes(image)
+    m = Model.from_gguf(gpu_ctx, str(path))
+    assert np.array_equal(m.forward_packed(toks, off, 768).view(np.uint32), want.view(np.uint32))
+    m.close()
+    qm = synth.quantized_norms(tiny_model)
+    a, b = Model(gpu_ctx, qm), Model.from_gguf(gpu_ctx, synth.model_gguf(qm, norms_q8=True))
+    assert np.array_equal(a.forward_packed(toks, off, 256).view(np.uint32),
+                          b.forward_packed(toks, off, 256).view(np.uint32))
+    a.close()
+    b.close()
+    md, ts = synth.model_gguf_parts(tiny_model)
+    ts = [(n, dims, 1 if n == "blk.0.attn_q.weight" else dt, raw) for n, dims, dt, raw in ts]
+    with pytest.raises(SemanticaError) as ei:
+        Model.from_gguf(gpu_ctx, synth.gguf_image(md, ts))
+    assert ei.value.code == _lib.SG_ERR_INVALID
+    assert "expected Q8_0, got F16 for blk.0.attn_q.weight" in ei.value.message
+
+
 def test_forward_errors(tiny_gpu):
     from semantica_gpu import SemanticaError, _lib
     say("forward error cases")
