@@ -336,6 +336,92 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope(float* __restrict__ q,
   }
 }
 
+// The same per-(token, head) arithmetic as k_qknorm_rope, writing the split
+// attention operands, with coalesced I/O: a wave owns 8 (token, head) rows;
+// each row (256 floats, 1 KB) is loaded by one float4 instruction into LDS,
+// read back in the 8-lane order the RMSNorm needs, and the packed hi|lo
+// results go back through LDS so every lane stores 16-byte chunks (128
+// contiguous bytes per row per instruction) instead of 2-byte scattered
+// stores.
+__global__ __launch_bounds__(kThreads) void k_qknorm_rope_split(
+    const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk, const float* __restrict__ qw,
+    const float* __restrict__ kw, int H, int HKV, int T, const int32_t* __restrict__ row_pos,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, float eps, _Float16* __restrict__ qs_h,
+    _Float16* __restrict__ qs_l, int ldqs, _Float16* __restrict__ ks_h, _Float16* __restrict__ ks_l, int ldks) {
+  constexpr int NPL = 32, HALF = 128, RS = 256 + 8;  // row stride in floats: conflict-free 8-lane reads
+  __shared__ __attribute__((aligned(16))) float tile[kThreads / SG_WAVE][8][RS];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int per = H + HKV;
+  const int64_t n_rows = (int64_t)T * per;
+  const int64_t row0 = (int64_t)blockIdx.x * kRowsPerBlock + w * 8;
+#pragma unroll
+  for (int rr = 0; rr < 8; rr++) {
+    const int64_t g = row0 + rr;
+    if (g < n_rows) {
+      const int t = (int)(g / per), hh = (int)(g % per);
+      const float* src = hh < H ? q + (int64_t)t * ldq + hh * 256 : k + (int64_t)t * ldk + (hh - H) * 256;
+      *reinterpret_cast<f32x4_t*>(&tile[w][rr][4 * lane]) = *reinterpret_cast<const f32x4_t*>(src + 4 * lane);
+    }
+  }
+  __syncthreads();
+  const int gi = lane >> 3, j = lane & 7;
+  const int64_t g = row0 + gi;
+  const bool valid = g < n_rows;
+  const int t = valid ? (int)(g / per) : 0, hh = valid ? (int)(g % per) : 0;
+  float x[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; i++) x[i] = tile[w][gi][8 * i + j];
+  const float* wn = hh < H ? qw : kw;
+  if (wn) sg_rmsnorm8<NPL>(x, wn, j, eps);
+  const int pos = row_pos[t];
+  const float* cr = cos_t + (int64_t)pos * HALF;
+  const float* sr = sin_t + (int64_t)pos * HALF;
+#pragma unroll
+  for (int i = 0; i < NPL / 2; i++) {
+    const int e = 8 * i + j;
+    const float c = cr[e], s = sr[e];
+    const float v0 = x[i], v1 = x[i + NPL / 2];
+    const float a = v0 * c, b = v1 * s, cc = v0 * s, dd = v1 * c;
+    x[i] = a - b;
+    x[i + NPL / 2] = cc + dd;
+  }
+  // Each lane overwrites exactly the slots it read, so no barrier is needed
+  // before these writes; the chunk reads below need every lane's writes.
+  uint32_t* pk = reinterpret_cast<uint32_t*>(&tile[w][gi][0]);
+#pragma unroll
+  for (int i = 0; i < NPL; i++) {
+    const hl16 sp = split_f16(x[i] * sgk::kAttnQKScale);
+    pk[8 * i + j] = (uint32_t)__builtin_bit_cast(uint16_t, sp.hi) | ((uint32_t)__builtin_bit_cast(uint16_t, sp.lo) << 16);
+  }
+  __syncthreads();
+  if (!valid) return;
+  _Float16 *dh, *dl;
+  if (hh < H) {
+    dh = qs_h + (int64_t)t * ldqs + hh * 256;
+    dl = qs_l + (int64_t)t * ldqs + hh * 256;
+  } else {
+    dh = ks_h + (int64_t)t * ldks + (hh - H) * 256;
+    dl = ks_l + (int64_t)t * ldks + (hh - H) * 256;
+  }
+#pragma unroll
+  for (int kk = 0; kk < 4; kk++) {
+    const int c = j + 8 * kk;  // chunk of elements 8c .. 8c+7
+    const uint4 a = *reinterpret_cast<const uint4*>(&pk[8 * c]);
+    const uint4 b = *reinterpret_cast<const uint4*>(&pk[8 * c + 4]);
+    const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint4 hv, lv;
+    uint32_t* hp = &hv.x;
+    uint32_t* lp = &lv.x;
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      hp[m] = (u[2 * m] & 0xffffu) | (u[2 * m + 1] << 16);
+      lp[m] = (u[2 * m] >> 16) | (u[2 * m + 1] & 0xffff0000u);
+    }
+    *reinterpret_cast<uint4*>(dh + 8 * c) = hv;
+    *reinterpret_cast<uint4*>(dl + 8 * c) = lv;
+  }
+}
+
 // ------------------------------------------------------------ GELU * up --
 
 // GELUQuickSIMD (activation.go:47-95) then VecMulF32 (matmul.go:238-259):
@@ -545,8 +631,14 @@ hipError_t qknorm_rope(float* q, int ldq, float* k, int ldk, const float* qw, co
   if (T <= 0) return hipSuccess;
   if (qs_h && (!qs_l || !ks_h || !ks_l)) return hipErrorInvalidValue;
   const int64_t groups = (int64_t)T * (H + HKV);
-  hipLaunchKernelGGL(k_qknorm_rope, dim3(blocks_for(groups, kRowsPerBlock)), dim3(kThreads), 0, s, q, ldq, k, ldk,
-                     qw, kw, H, HKV, T, row_pos, cos_t, sin_t, eps, qs_h, qs_l, ldqs, ks_h, ks_l, ldks);
+  if (qs_h) {
+    if ((ldqs | ldks) & 7) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_qknorm_rope_split, dim3(blocks_for(groups, kRowsPerBlock)), dim3(kThreads), 0, s, q, ldq, k,
+                       ldk, qw, kw, H, HKV, T, row_pos, cos_t, sin_t, eps, qs_h, qs_l, ldqs, ks_h, ks_l, ldks);
+  } else {
+    hipLaunchKernelGGL(k_qknorm_rope, dim3(blocks_for(groups, kRowsPerBlock)), dim3(kThreads), 0, s, q, ldq, k, ldk,
+                       qw, kw, H, HKV, T, row_pos, cos_t, sin_t, eps, nullptr, nullptr, 0, nullptr, nullptr, 0);
+  }
   return hipGetLastError();
 }
 
