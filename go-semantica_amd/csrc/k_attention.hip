@@ -38,7 +38,7 @@
 // one query and 8 keys of the tile, so row max and row sum are lane-local
 // plus two exchanges, and those 8 registers are exactly the B operand of
 // O^T += V^T P^T (one 32-key MFMA step) once V^T's keys are stored in the
-// matching order (vt_pos; k_v_split_t writes that order).
+// matching order (vt_key; k_v_split_t writes that order).
 #include "sg_device.h"
 #include "sg_kernels.h"
 
@@ -63,11 +63,12 @@ __device__ __forceinline__ f32x4_t mfma16(half8_t a, half8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Position of key k (0..31) inside a V^T tile row.  Lane group g (lane/16)
-// holds the S^T entries of keys 4g..4g+3 (first 16-key subtile) and
-// 16+4g..16+4g+3 (second); as the B operand of a 32-key MFMA step its slots
-// are k = 8g..8g+7, so V^T stores key k at 8*((k&15)>>2) + 4*(k>>4) + (k&3).
-__device__ __forceinline__ int vt_pos(int k) { return ((k & 12) << 1) | ((k & 16) >> 2) | (k & 3); }
+// Key order inside a V^T tile row.  Lane group g (lane/16) holds the S^T
+// entries of keys 4g..4g+3 (first 16-key subtile) and 16+4g..16+4g+3
+// (second); as the B operand of a 32-key MFMA step its slots are positions
+// 8g..8g+7, so key k is stored at position 8*((k&15)>>2) + 4*(k>>4) + (k&3)
+// and position p holds key:
+__device__ __forceinline__ int vt_key(int p) { return ((p & 4) << 2) | ((p & 24) >> 1) | (p & 3); }
 
 __global__ __launch_bounds__(kNT, 2) void k_attn(
     const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
@@ -76,7 +77,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
     const int32_t* __restrict__ voff, const sg_item* __restrict__ items, int G, float sscale,
     float* __restrict__ amax) {
   __shared__ _Float16 Ks[2][kBK][kKStride];  // [hi/lo][key][dim]
-  __shared__ _Float16 Vs[2][kHD][kVStride];  // [hi/lo][dim][key, vt_pos order]
+  __shared__ _Float16 Vs[2][kHD][kVStride];  // [hi/lo][dim][key, vt_key order]
   __shared__ float red[kWaves];
 
   const sg_item it = items[blockIdx.x];
@@ -261,13 +262,18 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
 
 // V [T][ldv] fp32 (kv head blockIdx.y at column 256*kvh) -> V^T hi/lo fp16
 // [HKV*256][ldvt]: sequence s occupies columns voff[s] .. voff[s] + 32*ceil(S/32),
-// keys in vt_pos order inside every 32-key tile, zeros past S.
+// keys in vt_key order inside every 32-key tile, zeros past S.  The 32 x 256
+// fp32 tile is loaded with coalesced float4 rows into LDS; a thread then owns
+// one (dim, 8-key chunk), reads its 8 keys down the LDS column and stores the
+// chunk's hi and lo halves as two 16-byte writes (4 threads cover one dim's
+// 64 contiguous bytes).
 __global__ __launch_bounds__(256) void k_v_split_t(const float* __restrict__ v, int ldv,
                                                    const int32_t* __restrict__ seq_off,
                                                    const int32_t* __restrict__ voff,
                                                    const sg_item* __restrict__ vtiles, _Float16* __restrict__ vth,
                                                    _Float16* __restrict__ vtl, int ldvt) {
-  __shared__ _Float16 th[2][kHD][kVStride];
+  constexpr int RS = kHD + 4;  // fp32 row stride
+  __shared__ __attribute__((aligned(16))) float tv[kBK][RS];
   const sg_item t = vtiles[blockIdx.x];
   const int kvh = blockIdx.y;
   const int r0 = seq_off[t.seq], S = seq_off[t.seq + 1] - r0, k0 = t.c0;
@@ -278,22 +284,31 @@ __global__ __launch_bounds__(256) void k_v_split_t(const float* __restrict__ v, 
     const int key = idx >> 6, d4 = idx & 63;
     f32x4_t x = {0, 0, 0, 0};
     if (k0 + key < S) x = *reinterpret_cast<const f32x4_t*>(v + (int64_t)(r0 + k0 + key) * ldv + kvh * kHD + 4 * d4);
-    const int p = vt_pos(key);
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const hl16 s = split_f16(x[j]);
-      th[0][4 * d4 + j][p] = s.hi;
-      th[1][4 * d4 + j][p] = s.lo;
-    }
+    *reinterpret_cast<f32x4_t*>(&tv[key][4 * d4]) = x;
   }
   __syncthreads();
   const int64_t col = voff[t.seq] + k0;
 #pragma unroll
-  for (int u = 0; u < 8; u++) {  // 2 x 256 rows x 4 chunks of 8 keys
-    const int idx = tid + 256 * u;
-    const int hl = idx >> 10, dim = (idx >> 2) & 255, c8 = idx & 3;
-    _Float16* dst = (hl ? vtl : vth) + (int64_t)(kvh * kHD + dim) * ldvt + col + 8 * c8;
-    *reinterpret_cast<half8_t*>(dst) = *reinterpret_cast<const half8_t*>(&th[hl][dim][8 * c8]);
+  for (int u = 0; u < 4; u++) {  // 256 dims x 4 chunks of 8 key positions
+    const int dim = (tid >> 2) + 64 * u, c = tid & 3;
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      uint32_t hb[2], lb[2];
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const int p = 8 * c + 2 * m + e;                   // position in the tile row
+        const int key = vt_key(p);
+        const hl16 sp = split_f16(tv[key][dim]);
+        hb[e] = __builtin_bit_cast(uint16_t, sp.hi);
+        lb[e] = __builtin_bit_cast(uint16_t, sp.lo);
+      }
+      hw[m] = hb[0] | (hb[1] << 16);
+      lw[m] = lb[0] | (lb[1] << 16);
+    }
+    const int64_t o = (int64_t)(kvh * kHD + dim) * ldvt + col + 8 * c;
+    *reinterpret_cast<uint4*>(vth + o) = uint4{hw[0], hw[1], hw[2], hw[3]};
+    *reinterpret_cast<uint4*>(vtl + o) = uint4{lw[0], lw[1], lw[2], lw[3]};
   }
 }
 
