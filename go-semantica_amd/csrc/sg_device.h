@@ -46,18 +46,15 @@ __device__ __forceinline__ float sg_fast_exp_nonpos(float x) {
 }
 
 // GELUQuickSIMD element, activation.go:55-75: x * sigmoid(1.702 x) with the
-// sign-split sigmoid.
+// sign-split sigmoid: sx >= 0 -> 1/(1 + fastExp(-sx)), else e/(1 + e) with
+// e = fastExp(sx).  Both branches evaluate fastExp at -|sx| and differ only
+// in the numerator, so one exp and one (IEEE) division give the same bits
+// without divergent branches.
 __device__ __forceinline__ float sg_gelu_quick(float x) {
   const float sx = 1.702f * x;
-  float sig;
-  if (sx >= 0.0f) {
-    const float e = sg_fast_exp(-sx);
-    sig = 1.0f / (1.0f + e);
-  } else {
-    const float e = sg_fast_exp(sx);
-    sig = e / (1.0f + e);
-  }
-  return x * sig;
+  const float e = sg_fast_exp_nonpos(-fabsf(sx));
+  const float num = sx >= 0.0f ? 1.0f : e;
+  return x * (num / (1.0f + e));
 }
 
 // fp16 -> fp32 with subnormal support, internal/runtime/model_int8.go:571-597.
