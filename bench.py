@@ -126,6 +126,20 @@ def main():
             k["GB_s"] = round(p["work"] / (p["ms"] * 1e-3) / 1e9, 1)
         kernels[name] = k
 
+    # Algorithmic HBM bytes of one step's GEMMs (fp16 A, fp16 W, fp32 block scales,
+    # fp32 row scales, fp32 output; the gate/up GEMM writes only g = geluquick(gate)*up).
+    c = mdl.config
+    d, ff, T = c["embed_dim"], c["interm_dim"], B * S
+    hd = d // c["num_heads"]
+    qd, kvd = c["num_heads"] * hd, c["num_kv_heads"] * hd
+
+    def gemm_bytes(N, K, out_cols):
+        return T * K * 2 + N * K * 2 + N * (K // 32) * 4 + T * 4 + T * out_cols * 4
+
+    step_gemm_bytes = c["num_layers"] * (gemm_bytes(qd + 2 * kvd, d, qd + 2 * kvd) + gemm_bytes(d, qd, d) +
+                                          gemm_bytes(2 * ff, d, ff) + gemm_bytes(d, ff, d))
+    gemm_gbs = step_gemm_bytes * a.steps / (g["ms"] * 1e-3) / 1e9 if g["ms"] > 0 else 0.0
+
     traffic = None  # HBM bytes per GEMM launch from the committed rocprofv3 counter passes
     tp = os.path.join(ROOT, "profiles", "gemm_traffic.json")
     if os.path.exists(tp):
@@ -150,8 +164,11 @@ def main():
                    "weights": "random Q8_0 (int8 U[-127,127], fp16 |N(0,1e-3)|) seed 5; norms U[0.5,1.5] seed 2"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": traffic,
-                     "kernel": "k_gemm_q8 (all Q8_0 GEMM launches; int8 TOP/s)",
-                     "avg_launch_ms": round(g["ms"] / max(g["launches"], 1), 4)},
+                     "kernel": "k_gemm_q8_dl (all Q8_0 GEMM launches; int8 TOP/s)",
+                     "avg_launch_ms": round(g["ms"] / max(g["launches"], 1), 4),
+                     "algorithmic_bytes_per_launch": round(step_gemm_bytes * a.steps / max(g["launches"], 1)),
+                     "hbm_view": {"achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                  "frac": round(gemm_gbs / HBM_PEAK_GBS, 4)}},
         "kernels": kernels,
         "gemm_frac_of_step": round(g["ms"] / (dt * 1e3), 3),
     }
