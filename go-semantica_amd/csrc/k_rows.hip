@@ -145,7 +145,8 @@ __global__ __launch_bounds__(kThreads) void k_embed_only(const int32_t* __restri
 // quantize.go:29-103 with the tensor max replaced by the per-sequence max
 // gathered into amax (one reference call quantizes one sequence):
 // scale = m/127 (fp32), inv = 1/scale (fp32),
-// q = clamp(round_half_away(float64(x)*float64(inv)), +-127); m == 0 -> scale 1, q 0.
+// q = clamp(round_half_away(float64(x)*float64(inv)), +-127) (sg_round_prod);
+// m == 0 -> scale 1, q 0.
 // One row per wave (4 rows per workgroup): the row's scale and reciprocal are
 // computed once, then the wave walks the row in coalesced float4 slots.
 template <bool F16>
@@ -164,14 +165,13 @@ __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__
     inv = 1.0f / scale;
   }
   if (lane == 0) row_scale[row] = scale;
-  const double dinv = (double)inv;
   const float* xr = x + (int64_t)row * ldx;
   for (int c4 = lane; c4 < (cols >> 2); c4 += SG_WAVE) {
     const f32x4_t v = *reinterpret_cast<const f32x4_t*>(xr + 4 * c4);
     int qv[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
-      int q = (int)round((double)v[t] * dinv);  // m == 0: inv == 0 gives 0
+      int q = sg_round_prod(v[t], inv);  // m == 0: inv == 0 gives 0
       qv[t] = q > 127 ? 127 : (q < -127 ? -127 : q);
     }
     if (F16) {  // block-major GEMM operand: [k/32][a_rows][32]

@@ -163,6 +163,24 @@ __device__ __forceinline__ void sg_block_seq_max(float m, bool owner, int row, i
   }
 }
 
+// math.Round(float64(x) * float64(inv)) (quantize.go:67,95) without float64
+// arithmetic: the product of two floats is exact in float64, and here it is
+// carried exactly as hi + lo (hi = fl(x*inv), lo = fma(x, inv, -hi)).
+// roundf(hi) rounds half away from zero, like math.Round, and is the answer
+// unless hi sits exactly on a half while lo moves the true product off it
+// towards the other neighbour.  hi - q0 is exact (Sterbenz), |lo| is far
+// below a half.  Half the registers of the float64 form, and no float64 ops.
+__device__ __forceinline__ int sg_round_prod(float x, float inv) {
+  const float hi = x * inv;
+  const float lo = __builtin_fmaf(x, inv, -hi);
+  const float q0 = roundf(hi);
+  const float f = hi - q0;
+  float q = q0;
+  q = (f == 0.5f && lo > 0.0f) ? q + 1.0f : q;
+  q = (f == -0.5f && lo < 0.0f) ? q - 1.0f : q;
+  return (int)q;
+}
+
 // RMSNorm of one row held by an 8-lane group, internal/kernels/norm.go:8-36.
 // Lane j of the group holds x[i] = row[8*i + j] (NPL = n/8 values): that is
 // exactly lane j of dotProductAVX2Asm's YMM accumulator, which runs

@@ -174,6 +174,56 @@ def test_quantize_per_sequence_bit_exact(gpu_ctx, oracle, cols):
         assert np.array_equal(qg[off[i]:off[i + 1]], qo), i
 
 
+def _near_ties(m):
+    """Values x (|x| < m) whose float32 product with the kernel's inv =
+    1/(m/127) lands exactly on k + 1/2, while the exact product (what the
+    reference's float64 multiply gives) sits on, above or below that half:
+    the cases where rounding the float32 product alone would go wrong."""
+    inv = np.float32(1) / (np.float32(m) / np.float32(127))
+    xs, lo_sign = [], []
+    for k in range(-127, 127):
+        x0 = np.float32((k + 0.5) / np.float64(inv))
+        for d in range(-6, 7):
+            x = (np.array([x0]).view(np.int32) + d).view(np.float32)[0]
+            p = np.float64(x) * np.float64(inv)  # exact
+            hi = np.float32(p)
+            if np.float64(hi) == k + 0.5 and abs(x) < m:
+                xs.append(x)
+                lo_sign.append(np.sign(p - np.float64(hi)))
+    return np.array(xs, np.float32), np.array(lo_sign)
+
+
+def test_quantize_near_ties_bit_exact(gpu_ctx, oracle):
+    """Round-half-away of the exact product x*inv, on the inputs where a
+    float32 product rounds onto a half: one sequence per max value m."""
+    import torch
+    from semantica_gpu import kernels
+    cols = 64
+    rows, signs = [], []
+    for m in (127.0, 63.5, 254.0, 1.0, 3.7, 50.3, 126.9, 0.0123, 1e-3):  # first three: exact ties
+        xs, sg = _near_ties(m)
+        signs.append(sg)
+        n = -(-(len(xs) + 1) // cols) * cols
+        v = np.zeros(n, np.float32)
+        v[0] = m
+        v[1:len(xs) + 1] = xs
+        rows.append(v.reshape(-1, cols))
+    signs = np.concatenate(signs)
+    assert (signs > 0).sum() > 50 and (signs < 0).sum() > 50 and (signs == 0).sum() > 50
+    lens = [len(r) for r in rows]
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    x = np.concatenate(rows)
+    say(f"quantize near ties: {len(signs)} values over {len(lens)} sequences")
+    q = torch.empty(x.shape, dtype=torch.int8, device="cuda")
+    sc = torch.empty(len(lens), dtype=torch.float32, device="cuda")
+    kernels.quantize_symmetric_int8(gpu_ctx, dev(x), off, q, sc)
+    qg, sgp = host(q), host(sc)
+    for i in range(len(lens)):
+        qo, so = oracle.quantize(x[off[i]:off[i + 1]])
+        assert sgp[i] == so, i
+        assert np.array_equal(qg[off[i]:off[i + 1]], qo), i
+
+
 @pytest.mark.parametrize("n", [256, 768])
 def test_rmsnorm_bit_exact(gpu_ctx, oracle, n):
     import torch
