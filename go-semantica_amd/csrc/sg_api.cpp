@@ -45,70 +45,8 @@ namespace {
 
 using sgi::fail;
 
-#define SG_HIP(call)                                                                                     \
-  do {                                                                                                   \
-    hipError_t e_ = (call);                                                                              \
-    if (e_ != hipSuccess)                                                                                \
-      return fail(e_ == hipErrorInvalidValue ? SG_ERR_INVALID : SG_ERR_DEVICE, "%s: %s (%s:%d)", #call,  \
-                  hipGetErrorString(e_), __FILE__, __LINE__);                                            \
-  } while (0)
-
-#define SG_TRY(expr)        \
-  do {                      \
-    int r_ = (expr);        \
-    if (r_ != SG_OK) return r_; \
-  } while (0)
-
-// Grow-only device buffer.
-struct DevBuf {
-  void* p = nullptr;
-  size_t n = 0;
-  template <typename T>
-  T* as() const { return static_cast<T*>(p); }
-  int ensure(size_t bytes) {
-    if (bytes <= n) return SG_OK;
-    if (p) (void)hipFree(p);
-    p = nullptr;
-    n = 0;
-    if (bytes == 0) return SG_OK;
-    if (hipMalloc(&p, bytes) != hipSuccess) {
-      p = nullptr;
-      return fail(SG_ERR_NOMEM, "hipMalloc(%zu bytes) failed", bytes);
-    }
-    n = bytes;
-    return SG_OK;
-  }
-  void release() {
-    if (p) (void)hipFree(p);
-    p = nullptr;
-    n = 0;
-  }
-};
-
-// Grow-only pinned host buffer (staging for metadata / small copies).
-struct HostBuf {
-  void* p = nullptr;
-  size_t n = 0;
-  template <typename T>
-  T* as() const { return static_cast<T*>(p); }
-  int ensure(size_t bytes) {
-    if (bytes <= n) return SG_OK;
-    if (p) (void)hipHostFree(p);
-    p = nullptr;
-    n = 0;
-    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
-      p = nullptr;
-      return fail(SG_ERR_NOMEM, "hipHostMalloc(%zu bytes) failed", bytes);
-    }
-    n = bytes;
-    return SG_OK;
-  }
-  void release() {
-    if (p) (void)hipHostFree(p);
-    p = nullptr;
-    n = 0;
-  }
-};
+using sgi::DevBuf;
+using sgi::HostBuf;
 
 // Per-call sequence metadata built on the host from CSR offsets.
 struct Meta {
@@ -255,6 +193,13 @@ struct sg_ctx {
   HostBuf meta_h;
   DevBuf meta_d, f16, amax, tab, split;
 };
+
+namespace sgi {
+int ctx_device(const sg_ctx* c) { return c->device; }
+hipStream_t ctx_stream(const sg_ctx* c, void* stream) {
+  return stream ? static_cast<hipStream_t>(stream) : c->stream;
+}
+}  // namespace sgi
 
 struct sg_q8_weight {
   sg_ctx* ctx = nullptr;

@@ -1,8 +1,83 @@
 // sg_internal.h -- helpers shared by the library's host translation units.
 #pragma once
 
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+#include "semantica_gpu.h"
+
 namespace sgi {
 // Records a printf-style message for sg_last_error() (thread-local) and
 // returns `code`.
 __attribute__((visibility("hidden"))) int fail(int code, const char* fmt, ...);
+
+// sg_ctx accessors (the struct lives in sg_api.cpp): device ordinal, and the
+// stream a call runs on (the caller's, or the context's own when NULL).
+__attribute__((visibility("hidden"))) int ctx_device(const sg_ctx* c);
+__attribute__((visibility("hidden"))) hipStream_t ctx_stream(const sg_ctx* c, void* stream);
+
+// Grow-only device buffer.
+struct DevBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  template <typename T>
+  T* as() const { return static_cast<T*>(p); }
+  int ensure(size_t bytes) {
+    if (bytes <= n) return SG_OK;
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+    if (bytes == 0) return SG_OK;
+    if (hipMalloc(&p, bytes) != hipSuccess) {
+      p = nullptr;
+      return fail(SG_ERR_NOMEM, "hipMalloc(%zu bytes) failed", bytes);
+    }
+    n = bytes;
+    return SG_OK;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+};
+
+// Grow-only pinned host buffer (staging for metadata / small copies).
+struct HostBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  template <typename T>
+  T* as() const { return static_cast<T*>(p); }
+  int ensure(size_t bytes) {
+    if (bytes <= n) return SG_OK;
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    n = 0;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+      p = nullptr;
+      return fail(SG_ERR_NOMEM, "hipHostMalloc(%zu bytes) failed", bytes);
+    }
+    n = bytes;
+    return SG_OK;
+  }
+  void release() {
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    n = 0;
+  }
+};
 }  // namespace sgi
+
+#define SG_HIP(call)                                                                                     \
+  do {                                                                                                   \
+    hipError_t e_ = (call);                                                                              \
+    if (e_ != hipSuccess)                                                                                \
+      return ::sgi::fail(e_ == hipErrorInvalidValue ? SG_ERR_INVALID : SG_ERR_DEVICE, "%s: %s (%s:%d)", #call, \
+                         hipGetErrorString(e_), __FILE__, __LINE__);                                     \
+  } while (0)
+
+#define SG_TRY(expr)            \
+  do {                          \
+    int r_ = (expr);            \
+    if (r_ != SG_OK) return r_; \
+  } while (0)

@@ -101,4 +101,28 @@ hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Flo
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
                      float* amax, hipStream_t s);
 
+// ---- brute-force search (k_search.hip) ----
+// Storage modes, the values of brute.QuantizationMode (search/brute/quant.go:8-15).
+constexpr int kBfF32 = 0, kBfI8 = 1, kBfI16 = 2;
+// Index layout: grp [dim/8][N][8] elements, tail [N][dim%8] elements.
+// Rows row0..row0+n of the index from float vectors src[n][ld]: normalized
+// (builder.go:131-141) when `normalize`, then quantized (quant.go:17-41).
+hipError_t bf_build(int mode, const float* src, int64_t ld, int n, int dim, int row0, int N, void* grp, void* tail,
+                    bool normalize, hipStream_t s);
+// builder.go:131-141 in place on n rows [n][dim].
+hipError_t bf_normalize(float* x, int n, int dim, hipStream_t s);
+// Stored rows (row-major [n][dim], as serialized) -> rows row0.. of the layout.
+hipError_t bf_relayout(int mode, const void* rows, int n, int dim, int row0, int N, void* grp, void* tail,
+                       hipStream_t s);
+// Rows row0..row0+n of the layout -> row-major [n][dim].
+hipError_t bf_unpack(int mode, const void* grp, const void* tail, int row0, int n, int dim, int N, void* rows,
+                     hipStream_t s);
+// scores[q][ld_scores] for nq normalized queries [nq][dim] against all N vectors.
+hipError_t bf_score(int mode, const void* grp, const void* tail, int N, int dim, const float* queries, int nq,
+                    float* scores, int64_t ld_scores, hipStream_t s);
+// The reference's top-k of every query's scores (k <= N): out_idx/out_dist [nq][k]
+// in arbitrary order (positions, not ids).  state: int32 [nq][8]; hist: [nq][256].
+hipError_t bf_select(const float* scores, int64_t ld_scores, int N, int nq, int k, int32_t* state, uint32_t* hist,
+                     int32_t* out_idx, float* out_dist, hipStream_t s);
+
 }  // namespace sgk

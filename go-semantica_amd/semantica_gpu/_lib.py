@@ -115,6 +115,14 @@ _PROTOS = {
     "sg_gelu_quick_mul": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _vp, _i32, _i32, _i32, _vp]),
     "sg_embed_tokens": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp]),
     "sg_pool_l2": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _i32, _vp]),
+    "sg_index_build": (ctypes.c_int, [_vp, _i32, _i32, _vp, _vp, _i32, _pp]),
+    "sg_index_build_device": (ctypes.c_int, [_vp, _i32, _i32, _vp, _vp, ctypes.c_int64, _i32, _vp, _pp]),
+    "sg_index_deserialize": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t, _pp]),
+    "sg_index_serialize": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]),
+    "sg_index_info": (ctypes.c_int, [_vp, ctypes.POINTER(_i32), ctypes.POINTER(_i32), ctypes.POINTER(_i32)]),
+    "sg_index_vector": (ctypes.c_int, [_vp, _i32, _vp]),
+    "sg_index_search": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
+    "sg_index_free": (None, [_vp]),
 }
 
 _lib = None

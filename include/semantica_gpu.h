@@ -237,6 +237,59 @@ int sg_embed_tokens(sg_model *model, float *dst, const int32_t *d_tokens, int32_
 int sg_pool_l2(sg_ctx *ctx, float *out, const float *x, int32_t ldx, int32_t out_dim,
                const int32_t *seq_offsets, int32_t n_seq, void *stream);
 
+/* ---- brute-force vector search (search/brute) ----------------------------
+ * The reference's quantized brute-force index (search/brute/index.go,
+ * builder.go, storage.go) with its vectors in HBM.  Scores are bit-identical
+ * to the reference's amd64 AVX2 dot products (quant.go:79-135,
+ * index.go:199-214, dot_amd64.s) and the top-k is the reference's streaming
+ * selection (index.go:53-147), ties included; only the batching is new: one
+ * call searches n_queries queries. */
+typedef struct sg_index sg_index;
+
+/* brute.QuantizationMode, search/brute/quant.go:8-15 */
+#define SG_BF_FLOAT32 0
+#define SG_BF_INT8 1
+#define SG_BF_INT16 2
+
+/* brute.NewBuilder(WithDimension(dim), WithQuantization(q)) + AddVector for each
+ * (ids[i], vectors[i*dim ..]) + Build (builder.go:40-128): every vector is
+ * L2-normalized (builder.go:131-141) and stored in mode q (quant.go:17-41).
+ * Host vectors.  Errors as the reference: "brute: no vectors added" (n = 0),
+ * "brute: duplicate id %d", "brute: unsupported quantization %d". */
+int sg_index_build(sg_ctx *ctx, int32_t dim, int32_t quantization, const int32_t *ids,
+                   const float *vectors, int32_t n, sg_index **out);
+
+/* Same with the vectors in device memory (row stride ld floats), e.g. the
+ * embeddings sg_forward_device left in HBM; ids stay on the host. */
+int sg_index_build_device(sg_ctx *ctx, int32_t dim, int32_t quantization, const int32_t *ids,
+                          const float *d_vectors, int64_t ld, int32_t n, void *stream, sg_index **out);
+
+/* Serializer.Deserialize (storage.go:43-45,94-153) of a "BRUT" v1 image. */
+int sg_index_deserialize(sg_ctx *ctx, const void *data, size_t size, sg_index **out);
+
+/* Serializer.Serialize (storage.go:31-41,47-91): *size receives the image
+ * size; with buf == NULL nothing else is done. */
+int sg_index_serialize(sg_index *index, void *buf, size_t cap, size_t *size);
+
+/* Index.Dimension / Count (index.go:149-153) and the storage mode. */
+int sg_index_info(const sg_index *index, int32_t *dim, int32_t *count, int32_t *quantization);
+
+/* Index.Vector (index.go:155-172): the dequantized vector stored under id;
+ * SG_ERR_INVALID when there is none (the reference returns ok = false). */
+int sg_index_vector(sg_index *index, int32_t id, float *out);
+
+/* SearchVector (normalize = 1, index.go:27-41) or SearchNormalized
+ * (normalize = 0, index.go:43-51) for n_queries queries [n_queries][dim]
+ * (host).  Query q gets n_found[q] = min(top_k, count) results in
+ * out_ids/out_dist[q*top_k ...], distance descending, ties by id ascending.
+ * top_k <= 0: "brute: topK must be positive".  One call at a time per index
+ * (a per-index mutex). */
+int sg_index_search(sg_index *index, const float *queries, int32_t n_queries, int32_t top_k,
+                    int32_t normalize, int32_t *out_ids, float *out_dist, int32_t *n_found,
+                    void *stream);
+
+void sg_index_free(sg_index *index);
+
 #ifdef __cplusplus
 }
 #endif

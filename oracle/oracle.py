@@ -70,6 +70,11 @@ def load():
         "sgo_forward_batch": (ctypes.c_int, [vp, vp, vp, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int]),
         "sgo_simd_level": (ctypes.c_int, []),
         "sgo_force_scalar": (None, [ctypes.c_int]),
+        "sgo_bf_normalize": (None, [vp, ctypes.c_int]),
+        "sgo_bf_quantize_i8": (None, [vp, ctypes.c_int, vp]),
+        "sgo_bf_quantize_i16": (None, [vp, ctypes.c_int, vp]),
+        "sgo_bf_dot": (f32, [vp, ctypes.c_int, i64, vp, ctypes.c_int]),
+        "sgo_bf_search": (ctypes.c_int, [vp, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int, vp, vp]),
     }
     for name, (res, args) in protos.items():
         fn = getattr(lib, name)
@@ -208,6 +213,56 @@ def dequant_row(raw_row: np.ndarray, n: int) -> np.ndarray:
     out = np.empty(n, np.float32)
     load().sgo_dequant_q8_0_row(_p(out), _p(raw_row), n)
     return out
+
+
+# ---- brute-force search (search/brute), sg_oracle_search.c ----------------
+BF_F32, BF_I8, BF_I16 = 0, 1, 2
+_BF_DTYPE = {BF_F32: np.float32, BF_I8: np.int8, BF_I16: np.int16}
+
+
+def bf_normalize(v: np.ndarray) -> np.ndarray:
+    """builder.go:131-141 on a copy of each row of v ([dim] or [n, dim])."""
+    out = np.array(v, np.float32, copy=True, order="C")
+    rows = out.reshape(-1, out.shape[-1])
+    for r in rows:
+        load().sgo_bf_normalize(_p(r), r.size)
+    return out
+
+
+def bf_quantize(v: np.ndarray, mode: int) -> np.ndarray:
+    """quant.go:17-41 (rows already normalized); BF_F32 returns a float32 copy."""
+    v = np.ascontiguousarray(v, np.float32)
+    if mode == BF_F32:
+        return v.copy()
+    out = np.empty(v.shape, _BF_DTYPE[mode])
+    fn = load().sgo_bf_quantize_i8 if mode == BF_I8 else load().sgo_bf_quantize_i16
+    rows_in, rows_out = v.reshape(-1, v.shape[-1]), out.reshape(-1, v.shape[-1])
+    for a, b in zip(rows_in, rows_out):
+        fn(_p(a), a.size, _p(b))
+    return out
+
+
+def bf_scores(data: np.ndarray, mode: int, query: np.ndarray) -> np.ndarray:
+    """Score of every stored row against one (normalized) query."""
+    data = np.ascontiguousarray(data, _BF_DTYPE[mode])
+    q = np.ascontiguousarray(query, np.float32)
+    n, dim = data.shape
+    lib = load()
+    return np.array([lib.sgo_bf_dot(_p(data), mode, i, _p(q), dim) for i in range(n)], np.float32)
+
+
+def bf_search(data: np.ndarray, mode: int, ids: np.ndarray, query: np.ndarray, top_k: int):
+    """searchNormalized (index.go:53-147): (ids, distances) sorted, or None for top_k <= 0."""
+    data = np.ascontiguousarray(data, _BF_DTYPE[mode])
+    ids = np.ascontiguousarray(ids, np.int32)
+    q = np.ascontiguousarray(query, np.float32)
+    n, dim = data.shape
+    out_i = np.empty(max(min(top_k, n), 1), np.int32)
+    out_d = np.empty(max(min(top_k, n), 1), np.float32)
+    r = load().sgo_bf_search(_p(data), mode, _p(ids), n, dim, _p(q), top_k, _p(out_i), _p(out_d))
+    if r < 0:
+        return None
+    return out_i[:r].copy(), out_d[:r].copy()
 
 
 class OracleModel:

@@ -126,6 +126,21 @@ int sgo_forward_batch(const sgo_model *m, const int32_t *tokens, const int32_t *
 int sgo_simd_level(void);
 void sgo_force_scalar(int on);
 
+/* Brute-force vector search (search/brute), sg_oracle_search.c.
+ * Storage modes: QuantizationMode, search/brute/quant.go:8-15. */
+enum { SGO_BF_F32 = 0, SGO_BF_I8 = 1, SGO_BF_I16 = 2 };
+void sgo_bf_normalize(float *v, int dim);                          /* builder.go:131-141 */
+void sgo_bf_quantize_i8(const float *v, int dim, int8_t *out);     /* quant.go:17-29 */
+void sgo_bf_quantize_i16(const float *v, int dim, int16_t *out);   /* quant.go:31-41 */
+float sgo_bf_dot_i8(const int8_t *vec, const float *q, int dim);   /* quant.go:79-105 */
+float sgo_bf_dot_i16(const int16_t *vec, const float *q, int dim); /* quant.go:107-135 */
+float sgo_bf_dot_f32(const float *a, const float *b, int dim);     /* index.go:199-214 */
+/* score of stored row `row` (data row-major [count][dim] in `mode`) */
+float sgo_bf_dot(const void *data, int mode, int64_t row, const float *q, int dim);
+/* searchNormalized, index.go:53-147 (query already normalized). */
+int sgo_bf_search(const void *data, int mode, const int32_t *ids, int count, int dim, const float *query,
+                  int top_k, int32_t *out_ids, float *out_dist);
+
 #ifdef __cplusplus
 }
 #endif
