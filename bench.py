@@ -42,6 +42,9 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, host CPUs)")
     ap.add_argument("--cpu-seqs", type=int, default=0, help="0: 6 x cpu threads")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-search", action="store_true", help="skip the brute-force search measurement")
+    ap.add_argument("--search-vectors", type=int, default=1_000_000)
+    ap.add_argument("--search-batch", type=int, default=64)
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="after the timed region, run a plain fp32 copy kernel (y = -x) of this many MiB "
                          "three times, so a counter run can scale FETCH_SIZE/WRITE_SIZE to bytes")
@@ -54,6 +57,8 @@ def cpu_baseline(model, toks, seq_len, threads, n_seq):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle
+    if n_seq * seq_len > toks.size:
+        raise ValueError(f"CPU sample of {n_seq} sequences exceeds the workload")
     om = oracle.OracleModel(model)
     off = np.arange(0, n_seq * seq_len + 1, seq_len, dtype=np.int32)
     sample = np.ascontiguousarray(toks[: n_seq * seq_len])
@@ -67,6 +72,91 @@ def cpu_baseline(model, toks, seq_len, threads, n_seq):
     return {"value": round(n_seq / dt, 3), "unit": "embeddings/sec", "cores": threads, "kind": "port",
             "sample": f"{n_seq} sequences x {seq_len} tokens (rows 0..{n_seq - 1} of the workload), "
                       f"C oracle, AVX2 VNNI-order GEMM, {threads} threads, {dt:.1f} s"}
+
+
+def search_leg(ctx, n, dim, batch, top_k, steps, with_cpu, gpu_events=True):
+    """Brute-force search (search/brute) on the GPU: an int8 index of n
+    random vectors (normalized and quantized on the device), queried in
+    batches of `batch` and one query at a time.  GPU time by HIP events on
+    the stream the search runs on; the host-side id mapping and final sort of
+    the k results per query are inside the wall time only."""
+    import numpy as np
+    import torch
+    from semantica_gpu import search
+    vecs = torch.empty((n, dim), device="cuda", dtype=torch.float32)
+    rng = np.random.default_rng(3)
+    for r0 in range(0, n, 65536):  # N(0,1) vectors, generated on the host in chunks
+        m = min(65536, n - r0)
+        vecs[r0:r0 + m].copy_(torch.from_numpy(rng.standard_normal((m, dim), dtype=np.float32)))
+    ids = np.arange(n, dtype=np.int32)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    idx = search.Index.from_device(ctx, ids, vecs.data_ptr(), dim, n, search.QUANTIZE_INT8)
+    build_s = time.perf_counter() - t0
+    del vecs
+    rng = np.random.default_rng(4)
+    queries = rng.standard_normal((batch, dim)).astype(np.float32)
+    st = torch.cuda.Stream()
+    out_i = np.zeros((batch, top_k), np.int32)
+    out_d = np.zeros((batch, top_k), np.float32)
+    found = np.zeros(batch, np.int32)
+    lib = idx.lib
+
+    def run(nq):
+        qv = np.ascontiguousarray(queries[:nq])
+        rc = lib.sg_index_search(idx.handle, qv.ctypes.data, nq, top_k, 1, out_i.ctypes.data, out_d.ctypes.data,
+                                 found.ctypes.data, st.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(lib.sg_last_error())
+
+    out = {}
+    for nq, reps in ((batch, steps), (1, 4 * steps)):
+        run(nq)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        if gpu_events:
+            e0.record(st)
+        for _ in range(reps):
+            run(nq)
+        if gpu_events:
+            e1.record(st)
+            e1.synchronize()
+        wall = (time.perf_counter() - w0) / reps
+        gpu_ms = e0.elapsed_time(e1) / reps if gpu_events else float("nan")
+        out[nq] = (wall, gpu_ms)
+    wall_b, gpu_b = out[batch]
+    wall_1, gpu_1 = out[1]
+    res = {
+        "workload": f"int8 index of {n} x {dim} N(0,1) vectors (seed 3; normalized + quantized on the GPU), top-{top_k}, "
+                    f"queries normalized (SearchVector)",
+        "build_s": round(build_s, 3),
+        "batch": batch,
+        "queries_per_s": round(batch / wall_b, 1),
+        "ms_per_batch": round(wall_b * 1e3, 3),
+        "gpu_ms_per_batch": round(gpu_b, 3),
+        "single_query_ms": round(wall_1 * 1e3, 3),
+        "single_query_gpu_ms": round(gpu_1, 3),
+        "single_query_index_GB_s": round(n * dim / (gpu_1 * 1e-3) / 1e9, 1),
+        "score_ops_per_query": 2 * n * dim,
+    }
+    idx.close()
+    if with_cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        m = min(n, 100_000)
+        host = np.random.default_rng(5).standard_normal((m, dim)).astype(np.float32)
+        data = oracle.bf_quantize(oracle.bf_normalize(host), oracle.BF_I8)
+        qn = oracle.bf_normalize(queries[0])
+        t0 = time.perf_counter()
+        reps = 3
+        for _ in range(reps):
+            oracle.bf_search(data, oracle.BF_I8, np.arange(m, dtype=np.int32), qn, top_k)
+        per = (time.perf_counter() - t0) / reps * (n / m)
+        res["cpu_baseline"] = {"ms_per_query": round(per * 1e3, 2), "cores": 1, "kind": "port",
+                               "sample": f"C oracle (AVX2-order restatement of searchNormalized), one thread, "
+                                         f"{m} vectors x {reps} queries, scaled to {n}"}
+    return res
 
 
 def main():
@@ -184,10 +274,13 @@ def main():
         "gemm_frac_of_step": round(g["ms"] / (dt_prof * 1e3), 3),
     }
     model.close()
+    if not a.no_search:
+        line["search"] = search_leg(ctx, a.search_vectors, 768, a.search_batch, 10, max(3, a.steps // 2),
+                                    not a.no_cpu_baseline)
     ctx.close()
     if not a.no_cpu_baseline:
         threads = a.cpu_threads or min(16, os.cpu_count() or 1)
-        line["cpu_baseline"] = cpu_baseline(mdl, toks, S, threads, a.cpu_seqs or 6 * threads)
+        line["cpu_baseline"] = cpu_baseline(mdl, toks, S, threads, min(a.cpu_seqs or 6 * threads, B))
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

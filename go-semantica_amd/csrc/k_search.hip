@@ -47,36 +47,48 @@ struct BfElem<float> {
   static constexpr bool kQuant = false;
 };
 
-// 8 consecutive stored elements -> the AVX2 loop's per-lane operand (no clamp:
-// VPMOVSX + VCVTDQ2PS take the code as it is).
+// One group of 8 stored elements as loaded (8, 16 or 32 bytes), and its
+// conversion to the AVX2 loop's per-lane operand (no clamp: VPMOVSX +
+// VCVTDQ2PS take the code as it is; then the scale multiply, rounded).
 template <typename T>
-__device__ __forceinline__ void bf_load8(const T* p, float (&v)[8]);
+struct BfRaw;
 template <>
-__device__ __forceinline__ void bf_load8<int8_t>(const int8_t* p, float (&v)[8]) {
-  const uint2 w = *reinterpret_cast<const uint2*>(p);
+struct BfRaw<int8_t> {
+  uint2 w;
+  __device__ void load(const int8_t* p) { w = *reinterpret_cast<const uint2*>(p); }
+  __device__ void get(float (&v)[8]) const {
 #pragma unroll
-  for (int l = 0; l < 4; l++) {
-    v[l] = (float)(int8_t)(w.x >> (8 * l)) * BfElem<int8_t>::inv();
-    v[4 + l] = (float)(int8_t)(w.y >> (8 * l)) * BfElem<int8_t>::inv();
+    for (int l = 0; l < 4; l++) {
+      v[l] = (float)(int8_t)(w.x >> (8 * l)) * BfElem<int8_t>::inv();
+      v[4 + l] = (float)(int8_t)(w.y >> (8 * l)) * BfElem<int8_t>::inv();
+    }
   }
-}
+};
 template <>
-__device__ __forceinline__ void bf_load8<int16_t>(const int16_t* p, float (&v)[8]) {
-  const uint4 w = *reinterpret_cast<const uint4*>(p);
-  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+struct BfRaw<int16_t> {
+  uint4 w;
+  __device__ void load(const int16_t* p) { w = *reinterpret_cast<const uint4*>(p); }
+  __device__ void get(float (&v)[8]) const {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-  for (int l = 0; l < 4; l++) {
-    v[2 * l] = (float)(int16_t)(u[l] & 0xffffu) * BfElem<int16_t>::inv();
-    v[2 * l + 1] = (float)(int16_t)(u[l] >> 16) * BfElem<int16_t>::inv();
+    for (int l = 0; l < 4; l++) {
+      v[2 * l] = (float)(int16_t)(u[l] & 0xffffu) * BfElem<int16_t>::inv();
+      v[2 * l + 1] = (float)(int16_t)(u[l] >> 16) * BfElem<int16_t>::inv();
+    }
   }
-}
+};
 template <>
-__device__ __forceinline__ void bf_load8<float>(const float* p, float (&v)[8]) {
-  const float4 a = *reinterpret_cast<const float4*>(p);
-  const float4 b = *reinterpret_cast<const float4*>(p + 4);
-  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-}
+struct BfRaw<float> {
+  float4 a, b;
+  __device__ void load(const float* p) {
+    a = *reinterpret_cast<const float4*>(p);
+    b = *reinterpret_cast<const float4*>(p + 4);
+  }
+  __device__ void get(float (&v)[8]) const {
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+};
 
 // Tail element through the lookup table of quant.go:57-77 (the most negative
 // code clamps to -127 / -32767).
@@ -135,19 +147,36 @@ __global__ __launch_bounds__(kBfThreads) void k_bf_build(const float* __restrict
 }
 
 // builder.go:131-141 in place on rows of x (the queries of SearchVector,
-// index.go:36-38); one thread per row.
-__global__ __launch_bounds__(kBfThreads) void k_bf_normalize(float* __restrict__ x, int n, int dim) {
-  const int r = blockIdx.x * kBfThreads + threadIdx.x;
-  if (r >= n) return;
-  float* v = x + (int64_t)r * dim;
+// index.go:36-38).  One wave per row: the row is staged in LDS with
+// coalesced loads, lane 0 runs the float64 sum in index order, and all lanes
+// scale.
+constexpr int kNormChunk = 1024;
+
+__global__ __launch_bounds__(64) void k_bf_normalize(float* __restrict__ x, int dim) {
+  __shared__ float buf[kNormChunk];
+  __shared__ float norm;
+  __shared__ int scale;
+  float* v = x + (int64_t)blockIdx.x * dim;
+  const int lane = threadIdx.x;
   double sum = 0.0;
-  for (int i = 0; i < dim; i++) {
-    const float sq = v[i] * v[i];
-    sum += (double)sq;
+  for (int c0 = 0; c0 < dim; c0 += kNormChunk) {
+    const int cn = min(kNormChunk, dim - c0);
+    for (int i = lane; i < cn; i += 64) buf[i] = v[c0 + i];
+    __syncthreads();
+    if (lane == 0)
+      for (int i = 0; i < cn; i++) {
+        const float sq = buf[i] * buf[i];
+        sum += (double)sq;
+      }
+    __syncthreads();
   }
-  if (sum == 0.0) return;
-  const float norm = (float)(1.0 / sqrt(sum));
-  for (int i = 0; i < dim; i++) v[i] = v[i] * norm;
+  if (lane == 0) {
+    scale = sum != 0.0;
+    norm = sum != 0.0 ? (float)(1.0 / sqrt(sum)) : 1.0f;
+  }
+  __syncthreads();
+  if (!scale) return;
+  for (int i = lane; i < dim; i += 64) v[i] = v[i] * norm;
 }
 
 // Stored rows (row-major, as serialized) -> the grouped layout, and back.
@@ -181,18 +210,23 @@ __global__ void k_bf_unpack(const T* __restrict__ grp, const T* __restrict__ tai
 // ---------------------------------------------------------------- scoring --
 
 // scores[q][n] for QB queries (rows q0.. of `queries`, already normalized)
-// against every stored vector; lane = vector.  The query values are uniform
-// across the wave and come through scalar loads.
+// against every stored vector; lane = vector.  The workgroup stages the
+// queries in LDS, kQChunk dimensions at a time, and every lane reads them by
+// broadcast; each lane issues the loads of kBfBatch groups before using them.
+constexpr int kQChunk = 256;
+// Groups loaded together per lane: 32 bytes of int8 / int16, 64 of float32.
+template <typename T>
+constexpr int kBfBatch = sizeof(T) == 1 ? 4 : 2;
+
 template <typename T, int QB>
 __global__ __launch_bounds__(kBfThreads) void k_bf_score(const T* __restrict__ grp, const T* __restrict__ tail,
                                                         int N, int dim, const float* __restrict__ queries, int q0,
                                                         int nq, float* __restrict__ scores, int64_t ld_scores) {
+  __shared__ __attribute__((aligned(16))) float qs[QB][kQChunk];
   const int n = blockIdx.x * kBfThreads + threadIdx.x;
-  if (n >= N) return;
+  const bool live = n < N;
+  const int nn = live ? n : N - 1;  // lanes past the end load a valid vector and store nothing
   const int G = dim >> 3, R = dim & 7;
-  const float* qp[QB];
-#pragma unroll
-  for (int j = 0; j < QB; j++) qp[j] = queries + (int64_t)min(q0 + j, nq - 1) * dim;
 
   float acc[QB][8];
 #pragma unroll
@@ -200,25 +234,46 @@ __global__ __launch_bounds__(kBfThreads) void k_bf_score(const T* __restrict__ g
 #pragma unroll
     for (int l = 0; l < 8; l++) acc[j][l] = 0.0f;
 
-  const T* gp = grp + (int64_t)n * 8;
+  const T* gp = grp + (int64_t)nn * 8;
   const int64_t gstride = (int64_t)N * 8;
-  for (int g = 0; g < G; g++) {
-    float v[8];
-    bf_load8<T>(gp + g * gstride, v);
+  for (int c0 = 0; c0 < 8 * G; c0 += kQChunk) {
+    const int cn = min(kQChunk, 8 * G - c0);
+    __syncthreads();  // the previous chunk's reads are done
+    for (int e = threadIdx.x; e < QB * cn; e += kBfThreads) {
+      const int j = e / cn, i = e - j * cn;
+      qs[j][i] = queries[(int64_t)min(q0 + j, nq - 1) * dim + c0 + i];
+    }
+    __syncthreads();
+    const int g0 = c0 >> 3, gn = cn >> 3;
+    for (int g = 0; g < gn; g += kBfBatch<T>) {
+      BfRaw<T> raw[kBfBatch<T>];  // all of a batch's loads in flight at once
 #pragma unroll
-    for (int j = 0; j < QB; j++) {
-      const float* x = qp[j] + 8 * g;
+      for (int u = 0; u < kBfBatch<T>; u++)
+        if (g + u < gn) raw[u].load(gp + (g0 + g + u) * gstride);
 #pragma unroll
-      for (int l = 0; l < 8; l++) {
-        if constexpr (BfElem<T>::kQuant) {
-          const float p = v[l] * x[l];
-          acc[j][l] = acc[j][l] + p;
-        } else {
-          acc[j][l] = __builtin_fmaf(v[l], x[l], acc[j][l]);
+      for (int u = 0; u < kBfBatch<T>; u++) {
+        if (g + u >= gn) break;
+        float v[8];
+        raw[u].get(v);
+#pragma unroll
+        for (int j = 0; j < QB; j++) {
+          const float4 xa = *reinterpret_cast<const float4*>(&qs[j][8 * (g + u)]);
+          const float4 xb = *reinterpret_cast<const float4*>(&qs[j][8 * (g + u) + 4]);
+          const float x[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+          for (int l = 0; l < 8; l++) {
+            if constexpr (BfElem<T>::kQuant) {
+              const float p = v[l] * x[l];
+              acc[j][l] = acc[j][l] + p;
+            } else {
+              acc[j][l] = __builtin_fmaf(v[l], x[l], acc[j][l]);
+            }
+          }
         }
       }
     }
   }
+  if (!live) return;
 
   const T* tp = tail + (int64_t)n * R;
 #pragma unroll
@@ -229,7 +284,7 @@ __global__ __launch_bounds__(kBfThreads) void k_bf_score(const T* __restrict__ g
       const float* l = acc[j];
       sum += ((l[0] + l[4]) + (l[1] + l[5])) + ((l[2] + l[6]) + (l[3] + l[7]));
     }
-    const float* x = qp[j] + 8 * G;
+    const float* x = queries + (int64_t)(q0 + j) * dim + 8 * G;
     if constexpr (BfElem<T>::kQuant) {
       float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
       int i = 0;
@@ -298,22 +353,39 @@ __global__ __launch_bounds__(kBfThreads) void k_bf_radix(const float* __restrict
   const int shift = 24 - 8 * digit;
   __syncthreads();
   const int base = blockIdx.x * kSelBlock;
+  // Scores crowd into a few bins (the top digit holds sign and exponent), so
+  // each wave adds its lanes bin by bin: one LDS atomic per distinct bin.
+  const int lane = threadIdx.x & 63;
 #pragma unroll 4
   for (int t = 0; t < kSelPerThread; t++) {
     const int i = base + t * kBfThreads + threadIdx.x;
+    int bin = -1;
     if (i < N) {
       const uint32_t k = bf_key(s[i]);
-      if ((k & mask) == prefix) atomicAdd(&h[(k >> shift) & 255u], 1u);
+      if ((k & mask) == prefix) bin = (int)((k >> shift) & 255u);
+    }
+    uint64_t todo = __ballot(bin >= 0);
+    while (todo) {
+      const int leader = __builtin_ctzll(todo);
+      const int lb = __shfl(bin, leader);
+      const uint64_t same = __ballot(bin == lb);
+      if (lane == leader) atomicAdd(&h[lb], (uint32_t)__popcll(same));
+      todo &= ~same;
     }
   }
   __syncthreads();
+  // Every value shared between workgroups here is read and written with
+  // device-scope atomics, so ordering needs no cache maintenance: each wave
+  // waits until its bin additions are performed before the workgroup counts
+  // itself done, and the last workgroup reads the bins with atomic loads.
+  // (A __threadfence() per workgroup would write back and invalidate the L2
+  // thousands of times per pass.)
   if (h[threadIdx.x]) atomicAdd(&hq[threadIdx.x], h[threadIdx.x]);
-  __threadfence();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) last = atomicAdd(&st[5], 1) == (int)gridDim.x - 1;
   __syncthreads();
   if (!last) return;
-  __threadfence();
   // suffix sums over the bins, highest first
   const uint32_t c = __hip_atomic_load(&hq[threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   suf[threadIdx.x] = c;
@@ -505,7 +577,7 @@ hipError_t bf_build(int mode, const float* src, int64_t ld, int n, int dim, int 
 
 hipError_t bf_normalize(float* x, int n, int dim, hipStream_t s) {
   if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(k_bf_normalize, dim3(nblocks(n, kBfThreads)), dim3(kBfThreads), 0, s, x, n, dim);
+  hipLaunchKernelGGL(k_bf_normalize, dim3(n), dim3(64), 0, s, x, dim);
   return hipGetLastError();
 }
 
