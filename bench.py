@@ -45,6 +45,10 @@ def parse():
     ap.add_argument("--no-search", action="store_true", help="skip the brute-force search measurement")
     ap.add_argument("--search-vectors", type=int, default=1_000_000)
     ap.add_argument("--search-batch", type=int, default=64)
+    ap.add_argument("--search-only", action="store_true",
+                    help="run only the search measurement and print its JSON (for profiling)")
+    ap.add_argument("--no-gpu-events", action="store_true",
+                    help="search timing by wall clock only (HIP events on a side stream do not work under rocprofv3)")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="after the timed region, run a plain fp32 copy kernel (y = -x) of this many MiB "
                          "three times, so a counter run can scale FETCH_SIZE/WRITE_SIZE to bytes")
@@ -169,6 +173,14 @@ def main():
     import torch
     from semantica_gpu import Context, Model, synth
 
+    if a.search_only:
+        ctx = Context(0)
+        res = search_leg(ctx, a.search_vectors, 768, a.search_batch, 10, max(3, a.steps // 2),
+                         not a.no_cpu_baseline, gpu_events=not a.no_gpu_events)
+        ctx.close()
+        print(json.dumps({"search": res}), flush=True)
+        return
+
     B, S = a.batch, a.seq_len
     mdl = synth.make_model()
     toks = synth.token_ids(B * S, mdl.config["vocab_size"], seed=0)
@@ -276,7 +288,7 @@ def main():
     model.close()
     if not a.no_search:
         line["search"] = search_leg(ctx, a.search_vectors, 768, a.search_batch, 10, max(3, a.steps // 2),
-                                    not a.no_cpu_baseline)
+                                    not a.no_cpu_baseline, gpu_events=not a.no_gpu_events)
     ctx.close()
     if not a.no_cpu_baseline:
         threads = a.cpu_threads or min(16, os.cpu_count() or 1)
