@@ -163,6 +163,38 @@ def search_leg(ctx, n, dim, batch, top_k, steps, with_cpu, gpu_events=True):
     return res
 
 
+def tokenizer_leg(n_texts=64, chars=2000):
+    """The host tokenizer (sg_tokenizer_*, internal/tokenizer) on a synthetic
+    262,144-token vocabulary (the real one is not available offline): texts of
+    random words, about one c2 batch of prompts."""
+    import numpy as np
+    from semantica_gpu.tokenizer import Tokenizer
+    rng = np.random.default_rng(6)
+    letters = np.array(list("abcdefghijklmnopqrstuvwxyz▁"))
+    pieces = set()
+    while len(pieces) < 262144 - 494:
+        pieces.add("".join(rng.choice(letters, size=int(rng.integers(2, 8)))))
+    vocab = ["<pad>", "<eos>", "<bos>"] + [f"<u{i}>" for i in range(235)] + [f"<0x{b:02X}>" for b in range(256)] + \
+        sorted(pieces)
+    scores = [0.0] * 238 + [-10.0] * 256 + (-rng.random(len(vocab) - 494)).tolist()
+    tok = Tokenizer.new(vocab, scores, add_bos=True, nfkc=True, bos_id=2, eos_id=1)
+    words = ["".join(rng.choice(letters[:26], size=int(rng.integers(2, 10)))) for _ in range(5000)]
+    texts = []
+    for _ in range(n_texts):
+        t = []
+        while sum(len(w) + 1 for w in t) < chars:
+            t.append(words[int(rng.integers(0, len(words)))])
+        texts.append("task: search result | query: " + " ".join(t))
+    tok.encode_batch(texts[:2])
+    t0 = time.perf_counter()
+    ids, off = tok.encode_batch(texts)
+    dt = time.perf_counter() - t0
+    tok.close()
+    return {"workload": f"{n_texts} prompts of ~{chars} characters, synthetic 262144-token vocabulary, host threads",
+            "texts_per_s": round(n_texts / dt, 1), "tokens_per_s": round(int(off[-1]) / dt, 1),
+            "tokens_per_text": round(int(off[-1]) / n_texts, 1)}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -287,6 +319,7 @@ def main():
     }
     model.close()
     if not a.no_search:
+        line["tokenizer"] = tokenizer_leg()
         line["search"] = search_leg(ctx, a.search_vectors, 768, a.search_batch, 10, max(3, a.steps // 2),
                                     not a.no_cpu_baseline, gpu_events=not a.no_gpu_events)
     ctx.close()

@@ -53,6 +53,8 @@ struct Meta {
   double f = 0;    // float payloads
   std::string s;
   uint64_t arr_len = 0;
+  uint32_t elem_type = 0;   // arrays: element type
+  std::vector<Meta> elems;  // arrays: the elements (the tokenizer reads them)
 };
 
 struct Tensor {
@@ -144,9 +146,16 @@ bool read_value(Cursor& c, uint32_t type, Meta* out, int depth) {
       const uint32_t et = c.get<uint32_t>();
       const uint64_t len = c.get<uint64_t>();
       if (!c.ok || len > c.n) return false;  // every element takes at least one byte
-      if (out) out->arr_len = len;
-      for (uint64_t i = 0; i < len && c.ok; i++)
-        if (!read_value(c, et, nullptr, depth + 1)) return false;
+      if (out) {
+        out->arr_len = len;
+        out->elem_type = et;
+        out->elems.resize(len);
+      }
+      for (uint64_t i = 0; i < len && c.ok; i++) {
+        Meta* e = out ? &out->elems[i] : nullptr;
+        if (e) e->type = et;
+        if (!read_value(c, et, e, depth + 1)) return false;
+      }
       break;
     }
     default:
@@ -382,6 +391,63 @@ int build_desc(const Gguf& g, Loaded& L) {
 
 }  // namespace
 
+namespace sgi {
+
+// LoadFromGGUF's reading of the tokenizer metadata (internal/tokenizer/
+// tokenizer.go:497-598): tokens (strings, required), scores (float32 or
+// float64, required), token_type (int32 / uint32 entries, others -> normal;
+// optional), add_bos_token (bool, default true), add_eos_token (bool, default
+// false), NFKC on, and the special ids when stored as uint32.
+int gguf_tokenizer_spec(const void* data, size_t size, TokenizerSpec& out) {
+  Gguf g;
+  SG_TRY(parse(data, size, g));
+  out = TokenizerSpec{};
+  const Meta* tk = find(g, "tokenizer.ggml.tokens");
+  if (!tk) return fail(SG_ERR_INVALID, "tokenizer.ggml.tokens not found");
+  if (tk->type != M_ARR) return fail(SG_ERR_INVALID, "tokenizer.ggml.tokens is not an array");
+  out.tokens.resize(tk->elems.size());
+  for (size_t i = 0; i < tk->elems.size(); i++) {
+    if (tk->elems[i].type != M_STR) return fail(SG_ERR_INVALID, "token %zu is not a string", i);
+    out.tokens[i] = tk->elems[i].s;
+  }
+  const Meta* sc = find(g, "tokenizer.ggml.scores");
+  if (!sc) return fail(SG_ERR_INVALID, "tokenizer.ggml.scores not found");
+  if (sc->type != M_ARR) return fail(SG_ERR_INVALID, "tokenizer.ggml.scores is not an array");
+  out.scores.resize(sc->elems.size());
+  for (size_t i = 0; i < sc->elems.size(); i++) {
+    const Meta& e = sc->elems[i];
+    if (e.type == M_F32 || e.type == M_F64)
+      out.scores[i] = (float)e.f;
+    else
+      return fail(SG_ERR_INVALID, "score %zu is not a number", i);
+  }
+  if (const Meta* ty = find(g, "tokenizer.ggml.token_type"); ty && ty->type == M_ARR) {
+    out.types.resize(ty->elems.size());
+    for (size_t i = 0; i < ty->elems.size(); i++) {
+      const Meta& e = ty->elems[i];
+      out.types[i] = (e.type == M_I32 || e.type == M_U32) ? (int32_t)(uint32_t)e.u : 1;
+    }
+  }
+  auto get_bool = [&](const char* k, bool dflt) {
+    const Meta* m = find(g, k);
+    return m && m->type == M_BOOL ? m->u != 0 : dflt;
+  };
+  out.add_bos = get_bool("tokenizer.ggml.add_bos_token", true);
+  out.add_eos = get_bool("tokenizer.ggml.add_eos_token", false);
+  out.nfkc = true;
+  auto get_id = [&](const char* k, int32_t& id) {
+    const Meta* m = find(g, k);
+    if (m && m->type == M_U32) id = (int32_t)(uint32_t)m->u;
+  };
+  get_id("tokenizer.ggml.bos_token_id", out.bos);
+  get_id("tokenizer.ggml.eos_token_id", out.eos);
+  get_id("tokenizer.ggml.unknown_token_id", out.unk);
+  get_id("tokenizer.ggml.padding_token_id", out.pad);
+  return SG_OK;
+}
+
+}  // namespace sgi
+
 extern "C" {
 
 int sg_gguf_read_config(const void* data, size_t size, sg_model_config* out) {
@@ -415,6 +481,24 @@ int sg_model_load_gguf_file(sg_ctx* ctx, const char* path, sg_model** out) {
   close(fd);
   if (p == MAP_FAILED) return fail(SG_ERR_INVALID, "mmap file: %s", strerror(errno));
   const int r = sg_model_load_gguf(ctx, p, (size_t)st.st_size, out);
+  munmap(p, (size_t)st.st_size);
+  return r;
+}
+
+int sg_tokenizer_from_gguf_file(const char* path, sg_tokenizer** out) {
+  if (!path || !out) return fail(SG_ERR_INVALID, "NULL argument");
+  *out = nullptr;
+  const int fd = open(path, O_RDONLY);
+  if (fd < 0) return fail(SG_ERR_INVALID, "open file: %s: %s", path, strerror(errno));
+  struct stat st;
+  if (fstat(fd, &st) != 0 || st.st_size <= 0) {
+    close(fd);
+    return fail(SG_ERR_INVALID, "file too small for header");
+  }
+  void* p = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+  close(fd);
+  if (p == MAP_FAILED) return fail(SG_ERR_INVALID, "mmap file: %s", strerror(errno));
+  const int r = sg_tokenizer_from_gguf(p, (size_t)st.st_size, out);
   munmap(p, (size_t)st.st_size);
   return r;
 }

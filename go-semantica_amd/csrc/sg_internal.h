@@ -4,6 +4,9 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include <string>
+#include <vector>
+
 #include "semantica_gpu.h"
 
 namespace sgi {
@@ -15,6 +18,18 @@ __attribute__((visibility("hidden"))) int fail(int code, const char* fmt, ...);
 // stream a call runs on (the caller's, or the context's own when NULL).
 __attribute__((visibility("hidden"))) int ctx_device(const sg_ctx* c);
 __attribute__((visibility("hidden"))) hipStream_t ctx_stream(const sg_ctx* c, void* stream);
+
+// A tokenizer's vocabulary and settings (tokenizer.New's arguments plus the
+// special ids LoadFromGGUF sets).  types empty = every token normal.
+struct TokenizerSpec {
+  std::vector<std::string> tokens;
+  std::vector<float> scores;
+  std::vector<int32_t> types;
+  bool add_bos = false, add_eos = false, lowercase = false, remove_accents = false, nfkc = false;
+  int32_t bos = -1, eos = -1, unk = -1, pad = -1;
+};
+// Reads the tokenizer metadata of a GGUF image (sg_gguf.cpp).
+__attribute__((visibility("hidden"))) int gguf_tokenizer_spec(const void* data, size_t size, TokenizerSpec& out);
 
 // Grow-only device buffer.
 struct DevBuf {

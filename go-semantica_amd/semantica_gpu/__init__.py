@@ -6,4 +6,4 @@ package only binds its C ABI and mirrors the reference's host API.
 from ._lib import SemanticaError, load  # noqa: F401
 from .runtime import (Context, Model, Runtime, read_gguf_config, resolve_dim, supported_dims,  # noqa: F401
                       DEFAULT_EMBED_DIM, SUPPORTED_DIMS)
-from . import search, synth  # noqa: F401
+from . import embed, search, synth, tokenizer  # noqa: F401

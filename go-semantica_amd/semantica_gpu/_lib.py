@@ -77,6 +77,11 @@ SG_K_CLASSES = 7
 KERNEL_CLASSES = ("gemm", "attention", "quantize", "norm", "gelu", "pool", "other")
 
 
+class TokenizerConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in ("add_bos", "add_eos", "lowercase", "remove_accents", "nfkc",
+                                                "bos_id", "eos_id", "unk_id", "pad_id")]
+
+
 class Profile(ctypes.Structure):
     _fields_ = [("ms", ctypes.c_double * SG_K_CLASSES), ("work", ctypes.c_double * SG_K_CLASSES),
                 ("launches", ctypes.c_int64 * SG_K_CLASSES)]
@@ -123,6 +128,14 @@ _PROTOS = {
     "sg_index_vector": (ctypes.c_int, [_vp, _i32, _vp]),
     "sg_index_search": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i32, _vp, _vp, _vp, _vp]),
     "sg_index_free": (None, [_vp]),
+    "sg_tokenizer_create": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _vp, _pp]),
+    "sg_tokenizer_from_gguf": (ctypes.c_int, [_vp, ctypes.c_size_t, _pp]),
+    "sg_tokenizer_from_gguf_file": (ctypes.c_int, [ctypes.c_char_p, _pp]),
+    "sg_tokenizer_encode": (ctypes.c_int, [_vp, _vp, ctypes.c_size_t, _vp, _i32, ctypes.POINTER(_i32)]),
+    "sg_tokenizer_encode_batch": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, ctypes.c_int64, _vp]),
+    "sg_tokenizer_decode": (ctypes.c_int, [_vp, _vp, _i32, _vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]),
+    "sg_tokenizer_vocab_size": (_i32, [_vp]),
+    "sg_tokenizer_free": (None, [_vp]),
 }
 
 _lib = None

@@ -237,6 +237,57 @@ int sg_embed_tokens(sg_model *model, float *dst, const int32_t *d_tokens, int32_
 int sg_pool_l2(sg_ctx *ctx, float *out, const float *x, int32_t ldx, int32_t out_dim,
                const int32_t *seq_offsets, int32_t n_seq, void *stream);
 
+/* ---- tokenizer (internal/tokenizer) -------------------------------------
+ * The reference's SentencePiece-style BPE tokenizer on the host: text ->
+ * the token IDs sg_forward takes.  Same normalization (NFKC / accents /
+ * lowercase), space handling, merge order (highest score, ties to the
+ * rightmost pair), byte fallback and special tokens as tokenizer.go. */
+typedef struct sg_tokenizer sg_tokenizer;
+
+/* tokenizer.Config (tokenizer.go:46-53) plus the special ids
+ * (LoadFromGGUF sets them from metadata, :570-595); -1 = none. */
+typedef struct {
+  int32_t add_bos, add_eos, lowercase, remove_accents, nfkc;
+  int32_t bos_id, eos_id, unk_id, pad_id;
+} sg_tokenizer_config;
+
+/* tokenizer.New (tokenizer.go:56-97).  Token i is
+ * token_data[token_offsets[i] .. token_offsets[i+1]) (UTF-8, any bytes);
+ * token_types may be NULL (all normal).  "vocab and scores length mismatch"
+ * cannot occur here (one n for both). */
+int sg_tokenizer_create(const char *token_data, const int64_t *token_offsets, const float *scores,
+                        const int32_t *token_types, int32_t n, const sg_tokenizer_config *cfg,
+                        sg_tokenizer **out);
+
+/* tokenizer.LoadFromGGUF (tokenizer.go:497-598) over a GGUF v3 image / file:
+ * tokenizer.ggml.tokens, .scores, .token_type, .add_bos_token,
+ * .add_eos_token and the special ids; NFKC on.  Same errors. */
+int sg_tokenizer_from_gguf(const void *data, size_t size, sg_tokenizer **out);
+int sg_tokenizer_from_gguf_file(const char *path, sg_tokenizer **out);
+
+/* Tokenizer.Encode (tokenizer.go:99-133) of text[0..len): *n_ids receives the
+ * number of IDs; the first min(n, cap) are written to ids (ids may be NULL to
+ * query the count). */
+int sg_tokenizer_encode(const sg_tokenizer *tok, const char *text, size_t len, int32_t *ids, int32_t cap,
+                        int32_t *n_ids);
+
+/* Encode of n_texts texts (text i = text_data[text_offsets[i] ..
+ * text_offsets[i+1])) into one packed array: id_offsets[n_texts+1] receives
+ * CSR offsets (the seq_offsets sg_forward takes); ids (capacity cap) may be
+ * NULL to query the total, id_offsets[n_texts]. */
+int sg_tokenizer_encode_batch(const sg_tokenizer *tok, const char *text_data, const int64_t *text_offsets,
+                              int32_t n_texts, int32_t *ids, int64_t cap, int32_t *id_offsets);
+
+/* Tokenizer.Decode (tokenizer.go:135-159): *len receives the byte length;
+ * the first min(len, cap) bytes go to buf (not NUL-terminated). */
+int sg_tokenizer_decode(const sg_tokenizer *tok, const int32_t *ids, int32_t n, char *buf, size_t cap,
+                        size_t *len);
+
+/* Tokenizer.VocabSize (tokenizer.go:438-440). */
+int32_t sg_tokenizer_vocab_size(const sg_tokenizer *tok);
+
+void sg_tokenizer_free(sg_tokenizer *tok);
+
 /* ---- brute-force vector search (search/brute) ----------------------------
  * The reference's quantized brute-force index (search/brute/index.go,
  * builder.go, storage.go) with its vectors in HBM.  Scores are bit-identical

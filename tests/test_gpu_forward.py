@@ -250,3 +250,51 @@ def test_config2_full_size_properties(full_gpu):
     toks_p = np.concatenate([toks[512 * i:512 * (i + 1)] for i in perm])
     yp = full_gpu.forward_packed(toks_p, np.arange(0, 4 * 512 + 1, 512, dtype=np.int32), 768)
     assert np.array_equal(yp.view(np.uint32), y[perm].view(np.uint32))
+
+
+def test_embed_texts_end_to_end(tiny_gpu, tiny_model):
+    """pkg/ggufembed over text (api.go:94-209): OpenBytes of one GGUF image
+    carrying the weights and a tokenizer vocabulary; EmbedInputs with mixed
+    tasks and dimensions must equal tokenizing each prompt with the oracle
+    tokenizer and running the descriptor-loaded model on those IDs, bit for
+    bit, in input order."""
+    import tokenizer_ref as ref
+    from semantica_gpu import embed, synth
+    rng = np.random.default_rng(8)
+    letters = list("abcdefghijklmnopqrstuvwxyz:|▁")
+    pieces = set()
+    while len(pieces) < 4096 - 494:
+        pieces.add("".join(rng.choice(letters, size=int(rng.integers(2, 6)))))
+    vocab = ["<pad>", "<eos>", "<bos>"] + letters + [f"<u{i}>" for i in range(238 - 3 - len(letters))] + \
+        [f"<0x{b:02X}>" for b in range(256)] + sorted(pieces)
+    assert len(vocab) == 4096
+    scores = [0.0] * 238 + [-10.0] * 256 + (-np.arange(len(vocab) - 494, dtype=np.float32) / 100).tolist()
+    types = [3, 3, 3] + [1] * 235 + [6] * 256 + [1] * (len(vocab) - 494)
+    md = [("tokenizer.ggml.tokens", "arr:str", vocab), ("tokenizer.ggml.scores", "arr:f32", scores),
+          ("tokenizer.ggml.token_type", "arr:i32", types), ("tokenizer.ggml.bos_token_id", "u32", 2),
+          ("tokenizer.ggml.eos_token_id", "u32", 1), ("tokenizer.ggml.padding_token_id", "u32", 0)]
+    image = synth.gguf_image(*synth.model_gguf_parts(tiny_model, vocab_tokens=False, extra_metadata=md))
+    say("embed: open_bytes + embed_inputs")
+    rt = embed.open_bytes(image)
+    try:
+        inputs = [embed.EmbedInput(embed.Task.SEARCH_QUERY, "hello world", dim=768),
+                  embed.EmbedInput(embed.Task.SEARCH_DOCUMENT, "the quick brown fox", title="fox", dim=256),
+                  embed.EmbedInput(embed.Task.NONE, "  plain text, ü and 😀 ", dim=0),
+                  embed.EmbedInput(embed.Task.CLUSTERING, "group these", dim=128),
+                  embed.EmbedInput(embed.Task.SEARCH_QUERY, "hello world", dim=256)]
+        got = rt.embed_inputs(inputs)
+        tok = ref.Tokenizer(vocab, scores, types, add_bos=True, nfkc=True, bos_id=2, eos_id=1, pad_id=0)
+        for inp, g in zip(inputs, got):
+            ids = tok.encode(embed.build_prompt(inp))
+            want = tiny_gpu.forward_batch([ids], embed.resolve_dim(inp.dim))[0]
+            assert g.shape == want.shape and np.array_equal(g.view(np.uint32), want.view(np.uint32)), inp
+        assert [len(v) for v in rt.embed(["a", "b c"])] == [512, 512]
+        assert rt.embed([]) is None and rt.embed_dim() == 768 and rt.max_seq_len() == 2048
+        with pytest.raises(embed.EmbedError, match=r"sequence too long: \d+ > 2048"):
+            rt.embed_single("é" * 1100)  # not in the vocabulary: two byte tokens each
+        with pytest.raises(embed.EmbedError, match="build prompt for input 1: content must not be empty"):
+            rt.embed_inputs([embed.EmbedInput(content="a"), embed.EmbedInput(content=" ")])
+        with pytest.raises(embed.EmbedError, match="input 0: unsupported embed dim 300"):
+            rt.embed_inputs([embed.EmbedInput(content="a", dim=300)])
+    finally:
+        rt.close()
