@@ -188,6 +188,50 @@ __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__
   }
 }
 
+// The next GEMM's operand straight from the residual stream: xn = RMSNorm(h; w)
+// recomputed with the lanes and order k_post_res_norm / k_embed_norm used
+// when they folded max|xn| into amax (so every value, and the scale, is the
+// one the unfused path quantizes), then quantized as k_quantize does
+// (model_int8.go:194-199 / :216-221: RMSNorm, then QuantizeSymmetricINT8 of
+// the normed sequence).  Saves writing xn and reading it back.
+template <int NC>
+__global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restrict__ h, const float* __restrict__ w,
+                                                            float eps, int T, const int32_t* __restrict__ row_seq,
+                                                            const float* __restrict__ amax,
+                                                            _Float16* __restrict__ qf, int a_rows,
+                                                            float* __restrict__ row_scale) {
+  constexpr int D = NC * 32;
+  __shared__ __attribute__((aligned(16))) float tiles[kThreads / SG_WAVE][8 * 40];
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
+  const int j = threadIdx.x & 7, r = (threadIdx.x >> 3) & 7;
+  if (row >= T) return;  // whole 8-lane groups: the group reductions stay complete
+  f32x4_t x[NC];
+  const f32x4_t* hr = reinterpret_cast<const f32x4_t*>(h + (int64_t)row * D) + j;
+#pragma unroll
+  for (int c = 0; c < NC; c++) x[c] = hr[8 * c];
+  sg_rmsnorm8_f4<NC>(x, w, tiles[threadIdx.x / SG_WAVE], r, j, eps);
+  const float m = amax[row_seq[row]];
+  float scale = 1.0f, inv = 0.0f;
+  if (m != 0.0f) {
+    scale = m / 127.0f;
+    inv = 1.0f / scale;
+  }
+  if (j == 0) row_scale[row] = scale;
+  // chunk c is K-block c; lane j holds its elements 4j..4j+3
+  _Float16* qr = qf + (int64_t)row * 32 + 4 * j;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    half4_t hv;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      int q = sg_round_prod(x[c][t], inv);
+      q = q > 127 ? 127 : (q < -127 ? -127 : q);
+      hv[t] = (_Float16)(float)q;
+    }
+    *reinterpret_cast<half4_t*>(qr + (int64_t)c * a_rows * 32) = hv;
+  }
+}
+
 __global__ void k_seq_scales(const float* __restrict__ amax, int n, float* __restrict__ out) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -228,37 +272,45 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(float* dst, const float* s
 
 // h = RMSNorm(o; w_post) + h (model_int8.go:203-210 / :225-232), then
 // xn = RMSNorm(h; w_next) -- the next pre-norm (:194/:216) or output_norm (:236).
-template <int NPL>
+// Float4 row layout (sg_rmsnorm8_f4): NC chunks of 32 elements per row.
+template <int NC>
 __global__ __launch_bounds__(kThreads) void k_post_res_norm(const float* __restrict__ o, float* __restrict__ h,
                                                             const float* __restrict__ w_post,
                                                             const float* __restrict__ w_next, float eps, int T,
                                                             float* __restrict__ xn,
                                                             const int32_t* __restrict__ row_seq,
                                                             float* __restrict__ amax) {
-  constexpr int D = NPL * 8;
+  constexpr int D = NC * 32;
+  __shared__ __attribute__((aligned(16))) float tiles[kThreads / SG_WAVE][8 * 40];
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
-  const int j = threadIdx.x & 7;
+  const int j = threadIdx.x & 7, r = (threadIdx.x >> 3) & 7;
+  float* tile = tiles[threadIdx.x / SG_WAVE];
   const bool valid = row < T;
   float m = 0.0f;
   if (valid) {
-    float x[NPL];
-    const float* orow = o + (int64_t)row * D;
+    f32x4_t x[NC];
+    const f32x4_t* orow = reinterpret_cast<const f32x4_t*>(o + (int64_t)row * D) + j;
 #pragma unroll
-    for (int i = 0; i < NPL; i++) x[i] = orow[8 * i + j];
-    if (w_post) sg_rmsnorm8<NPL>(x, w_post, j, eps);
-    float* hr = h + (int64_t)row * D;
+    for (int c = 0; c < NC; c++) x[c] = orow[8 * c];
+    if (w_post) sg_rmsnorm8_f4<NC>(x, w_post, tile, r, j, eps);
+    f32x4_t* hr = reinterpret_cast<f32x4_t*>(h + (int64_t)row * D) + j;
 #pragma unroll
-    for (int i = 0; i < NPL; i++) {
-      x[i] = x[i] + hr[8 * i + j];
-      hr[8 * i + j] = x[i];
+    for (int c = 0; c < NC; c++) {
+      const f32x4_t hv = hr[8 * c];
+#pragma unroll
+      for (int t = 0; t < 4; t++) x[c][t] = x[c][t] + hv[t];
+      hr[8 * c] = x[c];
     }
-    if (w_next) sg_rmsnorm8<NPL>(x, w_next, j, eps);
-    float* yr = xn + (int64_t)row * D;
+    if (w_next) sg_rmsnorm8_f4<NC>(x, w_next, tile, r, j, eps);
+    if (xn) {
+      f32x4_t* yr = reinterpret_cast<f32x4_t*>(xn + (int64_t)row * D) + j;
 #pragma unroll
-    for (int i = 0; i < NPL; i++) {
-      yr[8 * i + j] = x[i];
-      m = fmaxf(m, fabsf(x[i]));
+      for (int c = 0; c < NC; c++) yr[8 * c] = x[c];
     }
+#pragma unroll
+    for (int c = 0; c < NC; c++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) m = fmaxf(m, fabsf(x[c][t]));
   }
   if (amax) {
     m = sg_max8(m);
@@ -611,6 +663,16 @@ hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* 
   return hipGetLastError();
 }
 
+hipError_t norm_quantize(const float* h, const float* w, float eps, int T, int d, const int32_t* row_seq,
+                         const float* amax, _Float16* f16, int a_rows, float* row_scale, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  if (a_rows < T) return hipErrorInvalidValue;
+  SG_DISPATCH_NPL(d, NPL,
+                  hipLaunchKernelGGL(k_norm_quantize<NPL / 4>, dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads), 0,
+                                     s, h, w, eps, T, row_seq, amax, f16, a_rows, row_scale));
+  return hipGetLastError();
+}
+
 hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s) {
   hipLaunchKernelGGL(k_seq_scales, dim3(blocks_for(n_seq, 256)), dim3(256), 0, s, amax, n_seq, out);
   return hipGetLastError();
@@ -646,8 +708,8 @@ hipError_t post_res_norm(const float* o, float* h, const float* w_post, const fl
                          float* xn, const int32_t* row_seq, float* amax, hipStream_t s) {
   if (T <= 0) return hipSuccess;
   SG_DISPATCH_NPL(d, NPL,
-                  hipLaunchKernelGGL(k_post_res_norm<NPL>, dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads), 0,
-                                     s, o, h, w_post, w_next, eps, T, xn, row_seq, amax));
+                  hipLaunchKernelGGL(k_post_res_norm<NPL / 4>, dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads),
+                                     0, s, o, h, w_post, w_next, eps, T, xn, row_seq, amax));
   return hipGetLastError();
 }
 

@@ -399,7 +399,13 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
   for (int l = 0; l < L; l++) {
     if (l == stop) break;
     const LayerDev& ly = m->layers[l];
-    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 0), a16, ar, nullptr, sx, s));
+    if (l == 0) {
+      SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d),
+                sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 0), a16, ar, nullptr, sx, s));
+    } else {  // xn of this layer's pre-norm was never stored: recomputed from h
+      SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d),
+                sgk::norm_quantize(h, ly.attn_norm, eps, T, d, meta.row_seq, site(l, 0), a16, ar, sx, s));
+    }
     SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), sgk::gemm_q8(a16, ar, ly.wqkv, ly.sqkv, sx, qkv, nullptr, T, nqkv, d, s));
     SG_LAUNCH(SG_K_NORM, t * (qd + kvd) * 8.0,
               sgk::qknorm_rope(qkv, nqkv, qkv + qd, nqkv, ly.q_norm, ly.k_norm, c.num_heads, c.num_kv_heads, T,
@@ -413,17 +419,18 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
                              site(l, 1), s));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), sgk::quantize(att, qd, T, qd, meta.row_seq, site(l, 1), a16, ar, nullptr, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), sgk::gemm_q8(a16, ar, ly.wo, ly.so, sx, o, nullptr, T, d, qd, s));
-    SG_LAUNCH(SG_K_NORM, t * d * 16.0,
-              sgk::post_res_norm(o, h, ly.post_attn, ly.ffn_norm, eps, T, d, xn, meta.row_seq, site(l, 2), s));
-    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 2), a16, ar, nullptr, sx, s));
+    SG_LAUNCH(SG_K_NORM, t * d * 12.0,
+              sgk::post_res_norm(o, h, ly.post_attn, ly.ffn_norm, eps, T, d, nullptr, meta.row_seq, site(l, 2), s));
+    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d),
+              sgk::norm_quantize(h, ly.ffn_norm, eps, T, d, meta.row_seq, site(l, 2), a16, ar, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(2 * ff, d),
               sgk::gemm_q8_gelu(a16, ar, ly.wgu, ly.sgu, sx, g, T, ff, d, meta.row_seq, site(l, 3), s));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(ff), sgk::quantize(g, ff, T, ff, meta.row_seq, site(l, 3), a16, ar, nullptr, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), sgk::gemm_q8(a16, ar, ly.wd, ly.sd, sx, o, nullptr, T, d, ff, s));
     const bool last = l + 1 == L;
-    SG_LAUNCH(SG_K_NORM, t * d * 16.0,
-              sgk::post_res_norm(o, h, ly.post_ffw, last ? m->out_norm : m->layers[l + 1].attn_norm, eps, T, d, xn,
-                                 meta.row_seq, last ? nullptr : site(l + 1, 0), s));
+    SG_LAUNCH(SG_K_NORM, t * d * (last ? 16.0 : 12.0),
+              sgk::post_res_norm(o, h, ly.post_ffw, last ? m->out_norm : m->layers[l + 1].attn_norm, eps, T, d,
+                                 last ? xn : nullptr, meta.row_seq, last ? nullptr : site(l + 1, 0), s));
   }
   if (stop >= 0) {
     SG_HIP(hipMemcpyAsync(d_out, h, sizeof(float) * (size_t)T * d, hipMemcpyDeviceToDevice, s));

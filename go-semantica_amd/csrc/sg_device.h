@@ -204,3 +204,52 @@ __device__ __forceinline__ void sg_rmsnorm8(float (&x)[NPL], const float* __rest
   }
 }
 
+// Coalesced variant for the bandwidth-bound row kernels.  The 8-lane group
+// loads the row as float4 slots: lane j owns elements 32c + 4j .. 32c + 4j + 3
+// of every 32-element chunk c, so one load instruction covers 128 contiguous
+// bytes of each row (the stride-8 layout above covers 32).  The sum of squares
+// must still run in the AVX2 lane order, lane v chaining element 8i + v over
+// i, so each chunk is transposed through the wave's LDS tile (8 rows x 40
+// floats; the stride of 40 puts the 8 rows' reads in distinct banks): after
+// the write, lane v of row r reads elements 8k + v of the chunk, k = 0..3,
+// i.e. i = 4c + k in order.  LDS operations of one wave complete in issue
+// order, so only the compiler has to be kept from reordering them.
+template <int NC>
+__device__ __forceinline__ float sg_sumsq8_f4(const f32x4_t (&x)[NC], float* tile, int r, int j) {
+  f32x4_t* wr = reinterpret_cast<f32x4_t*>(tile + r * 40 + 4 * j);
+  const float* rd = tile + r * 40 + j;
+  float acc = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    asm volatile("" ::: "memory");
+    *wr = x[c];
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const float v = rd[8 * k];
+      acc = __builtin_fmaf(v, v, acc);
+    }
+  }
+  asm volatile("" ::: "memory");
+  return sg_hsum8(acc);
+}
+
+// sg_rmsnorm8 on the float4 layout: same sum, same scalar steps, y = (x*inv)*w.
+template <int NC>
+__device__ __forceinline__ void sg_rmsnorm8_f4(f32x4_t (&x)[NC], const float* __restrict__ w, float* tile, int r,
+                                               int j, float eps) {
+  const float ss = sg_sumsq8_f4<NC>(x, tile, r, j);
+  const float ms = ss / (float)(NC * 32);
+  const float rms = sg_sqrt(ms + eps);
+  const float inv = 1.0f / rms;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(w + 32 * c + 4 * j);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const float u = x[c][t] * inv;
+      x[c][t] = u * wv[t];
+    }
+  }
+}
+

@@ -40,6 +40,11 @@ hipError_t embed_norm(const int32_t* tokens, int T, const int8_t* eq, const floa
 // GEMM operand) or int8 row-major i8[rows][cols] (i8 != null), and row_scale[rows].
 hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
                     _Float16* f16, int a_rows, int8_t* i8, float* row_scale, hipStream_t s);
+// xn = RMSNorm(h; w) recomputed row by row exactly as post_res_norm / embed_norm
+// formed it, quantized with amax[row_seq[r]] into the block-major fp16 GEMM
+// operand f16[d/32][a_rows][32] and row_scale[T] (quantize's arithmetic).
+hipError_t norm_quantize(const float* h, const float* w, float eps, int T, int d, const int32_t* row_seq,
+                         const float* amax, _Float16* f16, int a_rows, float* row_scale, hipStream_t s);
 hipError_t absmax_rows(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, float* amax,
                        hipStream_t s);
 hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s);
@@ -53,7 +58,8 @@ hipError_t qknorm_rope(float* q, int ldq, float* k, int ldk, const float* qw, co
                        int T, const int32_t* row_pos, const float* cos_t, const float* sin_t, float eps,
                        _Float16* qs_h, _Float16* qs_l, int ldqs, _Float16* ks_h, _Float16* ks_l, int ldks,
                        hipStream_t s);
-// h = RMSNorm(o; w_post) + h ; xn = RMSNorm(h; w_next) ; amax (optional) per sequence of max|xn|.
+// h = RMSNorm(o; w_post) + h ; xn = RMSNorm(h; w_next) (stored when xn != null) ;
+// amax (optional) per sequence of max|xn|.
 hipError_t post_res_norm(const float* o, float* h, const float* w_post, const float* w_next, float eps, int T,
                          int d, float* xn, const int32_t* row_seq, float* amax, hipStream_t s);
 // g = geluquick(gate)*up over rows x cols; amax (optional) per sequence of max|g|.
