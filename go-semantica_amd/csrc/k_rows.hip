@@ -389,64 +389,44 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope(float* __restrict__ q,
 }
 
 // The same per-(token, head) arithmetic as k_qknorm_rope, writing the split
-// attention operands, with coalesced I/O: a wave owns 8 (token, head) rows;
-// each row (256 floats, 1 KB) is loaded by one float4 instruction into LDS,
-// read back in the 8-lane order the RMSNorm needs, and the packed hi|lo
-// results go back through LDS so every lane stores 16-byte chunks (128
-// contiguous bytes per row per instruction) instead of 2-byte scattered
-// stores.
+// attention operands, in the float4 row layout (sg_rmsnorm8_f4): lane j of
+// the row's 8-lane group holds elements 32c + 4j .. 32c + 4j + 3, so loads
+// are 128 contiguous bytes per row and the RoPE partner e + 128 of element e
+// (chunk c + 4) sits in the same lane and slot.  Stores are 8-byte half4 hi
+// and lo pieces, 64 contiguous bytes per row and chunk.
 __global__ __launch_bounds__(kThreads) void k_qknorm_rope_split(
     const float* __restrict__ q, int ldq, const float* __restrict__ k, int ldk, const float* __restrict__ qw,
     const float* __restrict__ kw, int H, int HKV, int T, const int32_t* __restrict__ row_pos,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, float eps, _Float16* __restrict__ qs_h,
     _Float16* __restrict__ qs_l, int ldqs, _Float16* __restrict__ ks_h, _Float16* __restrict__ ks_l, int ldks) {
-  constexpr int NPL = 32, HALF = 128, RS = 256 + 8;  // row stride in floats: conflict-free 8-lane reads
-  __shared__ __attribute__((aligned(16))) float tile[kThreads / SG_WAVE][8][RS];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  constexpr int NC = 8, HALF = 128;
+  __shared__ __attribute__((aligned(16))) float tiles[kThreads / SG_WAVE][8 * 40];
+  const int64_t g = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
+  const int j = threadIdx.x & 7, r = (threadIdx.x >> 3) & 7;
   const int per = H + HKV;
-  const int64_t n_rows = (int64_t)T * per;
-  const int64_t row0 = (int64_t)blockIdx.x * kRowsPerBlock + w * 8;
+  if (g >= (int64_t)T * per) return;  // whole 8-lane groups
+  const int t = (int)(g / per), hh = (int)(g % per);
+  const float* src = hh < H ? q + (int64_t)t * ldq + hh * 256 : k + (int64_t)t * ldk + (hh - H) * 256;
+  f32x4_t x[NC];
 #pragma unroll
-  for (int rr = 0; rr < 8; rr++) {
-    const int64_t g = row0 + rr;
-    if (g < n_rows) {
-      const int t = (int)(g / per), hh = (int)(g % per);
-      const float* src = hh < H ? q + (int64_t)t * ldq + hh * 256 : k + (int64_t)t * ldk + (hh - H) * 256;
-      *reinterpret_cast<f32x4_t*>(&tile[w][rr][4 * lane]) = *reinterpret_cast<const f32x4_t*>(src + 4 * lane);
+  for (int c = 0; c < NC; c++) x[c] = *reinterpret_cast<const f32x4_t*>(src + 32 * c + 4 * j);
+  const float* wn = hh < H ? qw : kw;
+  if (wn) sg_rmsnorm8_f4<NC>(x, wn, tiles[threadIdx.x / SG_WAVE], r, j, eps);
+  const int pos = row_pos[t];
+  const float* cr = cos_t + (int64_t)pos * HALF + 4 * j;
+  const float* sr = sin_t + (int64_t)pos * HALF + 4 * j;
+#pragma unroll
+  for (int c = 0; c < NC / 2; c++) {
+    const f32x4_t cv = *reinterpret_cast<const f32x4_t*>(cr + 32 * c);
+    const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(sr + 32 * c);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const float v0 = x[c][u], v1 = x[c + NC / 2][u];
+      const float a = v0 * cv[u], b = v1 * sv[u], cc = v0 * sv[u], dd = v1 * cv[u];
+      x[c][u] = a - b;
+      x[c + NC / 2][u] = cc + dd;
     }
   }
-  __syncthreads();
-  const int gi = lane >> 3, j = lane & 7;
-  const int64_t g = row0 + gi;
-  const bool valid = g < n_rows;
-  const int t = valid ? (int)(g / per) : 0, hh = valid ? (int)(g % per) : 0;
-  float x[NPL];
-#pragma unroll
-  for (int i = 0; i < NPL; i++) x[i] = tile[w][gi][8 * i + j];
-  const float* wn = hh < H ? qw : kw;
-  if (wn) sg_rmsnorm8<NPL>(x, wn, j, eps);
-  const int pos = row_pos[t];
-  const float* cr = cos_t + (int64_t)pos * HALF;
-  const float* sr = sin_t + (int64_t)pos * HALF;
-#pragma unroll
-  for (int i = 0; i < NPL / 2; i++) {
-    const int e = 8 * i + j;
-    const float c = cr[e], s = sr[e];
-    const float v0 = x[i], v1 = x[i + NPL / 2];
-    const float a = v0 * c, b = v1 * s, cc = v0 * s, dd = v1 * c;
-    x[i] = a - b;
-    x[i + NPL / 2] = cc + dd;
-  }
-  // Each lane overwrites exactly the slots it read, so no barrier is needed
-  // before these writes; the chunk reads below need every lane's writes.
-  uint32_t* pk = reinterpret_cast<uint32_t*>(&tile[w][gi][0]);
-#pragma unroll
-  for (int i = 0; i < NPL; i++) {
-    const hl16 sp = split_f16(x[i] * sgk::kAttnQKScale);
-    pk[8 * i + j] = (uint32_t)__builtin_bit_cast(uint16_t, sp.hi) | ((uint32_t)__builtin_bit_cast(uint16_t, sp.lo) << 16);
-  }
-  __syncthreads();
-  if (!valid) return;
   _Float16 *dh, *dl;
   if (hh < H) {
     dh = qs_h + (int64_t)t * ldqs + hh * 256;
@@ -456,21 +436,16 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope_split(
     dl = ks_l + (int64_t)t * ldks + (hh - H) * 256;
   }
 #pragma unroll
-  for (int kk = 0; kk < 4; kk++) {
-    const int c = j + 8 * kk;  // chunk of elements 8c .. 8c+7
-    const uint4 a = *reinterpret_cast<const uint4*>(&pk[8 * c]);
-    const uint4 b = *reinterpret_cast<const uint4*>(&pk[8 * c + 4]);
-    const uint32_t u[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    uint4 hv, lv;
-    uint32_t* hp = &hv.x;
-    uint32_t* lp = &lv.x;
+  for (int c = 0; c < NC; c++) {
+    half4_t hv, lv;
 #pragma unroll
-    for (int m = 0; m < 4; m++) {
-      hp[m] = (u[2 * m] & 0xffffu) | (u[2 * m + 1] << 16);
-      lp[m] = (u[2 * m] >> 16) | (u[2 * m + 1] & 0xffff0000u);
+    for (int u = 0; u < 4; u++) {
+      const hl16 sp = split_f16(x[c][u] * sgk::kAttnQKScale);
+      hv[u] = sp.hi;
+      lv[u] = sp.lo;
     }
-    *reinterpret_cast<uint4*>(dh + 8 * c) = hv;
-    *reinterpret_cast<uint4*>(dl + 8 * c) = lv;
+    *reinterpret_cast<half4_t*>(dh + 32 * c + 4 * j) = hv;
+    *reinterpret_cast<half4_t*>(dl + 32 * c + 4 * j) = lv;
   }
 }
 
@@ -694,7 +669,8 @@ hipError_t qknorm_rope(float* q, int ldq, float* k, int ldk, const float* qw, co
   if (qs_h && (!qs_l || !ks_h || !ks_l)) return hipErrorInvalidValue;
   const int64_t groups = (int64_t)T * (H + HKV);
   if (qs_h) {
-    if ((ldqs | ldks) & 7) return hipErrorInvalidValue;
+    if ((ldqs | ldks) & 7 || (ldq | ldk) & 3 || (reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) & 15)
+      return hipErrorInvalidValue;  // float4 loads of every head row
     hipLaunchKernelGGL(k_qknorm_rope_split, dim3(blocks_for(groups, kRowsPerBlock)), dim3(kThreads), 0, s, q, ldq, k,
                        ldk, qw, kw, H, HKV, T, row_pos, cos_t, sin_t, eps, qs_h, qs_l, ldqs, ks_h, ks_l, ldks);
   } else {
