@@ -145,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void k_embed_only(const int32_t* __restri
 // quantize.go:29-103 with the tensor max replaced by the per-sequence max
 // gathered into amax (one reference call quantizes one sequence):
 // scale = m/127 (fp32), inv = 1/scale (fp32),
-// q = clamp(round_half_away(float64(x)*float64(inv)), +-127) (sg_round_prod);
+// q = clamp(round_half_away(float64(x)*float64(inv)), +-127) (sg_quant_code);
 // m == 0 -> scale 1, q 0.
 // One row per wave (4 rows per workgroup): the row's scale and reciprocal are
 // computed once, then the wave walks the row in coalesced float4 slots.
@@ -168,21 +168,19 @@ __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__
   const float* xr = x + (int64_t)row * ldx;
   for (int c4 = lane; c4 < (cols >> 2); c4 += SG_WAVE) {
     const f32x4_t v = *reinterpret_cast<const f32x4_t*>(xr + 4 * c4);
-    int qv[4];
+    float qv[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      int q = sg_round_prod(v[t], inv);  // m == 0: inv == 0 gives 0
-      qv[t] = q > 127 ? 127 : (q < -127 ? -127 : q);
-    }
+    for (int t = 0; t < 4; t++) qv[t] = sg_quant_code(v[t], inv);  // m == 0: inv == 0 gives 0
     if (F16) {  // block-major GEMM operand: [k/32][a_rows][32]
       half4_t h;
 #pragma unroll
-      for (int t = 0; t < 4; t++) h[t] = (_Float16)(float)qv[t];
+      for (int t = 0; t < 4; t++) h[t] = (_Float16)qv[t];
       const int k = 4 * c4;
       *reinterpret_cast<half4_t*>(qf + ((int64_t)(k >> 5) * a_rows + row) * 32 + (k & 31)) = h;
     } else {
       char4 c;
-      c.x = (signed char)qv[0]; c.y = (signed char)qv[1]; c.z = (signed char)qv[2]; c.w = (signed char)qv[3];
+      c.x = (signed char)(int)qv[0]; c.y = (signed char)(int)qv[1]; c.z = (signed char)(int)qv[2];
+      c.w = (signed char)(int)qv[3];
       *reinterpret_cast<char4*>(qi + (int64_t)row * cols + 4 * c4) = c;
     }
   }
@@ -223,11 +221,7 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
   for (int c = 0; c < NC; c++) {
     half4_t hv;
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-      int q = sg_round_prod(x[c][t], inv);
-      q = q > 127 ? 127 : (q < -127 ? -127 : q);
-      hv[t] = (_Float16)(float)q;
-    }
+    for (int t = 0; t < 4; t++) hv[t] = (_Float16)sg_quant_code(x[c][t], inv);
     *reinterpret_cast<half4_t*>(qr + (int64_t)c * a_rows * 32) = hv;
   }
 }

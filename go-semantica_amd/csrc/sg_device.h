@@ -164,21 +164,30 @@ __device__ __forceinline__ void sg_block_seq_max(float m, bool owner, int row, i
 }
 
 // math.Round(float64(x) * float64(inv)) (quantize.go:67,95) without float64
-// arithmetic: the product of two floats is exact in float64, and here it is
-// carried exactly as hi + lo (hi = fl(x*inv), lo = fma(x, inv, -hi)).
-// roundf(hi) rounds half away from zero, like math.Round, and is the answer
-// unless hi sits exactly on a half while lo moves the true product off it
-// towards the other neighbour.  hi - q0 is exact (Sterbenz), |lo| is far
-// below a half.  Half the registers of the float64 form, and no float64 ops.
-__device__ __forceinline__ int sg_round_prod(float x, float inv) {
+// arithmetic, as an integer-valued float.  hi = fl(x*inv) is within half an
+// ulp of the exact product p, and every half-integer k + 0.5 (|k| < 2^22) is a
+// float, so p and hi lie on the same side of every such half unless hi lands
+// exactly on one: away from ties rint(hi) is round(p).  On a tie (hi - rint(hi)
+// = +-0.5, exact) the exact remainder lo = fma(x, inv, -hi) decides: p above
+// the half rounds up, below it rounds down, and p == hi (lo == 0) rounds away
+// from zero like math.Round.  Ties are rare (~2^-16 per value), so they take a
+// branch; the common path is a multiply, a rint and a compare.
+__device__ __forceinline__ float sg_round_prod_f(float x, float inv) {
   const float hi = x * inv;
-  const float lo = __builtin_fmaf(x, inv, -hi);
-  const float q0 = roundf(hi);
-  const float f = hi - q0;
-  float q = q0;
-  q = (f == 0.5f && lo > 0.0f) ? q + 1.0f : q;
-  q = (f == -0.5f && lo < 0.0f) ? q - 1.0f : q;
-  return (int)q;
+  float q = __builtin_rintf(hi);
+  if (__builtin_expect(__builtin_fabsf(hi - q) == 0.5f, 0)) {
+    const float lo = __builtin_fmaf(x, inv, -hi);
+    q = (lo > 0.0f || (lo == 0.0f && hi > 0.0f)) ? hi + 0.5f : hi - 0.5f;
+  }
+  return q;
+}
+
+__device__ __forceinline__ int sg_round_prod(float x, float inv) { return (int)sg_round_prod_f(x, inv); }
+
+// The int8 code of x at reciprocal scale inv: clamp(round(x*inv), +-127),
+// returned as an integer-valued float.
+__device__ __forceinline__ float sg_quant_code(float x, float inv) {
+  return __builtin_amdgcn_fmed3f(sg_round_prod_f(x, inv), -127.0f, 127.0f);
 }
 
 // RMSNorm of one row held by an 8-lane group, internal/kernels/norm.go:8-36.
