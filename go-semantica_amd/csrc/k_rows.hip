@@ -226,6 +226,40 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
   }
 }
 
+// The GEMM-operand form of k_quantize on the float4 row layout: an 8-lane
+// group per row, lane j handling elements 32c + 4j .. + 3 of every chunk c
+// (chunk c is K-block c), so a wave's stores cover 8 consecutive rows' 64-byte
+// block pieces: 512 contiguous bytes per instruction.
+template <int NC>
+__global__ __launch_bounds__(kThreads) void k_quantize_blocked(const float* __restrict__ x, int ldx, int rows,
+                                                               const int32_t* __restrict__ row_seq,
+                                                               const float* __restrict__ amax,
+                                                               _Float16* __restrict__ qf, int a_rows,
+                                                               float* __restrict__ row_scale) {
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
+  const int j = threadIdx.x & 7;
+  if (row >= rows) return;
+  const float m = amax[row_seq[row]];
+  float scale = 1.0f, inv = 0.0f;
+  if (m != 0.0f) {
+    scale = m / 127.0f;
+    inv = 1.0f / scale;
+  }
+  if (j == 0) row_scale[row] = scale;
+  const f32x4_t* xr = reinterpret_cast<const f32x4_t*>(x + (int64_t)row * ldx) + j;
+  f32x4_t v[NC];  // every load in flight before the first store
+#pragma unroll
+  for (int c = 0; c < NC; c++) v[c] = xr[8 * c];
+  _Float16* qr = qf + (int64_t)row * 32 + 4 * j;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    half4_t hv;
+#pragma unroll
+    for (int t = 0; t < 4; t++) hv[t] = (_Float16)sg_quant_code(v[c][t], inv);
+    *reinterpret_cast<half4_t*>(qr + (int64_t)c * a_rows * 32) = hv;
+  }
+}
+
 __global__ void k_seq_scales(const float* __restrict__ amax, int n, float* __restrict__ out) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -623,6 +657,20 @@ hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* 
   if (cols % 4 || ldx % 4) return hipErrorInvalidValue;
   if (f16 && (cols % 32 || a_rows < rows)) return hipErrorInvalidValue;
   const unsigned nblk = blocks_for(rows, kThreads / SG_WAVE);
+  if (f16 && (ldx & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    switch (cols) {  // the widths the forward quantizes: hidden, attention output, FFN
+      case 768:
+        hipLaunchKernelGGL(k_quantize_blocked<24>, dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0, s, x,
+                           ldx, rows, row_seq, amax, f16, a_rows, row_scale);
+        return hipGetLastError();
+      case 1152:
+        hipLaunchKernelGGL(k_quantize_blocked<36>, dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0, s, x,
+                           ldx, rows, row_seq, amax, f16, a_rows, row_scale);
+        return hipGetLastError();
+      default:
+        break;
+    }
+  }
   if (f16)
     hipLaunchKernelGGL(k_quantize<true>, dim3(nblk), dim3(kThreads), 0, s, x, ldx, rows, cols, row_seq, amax, f16,
                        a_rows, nullptr, row_scale);
