@@ -252,6 +252,43 @@ def test_config2_full_size_properties(full_gpu):
     assert np.array_equal(yp.view(np.uint32), y[perm].view(np.uint32))
 
 
+def _batch_invariance(gpu, toks, off, out_dim, y, rows):
+    """Each listed sequence embedded alone is bit-identical to its row of the packed batch."""
+    for i in rows:
+        a, b = int(off[i]), int(off[i + 1])
+        alone = gpu.forward_packed(toks[a:b], np.array([0, b - a], np.int32), out_dim)[0]
+        assert np.array_equal(alone.view(np.uint32), y[i].view(np.uint32)), i
+
+
+def test_config3_full_size_properties(full_gpu):
+    """Config 3 (8 sequences, lengths U[1024, 2048] seed 4, full model): finite, unit
+    norm, and batch invariance for every sequence."""
+    from semantica_gpu import synth
+    lens = synth.lengths_uniform(8, 1024, 2048, seed=4)
+    off = synth.offsets_from_lengths(lens)
+    toks = synth.token_ids(int(off[-1]), 262144, seed=4)
+    say(f"config3 lens={lens.tolist()}")
+    y = full_gpu.forward_packed(toks, off, 768)
+    assert y.shape == (8, 768) and np.all(np.isfinite(y))
+    assert np.max(np.abs(np.sum(y.astype(np.float64) ** 2, axis=1) - 1)) < 1e-5
+    _batch_invariance(full_gpu, toks, off, 768, y, range(8))
+
+
+def test_config4_full_size_properties(full_gpu):
+    """Config 4 at full size (256 sequences, log-uniform lengths in [8, 512] seed 1,
+    Matryoshka 256 dims): finite, unit norm over the 256 dims, and batch invariance on
+    a spread of rows."""
+    from semantica_gpu import synth
+    lens = synth.lengths_log_uniform(256, 8, 512, seed=1)
+    off = synth.offsets_from_lengths(lens)
+    toks = synth.token_ids(int(off[-1]), 262144, seed=1)
+    say(f"config4 full: 256 sequences, {int(off[-1])} tokens")
+    y = full_gpu.forward_packed(toks, off, 256)
+    assert y.shape == (256, 256) and np.all(np.isfinite(y))
+    assert np.max(np.abs(np.sum(y.astype(np.float64) ** 2, axis=1) - 1)) < 1e-5
+    _batch_invariance(full_gpu, toks, off, 256, y, (0, 1, 100, 255))
+
+
 def test_embed_texts_end_to_end(tiny_gpu, tiny_model):
     """pkg/ggufembed over text (api.go:94-209): OpenBytes of one GGUF image
     carrying the weights and a tokenizer vocabulary; EmbedInputs with mixed
