@@ -368,6 +368,7 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
     // (n0 / 2) + 32p + lr.
     static_assert(TN % 2 == 0, "GELU pairs gate and up subtiles");
     __shared__ float red[NW];
+    __shared__ float rmax[NW * BMW];
     const int Nh = N >> 1;
     const int r_first = by * NW * BMW, r_last = min(r_first + NW * BMW, M) - 1;
     const bool one_seq = amax && row_seq[r_first] == row_seq[r_last];  // workgroup-uniform
@@ -391,10 +392,10 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
         }
         if (one_seq) {
           mx = fmaxf(mx, a);
-        } else if (amax) {  // rows of several sequences: one maximum per row
+        } else if (amax) {  // rows of several sequences: per-row maxima, folded below
 #pragma unroll
           for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
-          if (lr == 0 && row < M) sg_atomic_max_nonneg(amax + row_seq[row], a);
+          if (lr == 0) rmax[row - r_first] = a;
         }
       }
     }
@@ -408,6 +409,9 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
         for (int i = 1; i < NW; i++) mm = fmaxf(mm, red[i]);
         sg_atomic_max_nonneg(amax + row_seq[r_first], mm);
       }
+    } else if (amax) {  // workgroup-uniform
+      __syncthreads();
+      sg_seg_seq_max(rmax, r_last - r_first + 1, r_first, row_seq, amax);
     }
   } else {
 #pragma unroll

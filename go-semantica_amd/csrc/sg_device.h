@@ -134,19 +134,42 @@ __device__ __forceinline__ void sg_atomic_max_nonneg(float* addr, float v) {
   atomicMax(reinterpret_cast<unsigned int*>(addr), __float_as_uint(v));
 }
 
+// Per-sequence maxima of a workgroup's rows [r_first, r_first + n), n <= the
+// workgroup size: rmax[i] (LDS, written and published by the caller) is row
+// r_first + i's maximum.  Rows are packed sequence by sequence (row_seq is
+// non-decreasing), so thread i takes row i, a segmented max-scan over each
+// wave's 64 rows gathers every run of equal row_seq, and the run's last lane
+// issues one atomic: one atomic per sequence and wave instead of one per row
+// (same-address atomics serialise in L2).
+__device__ __forceinline__ void sg_seg_seq_max(const float* rmax, int n, int r_first,
+                                               const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
+  const int i = threadIdx.x, lane = i & 63;
+  if ((i & ~63) >= n) return;  // wave-uniform: waves past the rows
+  const bool v = i < n;
+  float m = v ? rmax[i] : 0.0f;
+  const int s = v ? row_seq[r_first + i] : -1;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float mo = __shfl_up(m, o);
+    const int so = __shfl_up(s, o);
+    if (lane >= o && so == s) m = fmaxf(m, mo);
+  }
+  const int sn = __shfl_down(s, 1);
+  if (v && (lane == 63 || sn != s)) sg_atomic_max_nonneg(amax + s, m);
+}
+
 // Folds per-row maxima into the per-sequence maxima amax[row_seq[row]] for
-// the rows [r_first, r_last] a workgroup of NT threads owns.  Rows are packed
-// sequence by sequence (row_seq is non-decreasing), so when the first and the
-// last row share a sequence the whole workgroup reduces to ONE atomic; a
-// workgroup that straddles sequences issues one atomic per row from the
-// row's owner thread.  Thousands of same-address atomics (one per row)
-// serialise in L2, hence the reduction.  m: the caller's row maximum (0 for
-// threads without a row), non-negative.  Every thread of the workgroup must
-// call this (it holds a barrier).
-template <int NT>
+// the rows [r_first, r_last] (at most ROWS) a workgroup of NT threads owns.
+// When the first and the last row share a sequence the whole workgroup
+// reduces to ONE atomic; otherwise sg_seg_seq_max issues one per sequence
+// and wave.  m: the caller's row maximum (0 for threads without a row),
+// non-negative; owner: this thread publishes its row's maximum.  Every thread
+// of the workgroup must call this (it holds a barrier).
+template <int NT, int ROWS = NT / 8>
 __device__ __forceinline__ void sg_block_seq_max(float m, bool owner, int row, int r_first, int r_last,
                                                  const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
   __shared__ float red[NT / 64];
+  __shared__ float rmax[ROWS];
   const int s0 = row_seq[r_first];
   if (s0 == row_seq[r_last]) {
     m = sg_wave_max(m);
@@ -158,8 +181,10 @@ __device__ __forceinline__ void sg_block_seq_max(float m, bool owner, int row, i
       for (int i = 1; i < NT / 64; i++) mm = fmaxf(mm, red[i]);
       sg_atomic_max_nonneg(amax + s0, mm);
     }
-  } else if (owner) {
-    sg_atomic_max_nonneg(amax + row_seq[row], m);
+  } else {
+    if (owner) rmax[row - r_first] = m;
+    __syncthreads();
+    sg_seg_seq_max(rmax, r_last - r_first + 1, r_first, row_seq, amax);
   }
 }
 
