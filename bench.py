@@ -163,6 +163,30 @@ def search_leg(ctx, n, dim, batch, top_k, steps, with_cpu, gpu_events=True):
     return res
 
 
+def small_batch_latency(model, shapes=((1, 32), (8, 32), (1, 512), (8, 512)), reps=10):
+    """Wall time of one device-resident forward (tokens already in HBM, embeddings
+    left there) at small batches, where the forward is a chain of ~290 short
+    kernels rather than a throughput job: the serving latency of EmbedSingle-like
+    calls.  Same synthetic model and token stream as the headline."""
+    import numpy as np
+    import torch
+    from semantica_gpu import synth
+    res = {}
+    for b, s in shapes:
+        toks = torch.from_numpy(synth.token_ids(b * s, 262144, seed=0)).cuda()
+        off = np.arange(0, b * s + 1, s, dtype=np.int32)
+        out = torch.empty((b, 768), dtype=torch.float32, device="cuda")
+        for _ in range(3):
+            model.forward_device(toks.data_ptr(), off, 768, out.data_ptr())
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            model.forward_device(toks.data_ptr(), off, 768, out.data_ptr())
+        torch.cuda.synchronize()
+        res[f"{b}x{s}_ms"] = round((time.perf_counter() - t0) / reps * 1e3, 3)
+    return res
+
+
 def tokenizer_leg(n_texts=64, chars=2000):
     """The host tokenizer (sg_tokenizer_*, internal/tokenizer) on a synthetic
     262,144-token vocabulary (the real one is not available offline): texts of
@@ -317,6 +341,7 @@ def main():
         "instrumented_ms_per_step": round(dt_prof / a.steps * 1e3, 3),
         "gemm_frac_of_step": round(g["ms"] / (dt_prof * 1e3), 3),
     }
+    line["latency"] = small_batch_latency(model)
     model.close()
     if not a.no_search:
         line["tokenizer"] = tokenizer_leg()

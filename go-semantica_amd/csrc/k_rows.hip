@@ -569,14 +569,20 @@ __global__ __launch_bounds__(kThreads) void k_pool_mean(float* __restrict__ out,
 }
 
 // l2Normalize (runtime/model.go:808-820) of each pooled row in place: serial
-// fp32 sum of squares, n = sqrt, v / n; an all-zero row is left as is.
+// fp32 sum of squares, n = sqrt, v / n; an all-zero row is left as is.  The
+// row is staged in LDS with coalesced loads so the one thread that runs the
+// serial sum reads LDS, not a chain of global loads.
+constexpr int kL2MaxDim = 1024;
 __global__ __launch_bounds__(kThreads) void k_l2_rows(float* __restrict__ out, int out_dim) {
+  __shared__ float row[kL2MaxDim];
   __shared__ float nrm;
   float* v = out + (int64_t)blockIdx.x * out_dim;
+  for (int c = threadIdx.x; c < out_dim; c += kThreads) row[c] = v[c];
+  __syncthreads();
   if (threadIdx.x == 0) {
     float ss = 0.0f;
     for (int c = 0; c < out_dim; c++) {
-      const float t = v[c] * v[c];
+      const float t = row[c] * row[c];
       ss = ss + t;
     }
     nrm = ss == 0.0f ? 0.0f : sg_sqrt(ss);
@@ -584,7 +590,7 @@ __global__ __launch_bounds__(kThreads) void k_l2_rows(float* __restrict__ out, i
   __syncthreads();
   const float n = nrm;
   if (n != 0.0f)
-    for (int c = threadIdx.x; c < out_dim; c += kThreads) v[c] = v[c] / n;
+    for (int c = threadIdx.x; c < out_dim; c += kThreads) v[c] = row[c] / n;
 }
 
 inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
@@ -743,7 +749,7 @@ hipError_t gelu_mul(float* g, int ldd, const float* gate, int ldg, const float* 
 hipError_t pool_l2(float* out, const float* x, int ldx, int out_dim, const int32_t* seq_off, int n_seq,
                    hipStream_t s) {
   if (n_seq <= 0) return hipSuccess;
-  if (out_dim > 1024) return hipErrorInvalidValue;
+  if (out_dim > kL2MaxDim) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_pool_mean, dim3(n_seq, blocks_for(out_dim, kPoolCols)), dim3(kThreads), 0, s, out, x, ldx,
                      out_dim, seq_off);
   hipLaunchKernelGGL(k_l2_rows, dim3(n_seq), dim3(kThreads), 0, s, out, out_dim);
