@@ -187,6 +187,49 @@ def small_batch_latency(model, shapes=((1, 32), (8, 32), (1, 512), (8, 512)), re
     return res
 
 
+C1_SHAPES = (("Q/O", 768, 768), ("K/V", 256, 768), ("gate/up", 1152, 768), ("down", 768, 1152),
+             ("3072x768", 3072, 768), ("768x3072", 768, 3072))
+
+
+def gemm_c1_leg(ctx, m=2048, reps=50):
+    """Config 1: the isolated Q8_0 GEMMs at the model's layer shapes with M = 2048
+    rows, through sg_matmul_q8_0_int8 (the kernel seam: int8 activations in,
+    fp32 out, including the operand relayout it performs).  Back-to-back calls on
+    one stream between two HIP events, so launch gaps do not dominate.  Work =
+    2*M*N*K int8 ops; bytes = int8 A + Q8_0 W (34/32 B per weight) + fp32 Y +
+    fp32 row scales, each once."""
+    import numpy as np
+    import torch
+    from semantica_gpu import kernels, synth
+    rng = np.random.default_rng(3)
+    stream = torch.cuda.Stream()
+    res = []
+    for name, n, k in C1_SHAPES:
+        w = kernels.Q8Weight(ctx, synth.q8_0_random(rng, n, k), n, k)
+        xf = rng.standard_normal((m, k)).astype(np.float32)
+        x = torch.from_numpy(np.clip(np.round(xf * (127.0 / np.abs(xf).max())), -127, 127).astype(np.int8)).cuda()
+        rs = torch.full((m,), 0.01, dtype=torch.float32, device="cuda")
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()  # inputs made on the default stream are complete
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                kernels.matmul_q8_0(ctx, y, w, x, rs, stream=stream.cuda_stream)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(reps):
+                kernels.matmul_q8_0(ctx, y, w, x, rs, stream=stream.cuda_stream)
+            e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        ops, nbytes = 2.0 * m * n * k, m * k + n * k * 34 / 32 + m * n * 4 + m * 4
+        res.append({"gemm": name, "N": n, "K": k, "us": round(us, 2), "TOPS_int8": round(ops / us / 1e6, 1),
+                    "frac_int8_peak": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
+                    "GB_s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+        w.close()
+    return {"workload": f"config 1: isolated Q8_0 GEMMs, M = {m}, seed-random Q8_0 weights, {reps} back-to-back calls",
+            "shapes": res}
+
+
 def tokenizer_leg(n_texts=64, chars=2000):
     """The host tokenizer (sg_tokenizer_*, internal/tokenizer) on a synthetic
     262,144-token vocabulary (the real one is not available offline): texts of
@@ -342,6 +385,7 @@ def main():
         "gemm_frac_of_step": round(g["ms"] / (dt_prof * 1e3), 3),
     }
     line["latency"] = small_batch_latency(model)
+    line["gemm_c1"] = gemm_c1_leg(ctx)
     model.close()
     if not a.no_search:
         line["tokenizer"] = tokenizer_leg()

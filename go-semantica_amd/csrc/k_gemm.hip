@@ -577,27 +577,39 @@ __global__ __launch_bounds__(NW* SG_WAVE) void k_gemm_q8_sp(const _Float16* __re
   gemm_epilogue<NW, TM, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
 }
 
-// Direct-to-LDS variant.  Workgroup: 8 waves x 32 rows = 256 rows, 32*TN
-// columns.  Every K-block's A tile (each wave's own 32 rows), weight tile and
-// scales are copied global -> LDS by global_load_lds_dwordx4/dword (no
-// staging registers) into a ring of STAGES buffers, STAGES-1 blocks ahead.
-// Each wave issues exactly 4 copies per block (clamped, redundant past the
-// last block) so one constant s_waitcnt vmcnt covers "this wave's copies of
-// block b have landed"; a bare s_barrier then publishes every wave's copies.
-// (__syncthreads' fence would wait for all copies in flight.)  Rows are
-// stored in 64-byte lines with the 16-byte chunks XOR-swizzled by row, so
+// Direct-to-LDS variant.  Workgroup: NW waves x 32 rows, 32*TN columns.
+// Every K-block's A tile (each wave's own 32 rows), weight tile and scales are
+// copied global -> LDS by global_load_lds_dwordx4/dword (no staging
+// registers) into a ring of STAGES buffers, STAGES-1 blocks ahead.  Each wave
+// issues the same number of copies per block, CPB (clamped, redundant past
+// the last block), so one constant s_waitcnt vmcnt covers "this wave's copies
+// of block b have landed"; a bare s_barrier then publishes every wave's
+// copies.  (__syncthreads' fence would wait for all copies in flight.)  Rows
+// are stored in 64-byte lines with the 16-byte chunks XOR-swizzled by row, so
 // fragment reads are conflict-free; the swizzle is applied by choosing which
-// global chunk each lane copies.
-template <int TN, bool GELU, int STAGES>
-__global__ __launch_bounds__(512, 4) void k_gemm_q8_dl(const _Float16* __restrict__ A, int a_rows,
-                                                   const _Float16* __restrict__ W, const float* __restrict__ St,
-                                                   const float* __restrict__ row_scale, float* __restrict__ Y, int M,
-                                                   int N, int K, const int32_t* __restrict__ row_seq,
-                                                   float* __restrict__ amax) {
-  constexpr int NW = 8, BN = TN * 32;
+// global chunk each lane copies.  Large M uses 8 waves, 4 subtiles, 3 stages
+// (two workgroups per CU); small M uses small workgroups with a deep ring, as
+// its K loop is bound by copy latency, not by throughput.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int NW, int TN, bool GELU, int STAGES>
+__global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_dl(
+    const _Float16* __restrict__ A, int a_rows, const _Float16* __restrict__ W, const float* __restrict__ St,
+    const float* __restrict__ row_scale, float* __restrict__ Y, int M, int N, int K,
+    const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
+  constexpr int BN = TN * 32;
   constexpr int A_BYTES = NW * 32 * 64, W_BYTES = BN * 64, S_BYTES = BN * 4;
   constexpr int STAGE = A_BYTES + W_BYTES + S_BYTES;
-  static_assert(STAGES >= 3 && STAGES <= 4, "wait counts below cover 3 or 4 stages");
+  constexpr int WROWS = BN / NW;               // weight rows each wave copies (64 B each)
+  constexpr int WCOPIES = (WROWS + 15) / 16;   // 1-KB copies per wave for them
+  constexpr int SLANES = BN / NW;              // scales each wave copies
+  constexpr int CPB = 2 + WCOPIES + 1;         // copies per wave per K-block
+  static_assert(BN % NW == 0 && SLANES <= SG_WAVE, "weight tile split over the waves");
+  static_assert(STAGES >= 3 && (STAGES - 2) * CPB <= 63, "vmcnt covers the copies in flight");
   __shared__ __attribute__((aligned(16))) unsigned char lds[STAGES * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -618,25 +630,30 @@ __global__ __launch_bounds__(512, 4) void k_gemm_q8_dl(const _Float16* __restric
     asrc[j] = A + (int64_t)(mw + r) * 32 + 8 * swz(r, lane & 3);
   }
   const int64_t a_bstride = (int64_t)a_rows * 32;
-  // W: 4*TN rows per wave (16*TN active lanes), lane -> row 4*TN*wave + lane/4.
-  constexpr int WLANES = 16 * TN;
-  const int wr = 4 * TN * wave + (lane >> 2);
-  const _Float16* wsrc = W + (int64_t)min(n0 + wr, N - 1) * 32 + 8 * swz(wr, lane & 3);
+  // W: WROWS rows per wave, copy j -> rows WROWS*wave + 16j + lane/4.
+  const _Float16* wsrc[WCOPIES];
+#pragma unroll
+  for (int j = 0; j < WCOPIES; j++) {
+    const int wr = WROWS * wave + 16 * j + (lane >> 2);
+    wsrc[j] = W + (int64_t)min(n0 + wr, N - 1) * 32 + 8 * swz(wr, lane & 3);
+  }
   const int64_t w_bstride = (int64_t)N * 32;
-  // Scales: 4*TN per wave.
-  constexpr int SLANES = 4 * TN;
   const float* ssrc = St + min(n0 + SLANES * wave + lane, N - 1);
 
   auto issue = [&](int b, int st) {
     unsigned char* base = lds + st * STAGE;
 #pragma unroll
     for (int j = 0; j < 2; j++)
-      __builtin_amdgcn_global_load_lds(asrc[j] + b * a_bstride, base + wave * 2048 + j * 1024, 16, 0, 0);
-    if (lane < WLANES)
-      __builtin_amdgcn_global_load_lds(wsrc + b * w_bstride, base + A_BYTES + wave * (WLANES * 16), 16, 0, 0);
-    if (lane < SLANES)
-      __builtin_amdgcn_global_load_lds(ssrc + (int64_t)b * N, base + A_BYTES + W_BYTES + wave * (SLANES * 4), 4, 0,
+      __builtin_amdgcn_global_load_lds((const void*)(asrc[j] + b * a_bstride), base + wave * 2048 + j * 1024, 16, 0,
                                        0);
+#pragma unroll
+    for (int j = 0; j < WCOPIES; j++)
+      if (16 * j + (lane >> 2) < WROWS)
+        __builtin_amdgcn_global_load_lds((const void*)(wsrc[j] + b * w_bstride),
+                                         base + A_BYTES + WROWS * 64 * wave + j * 1024, 16, 0, 0);
+    if (lane < SLANES)
+      __builtin_amdgcn_global_load_lds((const void*)(ssrc + (int64_t)b * N),
+                                       base + A_BYTES + W_BYTES + wave * (SLANES * 4), 4, 0, 0);
   };
 
   f32x16_t acc[1][TN];
@@ -650,10 +667,7 @@ __global__ __launch_bounds__(512, 4) void k_gemm_q8_dl(const _Float16* __restric
   const f32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
   for (int b = 0; b < nb; b++) {
     const int st = b % STAGES;
-    if constexpr (STAGES == 3)
-      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    wait_vmcnt<(STAGES - 2) * CPB>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     issue(min(b + STAGES - 1, nb - 1), (b + STAGES - 1) % STAGES);
@@ -679,15 +693,15 @@ __global__ __launch_bounds__(512, 4) void k_gemm_q8_dl(const _Float16* __restric
   gemm_epilogue<NW, 1, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
 }
 
-template <int TN, bool GELU = false, int STAGES = 3>
+template <int NW, int TN, bool GELU, int STAGES>
 hipError_t launch_dl(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
                      int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
-  constexpr int BM = 256, BN = TN * 32;
+  constexpr int BM = NW * 32, BN = TN * 32;
   const int gm = (M + BM - 1) / BM;
   if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
   dim3 grid((N + BN - 1) / BN, gm);
-  hipLaunchKernelGGL((k_gemm_q8_dl<TN, GELU, STAGES>), grid, dim3(512), 0, s, A, a_rows, W, St, rs, Y, M, N, K,
-                     row_seq, amax);
+  hipLaunchKernelGGL((k_gemm_q8_dl<NW, TN, GELU, STAGES>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y,
+                     M, N, K, row_seq, amax);
   return hipGetLastError();
 }
 
@@ -727,6 +741,9 @@ hipError_t launch(const _Float16* A, int a_rows, const _Float16* W, const float*
   return hipGetLastError();
 }
 
+// Workgroups of the 8-wave direct-to-LDS launch.
+inline int64_t dl8_blocks(int M, int N) { return (int64_t)((M + 255) / 256) * ((N + 127) / 128); }
+
 }  // namespace
 
 namespace sgk {
@@ -736,11 +753,13 @@ hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float
   if (M <= 0 || N <= 0) return hipSuccess;
   if (K <= 0 || K % 32) return hipErrorInvalidValue;
   if (sums) return launch<1, 1, 1, 1, true>(A, a_rows, W, St, row_scale, Y, sums, M, N, K, s);
-  // Large M: direct-to-LDS workgroups of 8 waves (256 rows x 128 columns,
-  // 3-stage copy ring).  Small M: 64x64 register-direct tiles so the grid
-  // still covers the 256 compute units (tile sweeps on MI355X at the model's
-  // shapes).
-  if (M >= 8192) return launch_dl<4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+  // Direct-to-LDS workgroups of 8 waves (256 rows x 128 columns, 3-stage
+  // copy ring) once they cover half the compute units; below that, from 4096
+  // rows, 4 waves x 64 columns with a 6-stage ring; otherwise 64x64
+  // register-direct tiles, whose grid still covers the chip (tile sweeps on
+  // MI355X at the model's shapes, M = 32 .. 4096).
+  if (M >= 8192 || dl8_blocks(M, N) >= 128) return launch_dl<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+  if (M >= 4096) return launch_dl<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   return launch<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
 }
 
@@ -749,7 +768,8 @@ hipError_t gemm_q8_gelu(const _Float16* A, int a_rows, const _Float16* W, const 
   if (M <= 0 || Nh <= 0) return hipSuccess;
   if (K <= 0 || K % 32 || Nh % 32) return hipErrorInvalidValue;
   if (amax && !row_seq) return hipErrorInvalidValue;
-  if (M >= 8192) return launch_dl<4, true, 3>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
+  if (M >= 8192 || dl8_blocks(M, 2 * Nh) >= 128)
+    return launch_dl<8, 4, true, 3>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
   return launch_sp<4, 1, 2, true>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
 }
 

@@ -61,6 +61,27 @@ __global__ void k_i8_to_f16_blocked(const int8_t* __restrict__ x, int M, int K, 
   y[((int64_t)(k >> 5) * a_rows + m) * 32 + (k & 31)] = (_Float16)(float)x[i];
 }
 
+// 16 consecutive k of one row per thread: one 16-byte load, two 16-byte
+// stores into the row's 64-byte piece of K-block k/32.
+__global__ void k_i8_to_f16_blocked16(const int8_t* __restrict__ x, int M, int K, _Float16* __restrict__ y,
+                                      int a_rows) {
+  const int kc16 = K >> 4;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)M * kc16) return;
+  const int m = (int)(i / kc16), kc = (int)(i % kc16) << 4;
+  typedef int8_t i8x16_t __attribute__((ext_vector_type(16)));
+  const i8x16_t v = *reinterpret_cast<const i8x16_t*>(x + (int64_t)m * K + kc);
+  half8_t lo, hi;
+#pragma unroll
+  for (int t = 0; t < 8; t++) {
+    lo[t] = (_Float16)(float)v[t];
+    hi[t] = (_Float16)(float)v[8 + t];
+  }
+  _Float16* d = y + ((int64_t)(kc >> 5) * a_rows + m) * 32 + (kc & 31);
+  *reinterpret_cast<half8_t*>(d) = lo;
+  *reinterpret_cast<half8_t*>(d + 8) = hi;
+}
+
 __global__ void k_fill(float* __restrict__ p, float v, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = v;
@@ -618,6 +639,10 @@ hipError_t i8_to_f16_blocked(const int8_t* x, int M, int K, _Float16* y, int a_r
   const int64_t n = (int64_t)M * K;
   if (n <= 0) return hipSuccess;
   if (K % 32 || a_rows < M) return hipErrorInvalidValue;
+  if (K % 32 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    hipLaunchKernelGGL(k_i8_to_f16_blocked16, dim3(blocks_for(n / 16, 256)), dim3(256), 0, s, x, M, K, y, a_rows);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(k_i8_to_f16_blocked, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, M, K, y, a_rows);
   return hipGetLastError();
 }

@@ -192,6 +192,10 @@ struct sg_ctx {
   std::mutex mu;  // guards the scratch below for the kernel seam
   HostBuf meta_h;
   DevBuf meta_d, f16, amax, tab, split;
+  // Last use of f16 / split by an asynchronous GEMM call (sg_matmul_q8_0_int8,
+  // sg_ffn_gate_up): the next such call waits for it on its own stream.
+  hipEvent_t gemm_done = nullptr;
+  bool gemm_pending = false;
 };
 
 namespace sgi {
@@ -218,6 +222,21 @@ struct LayerDev {
 };
 
 hipStream_t pick(sg_ctx* c, void* stream) { return stream ? static_cast<hipStream_t>(stream) : c->stream; }
+
+// The asynchronous GEMM seam shares the context's operand scratch: a call
+// orders its stream after the previous call's last use (GPU-side, no host
+// wait) and marks its own.  Growing a scratch buffer frees the old one, and
+// hipFree waits for the device, so a reallocation never pulls memory from
+// under work in flight.
+int gemm_scratch_begin(sg_ctx* c, hipStream_t s) {
+  if (c->gemm_pending) SG_HIP(hipStreamWaitEvent(s, c->gemm_done, 0));
+  return SG_OK;
+}
+int gemm_scratch_end(sg_ctx* c, hipStream_t s) {
+  SG_HIP(hipEventRecord(c->gemm_done, s));
+  c->gemm_pending = true;
+  return SG_OK;
+}
 
 int set_device(sg_ctx* c) {
   SG_HIP(hipSetDevice(c->device));
@@ -518,6 +537,11 @@ int sg_init(int device_ordinal, sg_ctx** out) {
     delete c;
     return fail(SG_ERR_DEVICE, "hipStreamCreate failed");
   }
+  if (hipEventCreateWithFlags(&c->gemm_done, hipEventDisableTiming) != hipSuccess) {
+    (void)hipStreamDestroy(c->stream);
+    delete c;
+    return fail(SG_ERR_DEVICE, "hipEventCreateWithFlags failed");
+  }
   *out = c;
   return SG_OK;
 }
@@ -532,6 +556,7 @@ void sg_shutdown(sg_ctx* c) {
   c->amax.release();
   c->tab.release();
   c->split.release();
+  (void)hipEventDestroy(c->gemm_done);
   (void)hipStreamDestroy(c->stream);
   delete c;
 }
@@ -750,8 +775,9 @@ static int matmul_common(sg_ctx* ctx, float* dst, int32_t* sums, const sg_q8_wei
   hipStream_t s = pick(ctx, stream);
   const int ar = sgk::gemm_pad_rows(batch);
   SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)ar * w->K));
+  SG_TRY(gemm_scratch_begin(ctx, s));
   SG_HIP(sgk::i8_to_f16_blocked(x, batch, w->K, ctx->f16.as<_Float16>(), ar, s));
-  if (sums) {
+  if (sums) {  // parity dump: synchronous (a temporary output buffer)
     SG_TRY(ctx->amax.ensure(sizeof(float) * (size_t)batch));
     float* ones = ctx->amax.as<float>();
     SG_HIP(sgk::fill_f32(ones, 1.0f, batch, s));
@@ -767,8 +793,7 @@ static int matmul_common(sg_ctx* ctx, float* dst, int32_t* sums, const sg_q8_wei
   }
   if (!row_scale) return fail(SG_ERR_INVALID, "row_scale is NULL");
   SG_HIP(sgk::gemm_q8(ctx->f16.as<_Float16>(), ar, w->w, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s));
-  SG_HIP(hipStreamSynchronize(s));
-  return SG_OK;
+  return gemm_scratch_end(ctx, s);
 }
 
 int sg_matmul_q8_0_int8(sg_ctx* ctx, float* dst, const sg_q8_weight* w, const int8_t* x, const float* row_scale,
@@ -797,18 +822,18 @@ int sg_ffn_gate_up(sg_ctx* ctx, float* dst, const sg_q8_weight* w_gate, const sg
   const size_t wch = (size_t)sgk::kGeluGroup * 32 * sizeof(_Float16), sch = sgk::kGeluGroup * sizeof(float);
   const size_t nch = (size_t)(K / 32) * (N / sgk::kGeluGroup);
   SG_TRY(ctx->split.ensure(2 * nch * (wch + sch)));
+  SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)ar * K));
   uint8_t* wi = ctx->split.as<uint8_t>();
   uint8_t* si = wi + 2 * nch * wch;
+  SG_TRY(gemm_scratch_begin(ctx, s));
   SG_HIP(hipMemcpy2DAsync(wi, 2 * wch, w_gate->w, wch, wch, nch, hipMemcpyDeviceToDevice, s));
   SG_HIP(hipMemcpy2DAsync(wi + wch, 2 * wch, w_up->w, wch, wch, nch, hipMemcpyDeviceToDevice, s));
   SG_HIP(hipMemcpy2DAsync(si, 2 * sch, w_gate->st, sch, sch, nch, hipMemcpyDeviceToDevice, s));
   SG_HIP(hipMemcpy2DAsync(si + sch, 2 * sch, w_up->st, sch, sch, nch, hipMemcpyDeviceToDevice, s));
-  SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)ar * K));
   SG_HIP(sgk::i8_to_f16_blocked(x, batch, K, ctx->f16.as<_Float16>(), ar, s));
   SG_HIP(sgk::gemm_q8_gelu(ctx->f16.as<_Float16>(), ar, reinterpret_cast<const _Float16*>(wi),
                            reinterpret_cast<const float*>(si), row_scale, dst, batch, N, K, nullptr, nullptr, s));
-  SG_HIP(hipStreamSynchronize(s));
-  return SG_OK;
+  return gemm_scratch_end(ctx, s);
 }
 
 int sg_rmsnorm(sg_ctx* ctx, float* dst, const float* src, const float* weight, int32_t rows, int32_t n, float eps,
@@ -863,6 +888,7 @@ int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const flo
   // Split operands as the forward's producers write them.
   const size_t T = (size_t)meta.T, qd = (size_t)n_heads * head_dim, kvd = (size_t)n_kv_heads * head_dim;
   SG_TRY(ctx->split.ensure(2 * sizeof(_Float16) * (T * qd + T * kvd + kvd * (size_t)meta.Tp)));
+  SG_TRY(gemm_scratch_begin(ctx, s));  // split is shared with sg_ffn_gate_up
   _Float16* qs_h = ctx->split.as<_Float16>();
   _Float16* qs_l = qs_h + T * qd;
   _Float16* ks_h = qs_l + T * qd;

@@ -161,7 +161,13 @@ typedef struct sg_profile {
 int sg_profile_enable(sg_model *model, int on);
 int sg_profile_read(sg_model *model, sg_profile *out);
 
-/* ---- kernel seam (device pointers, asynchronous on `stream`) ------------ */
+/* ---- kernel seam (device pointers, work on `stream`) ---------------------
+ * sg_matmul_q8_0_int8 and sg_ffn_gate_up are asynchronous: they return once
+ * their work is enqueued on `stream`.  They share the context's operand
+ * scratch, so each is ordered on the GPU after the previous one of the same
+ * context (an event; no host wait), whatever streams they use.  The other
+ * calls (they read host-side seq_offsets, or dump into temporary buffers)
+ * return after their work on `stream` has completed. */
 
 /* Repacks one raw Q8_0 matrix [out_dim][in_dim/32][34 B] (host pointer) into
  * the device layout used by the GEMM.  in_dim must be a multiple of 32.

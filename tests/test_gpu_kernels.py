@@ -75,7 +75,7 @@ def test_gemm_fp32_config1(gpu_ctx, oracle, N, K):
     assert rel_err(got, avx2) <= 1e-5
 
 
-@pytest.mark.parametrize("M", [1, 33, 2048, 8200])
+@pytest.mark.parametrize("M", [1, 33, 2048, 4500, 8200])
 def test_ffn_gate_up_fused_bit_exact(gpu_ctx, oracle, M):
     """The fused gate/up GEMM with GELUQuick * up in its epilogue equals the
     unfused GEMMs followed by the GELU kernel bit for bit, and the first rows
@@ -128,13 +128,15 @@ def test_gemm_ragged_m_and_extremes(gpu_ctx, oracle):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("M", [4500, 8200])
 @pytest.mark.parametrize("N,K", [(1280, 768), (768, 1152)])
-def test_gemm_large_m(gpu_ctx, oracle, N, K):
-    """The large-M kernel (M >= 8192, ragged last tile): first and last rows
-    bit-exact to the block-serial order, every row within 1e-5 of AVX2's."""
+def test_gemm_large_m(gpu_ctx, oracle, M, N, K):
+    """The direct-to-LDS kernels (8 waves x 128 columns at M = 8200 and at
+    4500 x 1280; 4 waves x 64 columns with a 6-stage ring at 4500 x 768;
+    ragged last tiles): first and last rows bit-exact to the block-serial
+    order, every row within 1e-5 of AVX2's."""
     import torch
     from semantica_gpu import kernels, synth
-    M = 8200
     rng = np.random.default_rng(N + K)
     say(f"gemm large M={M} N={N} K={K}")
     raw = synth.q8_0_random(rng, N, K)
