@@ -131,12 +131,13 @@ __global__ __launch_bounds__(kThreads) void k_embed_norm(const int32_t* __restri
 #pragma unroll
     for (int i = 0; i < NPL; i++) hr[8 * i + j] = x[i];
     sg_rmsnorm8<NPL>(x, w, j, eps);
-    float* yr = xn + (int64_t)row * D;
+    if (xn) {
+      float* yr = xn + (int64_t)row * D;
 #pragma unroll
-    for (int i = 0; i < NPL; i++) {
-      yr[8 * i + j] = x[i];
-      m = fmaxf(m, fabsf(x[i]));
+      for (int i = 0; i < NPL; i++) yr[8 * i + j] = x[i];
     }
+#pragma unroll
+    for (int i = 0; i < NPL; i++) m = fmaxf(m, fabsf(x[i]));
   }
   if (amax) {
     m = sg_max8(m);

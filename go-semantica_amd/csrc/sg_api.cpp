@@ -412,19 +412,15 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
 
   SG_LAUNCH(SG_K_OTHER, 4.0 * 4 * L * ns, sgk::fill_f32(amax, 0.0f, (int64_t)4 * L * ns, s));
   SG_LAUNCH(SG_K_OTHER, 4.0, sgk::fill_f32(m->err.as<float>(), 0.0f, 1, s));
-  SG_LAUNCH(SG_K_NORM, t * (34.0 * d / 32 + 8.0 * d),
+  SG_LAUNCH(SG_K_NORM, t * (34.0 * d / 32 + 4.0 * d),
             sgk::embed_norm(d_tokens, T, m->emb_q, m->emb_s, c.vocab_size, d, m->sqrt_d, m->layers[0].attn_norm,
-                            eps, meta.row_seq, h, xn, site(0, 0), m->err.as<int32_t>(), s));
+                            eps, meta.row_seq, h, nullptr, site(0, 0), m->err.as<int32_t>(), s));
   for (int l = 0; l < L; l++) {
     if (l == stop) break;
     const LayerDev& ly = m->layers[l];
-    if (l == 0) {
-      SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d),
-                sgk::quantize(xn, d, T, d, meta.row_seq, site(l, 0), a16, ar, nullptr, sx, s));
-    } else {  // xn of this layer's pre-norm was never stored: recomputed from h
-      SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d),
-                sgk::norm_quantize(h, ly.attn_norm, eps, T, d, meta.row_seq, site(l, 0), a16, ar, sx, s));
-    }
+    // The pre-norm's output xn is never stored: recomputed from h while quantizing.
+    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d),
+              sgk::norm_quantize(h, ly.attn_norm, eps, T, d, meta.row_seq, site(l, 0), a16, ar, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), sgk::gemm_q8(a16, ar, ly.wqkv, ly.sqkv, sx, qkv, nullptr, T, nqkv, d, s));
     SG_LAUNCH(SG_K_NORM, t * (qd + kvd) * 8.0,
               sgk::qknorm_rope(qkv, nqkv, qkv + qd, nqkv, ly.q_norm, ly.k_norm, c.num_heads, c.num_kv_heads, T,

@@ -31,7 +31,8 @@ hipError_t i8_to_f16_blocked(const int8_t* x, int M, int K, _Float16* y, int a_r
 hipError_t fill_f32(float* p, float v, int64_t n, hipStream_t s);
 
 // ---- per-row kernels (k_rows.hip) ----
-// Embedding gather * sqrt(d) -> h; then RMSNorm(w) -> xn and per-sequence max|xn| -> amax.
+// Embedding gather * sqrt(d) -> h; then RMSNorm(w) -> xn (stored when xn != null) and
+// per-sequence max|xn| -> amax.
 hipError_t embed_norm(const int32_t* tokens, int T, const int8_t* eq, const float* es, int vocab, int d,
                       float sqrt_d, const float* w, float eps, const int32_t* row_seq, float* h, float* xn,
                       float* amax, int32_t* err, hipStream_t s);
