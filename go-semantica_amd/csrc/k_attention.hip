@@ -70,12 +70,17 @@ __device__ __forceinline__ f32x4_t mfma16(half8_t a, half8_t b, f32x4_t c) {
 // and position p holds key:
 __device__ __forceinline__ int vt_key(int p) { return ((p & 4) << 2) | ((p & 24) >> 1) | (p & 3); }
 
+// QPRE: Q arrives as the QKV GEMM's fp32 output and each wave applies
+// attn_q_norm and RoPE to its 16 rows itself (the arithmetic of
+// k_qknorm_rope_split, so the operands are bit-identical), which saves writing
+// Q's hi/lo operands and reading them back.
+template <bool QPRE>
 __global__ __launch_bounds__(kNT, 2) void k_attn(
     const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
     const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vth, const _Float16* __restrict__ vtl,
     int ldvt, float* __restrict__ out, int ldo, const int32_t* __restrict__ seq_off,
     const int32_t* __restrict__ voff, const sg_item* __restrict__ items, int G, float sscale,
-    float* __restrict__ amax) {
+    float* __restrict__ amax, sg_attn_qpre qp) {
   __shared__ _Float16 Ks[2][kBK][kKStride];  // [hi/lo][key][dim]
   __shared__ _Float16 Vs[2][kHD][kVStride];  // [hi/lo][dim][key, vt_key order]
   __shared__ float red[kWaves];
@@ -98,8 +103,93 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
 
   // Q^T as the B operand: lane (query ln, group g4), k-step c: dims 32c+8g4..+8.
   half8_t bqh[kHD / 32], bql[kHD / 32];
-  {
-    const int64_t qo = (int64_t)(r0 + min(qrow, S - 1)) * ldq + head * kHD + 8 * g4;
+  const int qr = r0 + min(qrow, S - 1);
+  if constexpr (QPRE) {
+    // Lane (ln, g4) holds elements e = 32ks + 8g4 + t of row ln.
+    float x[kHD / 32][8];
+    const float* src = qp.q + (int64_t)qr * qp.ldq + head * kHD + 8 * g4;
+#pragma unroll
+    for (int ks = 0; ks < kHD / 32; ks++) {
+      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src + 32 * ks);
+      const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + 32 * ks + 4);
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        x[ks][t] = a[t];
+        x[ks][4 + t] = b[t];
+      }
+    }
+    if (qp.w) {
+      // RMSNorm's sum of squares in the AVX2 lane order (sg_rmsnorm8): lane v
+      // of a row chains element 8i + v over i.  Element e sits at i = 4ks + g4,
+      // v = t here, so each 32-element chunk goes through a 16 x 40-float LDS
+      // tile of this wave (inside Ks, which nothing uses before the first
+      // barrier below); lane (row rA or rA + 8, v) then reads the chunk's
+      // elements 8k + v, k = 0..3, in order.
+      float* tile = reinterpret_cast<float*>(&Ks[0][0][0]) + w * (16 * 40);
+      const int v = lane & 7, rA = lane >> 3;
+      float accA = 0.0f, accB = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < kHD / 32; ks++) {
+        asm volatile("" ::: "memory");
+        *reinterpret_cast<f32x4_t*>(tile + ln * 40 + 8 * g4) = f32x4_t{x[ks][0], x[ks][1], x[ks][2], x[ks][3]};
+        *reinterpret_cast<f32x4_t*>(tile + ln * 40 + 8 * g4 + 4) = f32x4_t{x[ks][4], x[ks][5], x[ks][6], x[ks][7]};
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const float a = tile[rA * 40 + 8 * k + v];
+          accA = __builtin_fmaf(a, a, accA);
+          const float b = tile[(rA + 8) * 40 + 8 * k + v];
+          accB = __builtin_fmaf(b, b, accB);
+        }
+      }
+      asm volatile("" ::: "memory");
+      const float invA = 1.0f / sg_sqrt(sg_hsum8(accA) / (float)kHD + qp.eps);
+      const float invB = 1.0f / sg_sqrt(sg_hsum8(accB) / (float)kHD + qp.eps);
+      const float iA = __shfl(invA, 8 * (ln & 7)), iB = __shfl(invB, 8 * (ln & 7));
+      const float inv = ln < 8 ? iA : iB;
+#pragma unroll
+      for (int ks = 0; ks < kHD / 32; ks++) {
+        const f32x4_t wa = *reinterpret_cast<const f32x4_t*>(qp.w + 32 * ks + 8 * g4);
+        const f32x4_t wb = *reinterpret_cast<const f32x4_t*>(qp.w + 32 * ks + 8 * g4 + 4);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const float u = x[ks][t] * inv;
+          x[ks][t] = u * wa[t];
+          const float u2 = x[ks][4 + t] * inv;
+          x[ks][4 + t] = u2 * wb[t];
+        }
+      }
+    }
+    // RoPE (rope_cache.go:85-104): pairs (e, e + 128) are chunks ks and ks + 4
+    // of the same lane and slot.
+    const int pos = qp.row_pos[qr];
+    const float* cr = qp.cos_t + (int64_t)pos * (kHD / 2) + 8 * g4;
+    const float* sr = qp.sin_t + (int64_t)pos * (kHD / 2) + 8 * g4;
+#pragma unroll
+    for (int ks = 0; ks < kHD / 64; ks++) {
+      float cv[8], sv[8];
+      *reinterpret_cast<f32x4_t*>(cv) = *reinterpret_cast<const f32x4_t*>(cr + 32 * ks);
+      *reinterpret_cast<f32x4_t*>(cv + 4) = *reinterpret_cast<const f32x4_t*>(cr + 32 * ks + 4);
+      *reinterpret_cast<f32x4_t*>(sv) = *reinterpret_cast<const f32x4_t*>(sr + 32 * ks);
+      *reinterpret_cast<f32x4_t*>(sv + 4) = *reinterpret_cast<const f32x4_t*>(sr + 32 * ks + 4);
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const float v0 = x[ks][t], v1 = x[ks + kHD / 64][t];
+        const float a = v0 * cv[t], b = v1 * sv[t], cc = v0 * sv[t], dd = v1 * cv[t];
+        x[ks][t] = a - b;
+        x[ks + kHD / 64][t] = cc + dd;
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < kHD / 32; ks++)
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const hl16 sp = split_f16(x[ks][t] * kQKScale);
+        bqh[ks][t] = sp.hi;
+        bql[ks][t] = sp.lo;
+      }
+  } else {
+    const int64_t qo = (int64_t)qr * ldq + head * kHD + 8 * g4;
 #pragma unroll
     for (int ks = 0; ks < kHD / 32; ks++) {
       bqh[ks] = *reinterpret_cast<const half8_t*>(qh + qo + 32 * ks);
@@ -355,13 +445,23 @@ hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, 
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
                      const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
-                     float* amax, hipStream_t s) {
+                     float* amax, hipStream_t s, const sg_attn_qpre* qpre) {
   if (n_items <= 0) return hipSuccess;
   if (hd != kHD || HKV <= 0 || H % HKV) return hipErrorInvalidValue;
-  if ((ldq | ldk | ldvt) & 7 || (ldo & 3)) return hipErrorInvalidValue;
+  if ((ldk | ldvt) & 7 || (ldo & 3)) return hipErrorInvalidValue;
   const float sscale = scale / (kQKScale * kQKScale);
-  hipLaunchKernelGGL(k_attn, dim3(n_items, HKV), dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vth, vtl,
-                     ldvt, out, ldo, seq_off, voff, items, H / HKV, sscale, amax);
+  if (qpre) {
+    if (!qpre->q || !qpre->cos_t || !qpre->sin_t || !qpre->row_pos || (qpre->ldq & 3) ||
+        (reinterpret_cast<uintptr_t>(qpre->q) & 15) || (reinterpret_cast<uintptr_t>(qpre->w) & 15) ||
+        (reinterpret_cast<uintptr_t>(qpre->cos_t) & 15) || (reinterpret_cast<uintptr_t>(qpre->sin_t) & 15))
+      return hipErrorInvalidValue;  // float4 loads of Q rows, weights and table rows
+    hipLaunchKernelGGL(k_attn<true>, dim3(n_items, HKV), dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vth, vtl, ldvt,
+                       out, ldo, seq_off, voff, items, H / HKV, sscale, amax, *qpre);
+  } else {
+    if (ldq & 7) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_attn<false>, dim3(n_items, HKV), dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vth, vtl, ldvt,
+                       out, ldo, seq_off, voff, items, H / HKV, sscale, amax, sg_attn_qpre{});
+  }
   return hipGetLastError();
 }
 

@@ -740,10 +740,13 @@ hipError_t qknorm_rope(float* q, int ldq, float* k, int ldk, const float* qw, co
                        const int32_t* row_pos, const float* cos_t, const float* sin_t, float eps, _Float16* qs_h,
                        _Float16* qs_l, int ldqs, _Float16* ks_h, _Float16* ks_l, int ldks, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  if (qs_h && (!qs_l || !ks_h || !ks_l)) return hipErrorInvalidValue;
+  const bool split = ks_h != nullptr;
+  if (split && (!ks_l || (H > 0 && (!qs_h || !qs_l)))) return hipErrorInvalidValue;
   const int64_t groups = (int64_t)T * (H + HKV);
-  if (qs_h) {
-    if ((ldqs | ldks) & 7 || (ldq | ldk) & 3 || (reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) & 15)
+  if (groups <= 0) return hipSuccess;
+  if (split) {
+    if ((ldks & 7) || (ldk & 3) || (reinterpret_cast<uintptr_t>(k) & 15) ||
+        (H > 0 && ((ldqs & 7) || (ldq & 3) || (reinterpret_cast<uintptr_t>(q) & 15))))
       return hipErrorInvalidValue;  // float4 loads of every head row
     hipLaunchKernelGGL(k_qknorm_rope_split, dim3(blocks_for(groups, kRowsPerBlock)), dim3(kThreads), 0, s, q, ldq, k,
                        ldk, qw, kw, H, HKV, T, row_pos, cos_t, sin_t, eps, qs_h, qs_l, ldqs, ks_h, ks_l, ldks);

@@ -297,7 +297,7 @@ struct sg_model {
   std::vector<LayerDev> layers;
   // forward workspace (grown on demand)
   DevBuf h, xn, qkv, att, o, g, a16, sx, amax, meta_d, tokens, out, err;
-  DevBuf qs, ks, vt;  // attention operands, hi/lo fp16 (Q, K row-major; V^T)
+  DevBuf ks, vt;  // attention operands, hi/lo fp16 (K row-major; V^T); Q is split inside the attention kernel
   HostBuf meta_h, io_h;
   std::mutex mu;
 
@@ -311,7 +311,7 @@ struct sg_model {
   }
   ~sg_model() {
     for (void* p : allocs) (void)hipFree(p);
-    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a16, &sx, &amax, &meta_d, &tokens, &out, &err, &qs, &ks, &vt})
+    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a16, &sx, &amax, &meta_d, &tokens, &out, &err, &ks, &vt})
       b->release();
     meta_h.release();
     io_h.release();
@@ -393,8 +393,6 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
   float* g = m->g.as<float>();
   _Float16* a16 = m->a16.as<_Float16>();
   const int ar = sgk::gemm_pad_rows(T);
-  _Float16* qs_h = m->qs.as<_Float16>();
-  _Float16* qs_l = qs_h + (size_t)T * qd;
   _Float16* ks_h = m->ks.as<_Float16>();
   _Float16* ks_l = ks_h + (size_t)T * kvd;
   _Float16* vt_h = m->vt.as<_Float16>();
@@ -422,16 +420,18 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d),
               sgk::norm_quantize(h, ly.attn_norm, eps, T, d, meta.row_seq, site(l, 0), a16, ar, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), sgk::gemm_q8(a16, ar, ly.wqkv, ly.sqkv, sx, qkv, nullptr, T, nqkv, d, s));
-    SG_LAUNCH(SG_K_NORM, t * (qd + kvd) * 8.0,
-              sgk::qknorm_rope(qkv, nqkv, qkv + qd, nqkv, ly.q_norm, ly.k_norm, c.num_heads, c.num_kv_heads, T,
-                               meta.row_pos, m->cos_t, m->sin_t, eps, qs_h, qs_l, qd, ks_h, ks_l, kvd, s));
+    // K's QK-norm + RoPE here (H = 0: K rows only); Q's inside the attention kernel.
+    SG_LAUNCH(SG_K_NORM, t * kvd * 8.0,
+              sgk::qknorm_rope(nullptr, nqkv, qkv + qd, nqkv, ly.q_norm, ly.k_norm, 0, c.num_kv_heads, T,
+                               meta.row_pos, m->cos_t, m->sin_t, eps, nullptr, nullptr, 0, ks_h, ks_l, kvd, s));
     SG_LAUNCH(SG_K_NORM, t * kvd * 8.0,
               sgk::v_split_t(qkv + qd + kvd, nqkv, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles,
                              c.num_kv_heads, vt_h, vt_l, meta.Tp, s));
+    const sg_attn_qpre qpre{qkv, nqkv, ly.q_norm, m->cos_t, m->sin_t, meta.row_pos, eps};
     SG_LAUNCH(SG_K_ATTENTION, attn_flops,
-              sgk::attention(qs_h, qs_l, qd, ks_h, ks_l, kvd, vt_h, vt_l, meta.Tp, att, qd, meta.seq_off, meta.voff,
-                             meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale,
-                             site(l, 1), s));
+              sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, vt_l, meta.Tp, att, qd, meta.seq_off,
+                             meta.voff, meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale,
+                             site(l, 1), s, &qpre));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), sgk::quantize(att, qd, T, qd, meta.row_seq, site(l, 1), a16, ar, nullptr, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), sgk::gemm_q8(a16, ar, ly.wo, ly.so, sx, o, nullptr, T, d, qd, s));
     SG_LAUNCH(SG_K_NORM, t * d * 12.0,
@@ -486,7 +486,6 @@ int ensure_workspace(sg_model* m, int T, int n_seq, int Tp) {
   SG_TRY(m->a16.ensure(sizeof(_Float16) * (size_t)sgk::gemm_pad_rows(T) * a_cols));
   SG_TRY(m->sx.ensure(sizeof(float) * t));
   SG_TRY(m->amax.ensure(sizeof(float) * 4 * (size_t)c.num_layers * n_seq));
-  SG_TRY(m->qs.ensure(2 * sizeof(_Float16) * t * m->qd));
   SG_TRY(m->ks.ensure(2 * sizeof(_Float16) * t * m->kvd));
   SG_TRY(m->vt.ensure(2 * sizeof(_Float16) * (size_t)m->kvd * Tp));
   SG_TRY(m->err.ensure(64));

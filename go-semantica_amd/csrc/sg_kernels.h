@@ -8,6 +8,18 @@
 // One unit of per-sequence work: attention workgroup (sequence, first 32-row
 // chunk) or V^T split tile (sequence, first key).
 struct sg_item { int32_t seq, c0; };
+// Q's QK-norm + RoPE done inside the attention kernel: fp32 q [T][ldq] as the
+// QKV GEMM wrote it, attn_q_norm weights (null: no norm), the RoPE tables
+// [pos][128] and each row's position.
+struct sg_attn_qpre {
+  const float* q;
+  int ldq;
+  const float* w;
+  const float* cos_t;
+  const float* sin_t;
+  const int32_t* row_pos;
+  float eps;
+};
 
 namespace sgk {
 
@@ -52,9 +64,10 @@ hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s);
 // RMSNorm rows in the reference's order; amax (optional) collects per-sequence max|y|.
 hipError_t rmsnorm(float* dst, const float* src, const float* w, int rows, int n, float eps,
                    const int32_t* row_seq, float* amax, hipStream_t s);
-// QK-norm + RoPE; head_dim 256.  In place (fp32) when qs_h is null, else
+// QK-norm + RoPE; head_dim 256.  In place (fp32) when ks_h is null, else
 // written as the attention operands: hi/lo fp16 of x * kAttnQKScale into
-// qs_h/qs_l [T][ldqs] and ks_h/ks_l [T][ldks] (q and k are only read).
+// qs_h/qs_l [T][ldqs] and ks_h/ks_l [T][ldks] (q and k are only read; H = 0
+// processes K alone, for attention() with qpre).
 hipError_t qknorm_rope(float* q, int ldq, float* k, int ldk, const float* qw, const float* kw, int H, int HKV,
                        int T, const int32_t* row_pos, const float* cos_t, const float* sin_t, float eps,
                        _Float16* qs_h, _Float16* qs_l, int ldqs, _Float16* ks_h, _Float16* ks_l, int ldks,
@@ -103,10 +116,12 @@ hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, 
                       hipStream_t s);
 // out[T][ldo] = attention over the split operands; items: (seq, first chunk)
 // per workgroup, chunk c of a sequence = (head c / ceil(S/16), rows 16*(c % ceil(S/16))).
+// qpre != null: Q is taken from qpre (fp32, normed and rotated in the kernel
+// exactly as qknorm_rope does) and qh/ql/ldq are ignored.
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
                      const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
-                     float* amax, hipStream_t s);
+                     float* amax, hipStream_t s, const sg_attn_qpre* qpre = nullptr);
 
 // ---- brute-force search (k_search.hip) ----
 // Storage modes, the values of brute.QuantizationMode (search/brute/quant.go:8-15).
