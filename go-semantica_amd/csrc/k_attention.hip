@@ -104,6 +104,61 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
   // Q^T as the B operand: lane (query ln, group g4), k-step c: dims 32c+8g4..+8.
   half8_t bqh[kHD / 32], bql[kHD / 32];
   const int qr = r0 + min(qrow, S - 1);
+
+  // Tile staging through registers: 2048 16-B chunks per tile, 4 per thread.
+  // K chunk u: hi/lo u>>1, key (tid>>5) + 16(u&1), dims 8(tid&31)..+8.
+  // V^T chunk u: hi/lo u>>1, dim (tid>>2) + 128(u&1), keys 8(tid&3)..+8.
+  half8_t stg[4];
+  const _Float16* kbase_h = kh + kvh * kHD + 8 * (tid & 31);
+  const _Float16* kbase_l = kl + kvh * kHD + 8 * (tid & 31);
+  auto load_k = [&](int kt) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int key = (tid >> 5) + 16 * (u & 1);
+      const int64_t row = r0 + min(kt + key, S - 1);
+      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 1) ? kbase_l : kbase_h) + row * ldk);
+    }
+  };
+  auto store_k = [&]() {
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      *reinterpret_cast<half8_t*>(&Ks[u >> 1][(tid >> 5) + 16 * (u & 1)][8 * (tid & 31)]) = stg[u];
+  };
+  const int64_t vrow0 = (int64_t)(kvh * kHD + (tid >> 2)) * ldvt + vo + 8 * (tid & 3);
+  auto load_v = [&](int kt) {
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int64_t o = vrow0 + (int64_t)(128 * (u & 1)) * ldvt + kt;
+      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 1) ? vtl : vth) + o);
+    }
+  };
+  auto store_v = [&]() {
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      *reinterpret_cast<half8_t*>(&Vs[u >> 1][(tid >> 2) + 128 * (u & 1)][8 * (tid & 3)]) = stg[u];
+  };
+
+  // S^T subtile st (keys 16st..16st+15 of the tile x 16 queries), scaled by
+  // 64: lane holds query ln and keys 16st + 4g4 + r in register r.
+  auto scores = [&](int st) {
+    f32x4_t acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int ks = 0; ks < kHD / 32; ks++) {
+      const half8_t ah = *reinterpret_cast<const half8_t*>(&Ks[0][16 * st + ln][32 * ks + 8 * g4]);
+      const half8_t al = *reinterpret_cast<const half8_t*>(&Ks[1][16 * st + ln][32 * ks + 8 * g4]);
+      acc = mfma16(ah, bqh[ks], acc);
+      acc = mfma16(ah, bql[ks], acc);
+      acc = mfma16(al, bqh[ks], acc);
+    }
+    return acc;
+  };
+  auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
+
+  // ---- pass 1: row max ----
+  // Max of the raw (x64) scores; scaling by the power of two sscale commutes
+  // with max exactly.  Keys past S only occur in a sequence's last tile.
+  float m = -INFINITY;
+  load_k(0);  // in flight while Q is prepared
   if constexpr (QPRE) {
     // Lane (ln, g4) holds elements e = 32ks + 8g4 + t of row ln.
     float x[kHD / 32][8];
@@ -196,61 +251,6 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
       bql[ks] = *reinterpret_cast<const half8_t*>(ql + qo + 32 * ks);
     }
   }
-
-  // Tile staging through registers: 2048 16-B chunks per tile, 4 per thread.
-  // K chunk u: hi/lo u>>1, key (tid>>5) + 16(u&1), dims 8(tid&31)..+8.
-  // V^T chunk u: hi/lo u>>1, dim (tid>>2) + 128(u&1), keys 8(tid&3)..+8.
-  half8_t stg[4];
-  const _Float16* kbase_h = kh + kvh * kHD + 8 * (tid & 31);
-  const _Float16* kbase_l = kl + kvh * kHD + 8 * (tid & 31);
-  auto load_k = [&](int kt) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int key = (tid >> 5) + 16 * (u & 1);
-      const int64_t row = r0 + min(kt + key, S - 1);
-      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 1) ? kbase_l : kbase_h) + row * ldk);
-    }
-  };
-  auto store_k = [&]() {
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-      *reinterpret_cast<half8_t*>(&Ks[u >> 1][(tid >> 5) + 16 * (u & 1)][8 * (tid & 31)]) = stg[u];
-  };
-  const int64_t vrow0 = (int64_t)(kvh * kHD + (tid >> 2)) * ldvt + vo + 8 * (tid & 3);
-  auto load_v = [&](int kt) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int64_t o = vrow0 + (int64_t)(128 * (u & 1)) * ldvt + kt;
-      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 1) ? vtl : vth) + o);
-    }
-  };
-  auto store_v = [&]() {
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-      *reinterpret_cast<half8_t*>(&Vs[u >> 1][(tid >> 2) + 128 * (u & 1)][8 * (tid & 3)]) = stg[u];
-  };
-
-  // S^T subtile st (keys 16st..16st+15 of the tile x 16 queries), scaled by
-  // 64: lane holds query ln and keys 16st + 4g4 + r in register r.
-  auto scores = [&](int st) {
-    f32x4_t acc = {0, 0, 0, 0};
-#pragma unroll
-    for (int ks = 0; ks < kHD / 32; ks++) {
-      const half8_t ah = *reinterpret_cast<const half8_t*>(&Ks[0][16 * st + ln][32 * ks + 8 * g4]);
-      const half8_t al = *reinterpret_cast<const half8_t*>(&Ks[1][16 * st + ln][32 * ks + 8 * g4]);
-      acc = mfma16(ah, bqh[ks], acc);
-      acc = mfma16(ah, bql[ks], acc);
-      acc = mfma16(al, bqh[ks], acc);
-    }
-    return acc;
-  };
-  auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
-
-  // ---- pass 1: row max ----
-  // Max of the raw (x64) scores; scaling by the power of two sscale commutes
-  // with max exactly.  Keys past S only occur in a sequence's last tile.
-  float m = -INFINITY;
-  load_k(0);
   for (int kt = 0; kt < S; kt += kBK) {
     __syncthreads();  // every wave is done with the previous tile
     store_k();
