@@ -225,9 +225,9 @@ hipStream_t pick(sg_ctx* c, void* stream) { return stream ? static_cast<hipStrea
 
 // The asynchronous GEMM seam shares the context's operand scratch: a call
 // orders its stream after the previous call's last use (GPU-side, no host
-// wait) and marks its own.  Growing a scratch buffer frees the old one, and
-// hipFree waits for the device, so a reallocation never pulls memory from
-// under work in flight.
+// wait) and marks its own.  Growing a scratch buffer synchronizes the device
+// before freeing the old one (DevBuf::ensure), so a reallocation never pulls
+// memory from under work in flight.
 int gemm_scratch_begin(sg_ctx* c, hipStream_t s) {
   if (c->gemm_pending) SG_HIP(hipStreamWaitEvent(s, c->gemm_done, 0));
   return SG_OK;

@@ -31,7 +31,8 @@ struct TokenizerSpec {
 // Reads the tokenizer metadata of a GGUF image (sg_gguf.cpp).
 __attribute__((visibility("hidden"))) int gguf_tokenizer_spec(const void* data, size_t size, TokenizerSpec& out);
 
-// Grow-only device buffer.
+// Grow-only device buffer.  Growing waits for the device first, so work still
+// in flight on any stream never loses the old buffer under it.
 struct DevBuf {
   void* p = nullptr;
   size_t n = 0;
@@ -39,7 +40,10 @@ struct DevBuf {
   T* as() const { return static_cast<T*>(p); }
   int ensure(size_t bytes) {
     if (bytes <= n) return SG_OK;
-    if (p) (void)hipFree(p);
+    if (p) {
+      (void)hipDeviceSynchronize();
+      (void)hipFree(p);
+    }
     p = nullptr;
     n = 0;
     if (bytes == 0) return SG_OK;

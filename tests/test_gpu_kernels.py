@@ -128,6 +128,35 @@ def test_gemm_ragged_m_and_extremes(gpu_ctx, oracle):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+def test_gemm_seam_async_across_streams(gpu_ctx, oracle):
+    """sg_matmul_q8_0_int8 returns once enqueued and shares the context's operand
+    scratch: calls on two streams issued back to back (the second with a larger
+    input, which regrows the scratch) must each produce their own result."""
+    import torch
+    from semantica_gpu import kernels, synth
+    rng = np.random.default_rng(21)
+    N, K = 768, 768
+    raw = synth.q8_0_random(rng, N, K)
+    w = kernels.Q8Weight(gpu_ctx, raw, N, K)
+    xs = [rng.integers(-127, 128, size=(m, K), dtype=np.int8) for m in (300, 2100)]
+    rs = [rng.uniform(1e-3, 2.0, size=x.shape[0]).astype(np.float32) for x in xs]
+    dx = [dev(x) for x in xs]
+    drs = [dev(r) for r in rs]
+    ys = [torch.empty((x.shape[0], N), dtype=torch.float32, device="cuda") for x in xs]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    say("gemm seam: two streams, M=300 then M=2100")
+    for _ in range(3):
+        kernels.matmul_q8_0(gpu_ctx, ys[0], w, dx[0], drs[0], stream=s1.cuda_stream)
+        kernels.matmul_q8_0(gpu_ctx, ys[1], w, dx[1], drs[1], stream=s2.cuda_stream)
+    torch.cuda.synchronize()
+    w.close()
+    for x, r, y in zip(xs, rs, ys):
+        got = host(y)
+        ref = np.stack([oracle.matmul(raw, x[i:i + 1], r[i], N, oracle.ORDER_BLOCK_SERIAL)[0] for i in range(0, len(x), 97)])
+        assert np.array_equal(got[::97].view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("M", [4500, 8200])
 @pytest.mark.parametrize("N,K", [(1280, 768), (768, 1152)])
 def test_gemm_large_m(gpu_ctx, oracle, M, N, K):
