@@ -43,6 +43,8 @@ def parse():
     ap.add_argument("--cpu-seqs", type=int, default=0, help="0: 6 x cpu threads")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-search", action="store_true", help="skip the brute-force search measurement")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the small-batch latency and config-1 GEMM legs (profiles then hold only config-2 steps)")
     ap.add_argument("--search-vectors", type=int, default=1_000_000)
     ap.add_argument("--search-batch", type=int, default=64)
     ap.add_argument("--search-only", action="store_true",
@@ -384,8 +386,9 @@ def main():
         "instrumented_ms_per_step": round(dt_prof / a.steps * 1e3, 3),
         "gemm_frac_of_step": round(g["ms"] / (dt_prof * 1e3), 3),
     }
-    line["latency"] = small_batch_latency(model)
-    line["gemm_c1"] = gemm_c1_leg(ctx)
+    if not a.no_extras:
+        line["latency"] = small_batch_latency(model)
+        line["gemm_c1"] = gemm_c1_leg(ctx)
     model.close()
     if not a.no_search:
         line["tokenizer"] = tokenizer_leg()
