@@ -74,16 +74,31 @@ __device__ __forceinline__ int vt_key(int p) { return ((p & 4) << 2) | ((p & 24)
 // attn_q_norm and RoPE to its 16 rows itself (the arithmetic of
 // k_qknorm_rope_split, so the operands are bit-identical), which saves writing
 // Q's hi/lo operands and reading them back.
-template <bool QPRE>
+//
+// RS (every sequence of the launch at most kRegKeys keys): pass 1 keeps each
+// lane's raw scores in registers (8 per 32-key tile, 128 VGPRs at 512 keys)
+// and pass 2 reads them back instead of recomputing S^T, so K is streamed
+// once and a third of the MFMAs and LDS reads go away; pass 1 streams only K
+// and pass 2 only V^T, each through two LDS buffers (one barrier per tile).
+// The values are the ones pass 2 would recompute, so the output is identical.
+constexpr int kRegTiles = sgk::kAttnRegKeys / kBK;
+constexpr int kKBuf = 2 * kBK * kKStride;  // halves of one K tile buffer [hi/lo][key][dim]
+constexpr int kVBuf = 2 * kHD * kVStride;  // halves of one V^T tile buffer [hi/lo][dim][key]
+
+template <bool QPRE, bool RS>
 __global__ __launch_bounds__(kNT, 2) void k_attn(
     const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
     const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vth, const _Float16* __restrict__ vtl,
     int ldvt, float* __restrict__ out, int ldo, const int32_t* __restrict__ seq_off,
     const int32_t* __restrict__ voff, const sg_item* __restrict__ items, int G, float sscale,
     float* __restrict__ amax, sg_attn_qpre qp) {
-  __shared__ _Float16 Ks[2][kBK][kKStride];  // [hi/lo][key][dim]
-  __shared__ _Float16 Vs[2][kHD][kVStride];  // [hi/lo][dim][key, vt_key order]
+  // Two-pass: one K and one V^T buffer.  RS: two K buffers in pass 1, two V^T
+  // buffers in pass 2, over the same memory.
+  constexpr int kLdsHalves = RS ? (kKBuf > kVBuf ? 2 * kKBuf : 2 * kVBuf) : kKBuf + kVBuf;
+  __shared__ __attribute__((aligned(16))) _Float16 lds[kLdsHalves];
   __shared__ float red[kWaves];
+  auto kbuf = [&](int b) { return lds + b * kKBuf; };
+  auto vbuf = [&](int b) { return RS ? lds + b * kVBuf : lds + kKBuf; };
 
   const sg_item it = items[blockIdx.x];
   const int kvh = blockIdx.y;
@@ -119,10 +134,11 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
       stg[u] = *reinterpret_cast<const half8_t*>(((u >> 1) ? kbase_l : kbase_h) + row * ldk);
     }
   };
-  auto store_k = [&]() {
+  auto store_k = [&](_Float16* kb) {
 #pragma unroll
     for (int u = 0; u < 4; u++)
-      *reinterpret_cast<half8_t*>(&Ks[u >> 1][(tid >> 5) + 16 * (u & 1)][8 * (tid & 31)]) = stg[u];
+      *reinterpret_cast<half8_t*>(kb + ((u >> 1) * kBK + (tid >> 5) + 16 * (u & 1)) * kKStride + 8 * (tid & 31)) =
+          stg[u];
   };
   const int64_t vrow0 = (int64_t)(kvh * kHD + (tid >> 2)) * ldvt + vo + 8 * (tid & 3);
   auto load_v = [&](int kt) {
@@ -132,20 +148,22 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
       stg[u] = *reinterpret_cast<const half8_t*>(((u >> 1) ? vtl : vth) + o);
     }
   };
-  auto store_v = [&]() {
+  auto store_v = [&](_Float16* vb) {
 #pragma unroll
     for (int u = 0; u < 4; u++)
-      *reinterpret_cast<half8_t*>(&Vs[u >> 1][(tid >> 2) + 128 * (u & 1)][8 * (tid & 3)]) = stg[u];
+      *reinterpret_cast<half8_t*>(vb + ((u >> 1) * kHD + (tid >> 2) + 128 * (u & 1)) * kVStride + 8 * (tid & 3)) =
+          stg[u];
   };
 
   // S^T subtile st (keys 16st..16st+15 of the tile x 16 queries), scaled by
   // 64: lane holds query ln and keys 16st + 4g4 + r in register r.
-  auto scores = [&](int st) {
+  auto scores = [&](int st, const _Float16* kb) {
     f32x4_t acc = {0, 0, 0, 0};
 #pragma unroll
     for (int ks = 0; ks < kHD / 32; ks++) {
-      const half8_t ah = *reinterpret_cast<const half8_t*>(&Ks[0][16 * st + ln][32 * ks + 8 * g4]);
-      const half8_t al = *reinterpret_cast<const half8_t*>(&Ks[1][16 * st + ln][32 * ks + 8 * g4]);
+      const half8_t ah = *reinterpret_cast<const half8_t*>(kb + (16 * st + ln) * kKStride + 32 * ks + 8 * g4);
+      const half8_t al =
+          *reinterpret_cast<const half8_t*>(kb + (kBK + 16 * st + ln) * kKStride + 32 * ks + 8 * g4);
       acc = mfma16(ah, bqh[ks], acc);
       acc = mfma16(ah, bql[ks], acc);
       acc = mfma16(al, bqh[ks], acc);
@@ -153,6 +171,48 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
     return acc;
   };
   auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
+  // Pass-1 max over one tile's scores (keys past S only in a sequence's last tile).
+  auto tile_max = [&](float m, int kt, const f32x4_t& a0, const f32x4_t& a1) {
+    if (kt + kBK <= S) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) m = fmaxf(m, fmaxf(a0[r], a1[r]));
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        m = key_of(kt, 0, r) < S ? fmaxf(m, a0[r]) : m;
+        m = key_of(kt, 1, r) < S ? fmaxf(m, a1[r]) : m;
+      }
+    }
+    return m;
+  };
+  // Pass-2 weights of one tile: e = fastExp(s - m), row sum, split P^T.
+  auto weights = [&](int kt, const f32x4_t& a0, const f32x4_t& a1, float m, float& lsum, half8_t& ph,
+                     half8_t& pl) {
+    const bool full = kt + kBK <= S;
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float e = sg_fast_exp_nonpos((st ? a1[r] : a0[r]) * sscale - m);
+        if (!full) e = key_of(kt, st, r) < S ? e : 0.0f;
+        lsum = lsum + e;
+        const hl16 p = split_f16(e * kPScale);
+        ph[4 * st + r] = p.hi;
+        pl[4 * st + r] = p.lo;
+      }
+    }
+  };
+  // O^T += V^T P^T for one tile.
+  auto pv = [&](f32x4_t* o, const _Float16* vb, const half8_t& ph, const half8_t& pl) {
+#pragma unroll
+    for (int mt = 0; mt < kHD / 16; mt++) {
+      const half8_t ah = *reinterpret_cast<const half8_t*>(vb + (16 * mt + ln) * kVStride + 8 * g4);
+      const half8_t al = *reinterpret_cast<const half8_t*>(vb + (kHD + 16 * mt + ln) * kVStride + 8 * g4);
+      o[mt] = mfma16(ah, ph, o[mt]);
+      o[mt] = mfma16(ah, pl, o[mt]);
+      o[mt] = mfma16(al, ph, o[mt]);
+    }
+  };
 
   // ---- pass 1: row max ----
   // Max of the raw (x64) scores; scaling by the power of two sscale commutes
@@ -177,10 +237,10 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
       // RMSNorm's sum of squares in the AVX2 lane order (sg_rmsnorm8): lane v
       // of a row chains element 8i + v over i.  Element e sits at i = 4ks + g4,
       // v = t here, so each 32-element chunk goes through a 16 x 40-float LDS
-      // tile of this wave (inside Ks, which nothing uses before the first
-      // barrier below); lane (row rA or rA + 8, v) then reads the chunk's
+      // tile of this wave (inside K buffer 0, which nothing uses before the
+      // first barrier below); lane (row rA or rA + 8, v) then reads the chunk's
       // elements 8k + v, k = 0..3, in order.
-      float* tile = reinterpret_cast<float*>(&Ks[0][0][0]) + w * (16 * 40);
+      float* tile = reinterpret_cast<float*>(lds) + w * (16 * 40);
       const int v = lane & 7, rA = lane >> 3;
       float accA = 0.0f, accB = 0.0f;
 #pragma unroll
@@ -251,72 +311,74 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
       bql[ks] = *reinterpret_cast<const half8_t*>(ql + qo + 32 * ks);
     }
   }
-  for (int kt = 0; kt < S; kt += kBK) {
-    __syncthreads();  // every wave is done with the previous tile
-    store_k();
-    __syncthreads();
-    if (kt + kBK < S) load_k(kt + kBK);  // in flight during the MFMAs
-    if (active) {
-      const f32x4_t a0 = scores(0), a1 = scores(1);
-      if (kt + kBK <= S) {
-#pragma unroll
-        for (int r = 0; r < 4; r++) m = fmaxf(m, fmaxf(a0[r], a1[r]));
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          m = key_of(kt, 0, r) < S ? fmaxf(m, a0[r]) : m;
-          m = key_of(kt, 1, r) < S ? fmaxf(m, a1[r]) : m;
-        }
-      }
-    }
-  }
-  m = fmaxf(m, __shfl_xor(m, 16));
-  m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
-
-  // ---- pass 2: e = fastExp(s - m), row sums, O^T += V^T P^T ----
   f32x4_t o[kHD / 16];
 #pragma unroll
   for (int mt = 0; mt < kHD / 16; mt++) o[mt] = f32x4_t{0, 0, 0, 0};
   float lsum = 0.0f;
-  load_k(0);
-  __syncthreads();  // pass 1's last tile is consumed
-  store_k();
-  __syncthreads();
-  for (int kt = 0; kt < S; kt += kBK) {
-    load_v(kt);  // in flight during the score MFMAs
-    half8_t ph, pl;  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
-    if (active) {
-      const f32x4_t a0 = scores(0), a1 = scores(1);
-      const bool full = kt + kBK <= S;
+  if constexpr (RS) {
+    f32x4_t sr[kRegTiles][2];  // raw scores of tile t, subtiles 0 and 1
+    __syncthreads();            // the Q prologue's LDS tiles are free
 #pragma unroll
-      for (int st = 0; st < 2; st++) {
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          float e = sg_fast_exp_nonpos((st ? a1[r] : a0[r]) * sscale - m);
-          if (!full) e = key_of(kt, st, r) < S ? e : 0.0f;
-          lsum = lsum + e;
-          const hl16 p = split_f16(e * kPScale);
-          ph[4 * st + r] = p.hi;
-          pl[4 * st + r] = p.lo;
+    for (int t = 0; t < kRegTiles; t++) {
+      const int kt = t * kBK;
+      if (kt < S) {
+        // Buffer t & 1 was last read in tile t - 2, before the previous barrier.
+        store_k(kbuf(t & 1));
+        __syncthreads();
+        if (kt + kBK < S)
+          load_k(kt + kBK);  // in flight during the MFMAs
+        else
+          load_v(0);  // pass 2's first tile
+        if (active) {
+          sr[t][0] = scores(0, kbuf(t & 1));
+          sr[t][1] = scores(1, kbuf(t & 1));
+          m = tile_max(m, kt, sr[t][0], sr[t][1]);
         }
       }
     }
-    store_v();
-    __syncthreads();  // V^T tile staged; K tile free
-    const bool more = kt + kBK < S;
-    if (more) load_k(kt + kBK);  // in flight during the P.V MFMAs
-    if (active) {
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
+    __syncthreads();  // the K buffers are free (the V^T buffers overlay them)
 #pragma unroll
-      for (int mt = 0; mt < kHD / 16; mt++) {
-        const half8_t ah = *reinterpret_cast<const half8_t*>(&Vs[0][16 * mt + ln][8 * g4]);
-        const half8_t al = *reinterpret_cast<const half8_t*>(&Vs[1][16 * mt + ln][8 * g4]);
-        o[mt] = mfma16(ah, ph, o[mt]);
-        o[mt] = mfma16(ah, pl, o[mt]);
-        o[mt] = mfma16(al, ph, o[mt]);
+    for (int t = 0; t < kRegTiles; t++) {
+      const int kt = t * kBK;
+      if (kt < S) {
+        half8_t ph, pl;  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
+        if (active) weights(kt, sr[t][0], sr[t][1], m, lsum, ph, pl);
+        store_v(vbuf(t & 1));
+        __syncthreads();
+        if (kt + kBK < S) load_v(kt + kBK);  // in flight during the P.V MFMAs
+        if (active) pv(o, vbuf(t & 1), ph, pl);
       }
     }
-    if (more) store_k();  // nobody reads Ks between the two barriers
-    __syncthreads();      // K tile staged; V^T tile free
+  } else {
+    for (int kt = 0; kt < S; kt += kBK) {
+      __syncthreads();  // every wave is done with the previous tile
+      store_k(kbuf(0));
+      __syncthreads();
+      if (kt + kBK < S) load_k(kt + kBK);  // in flight during the MFMAs
+      if (active) m = tile_max(m, kt, scores(0, kbuf(0)), scores(1, kbuf(0)));
+    }
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
+
+    // ---- pass 2: e = fastExp(s - m), row sums, O^T += V^T P^T ----
+    load_k(0);
+    __syncthreads();  // pass 1's last tile is consumed
+    store_k(kbuf(0));
+    __syncthreads();
+    for (int kt = 0; kt < S; kt += kBK) {
+      load_v(kt);  // in flight during the score MFMAs
+      half8_t ph, pl;
+      if (active) weights(kt, scores(0, kbuf(0)), scores(1, kbuf(0)), m, lsum, ph, pl);
+      store_v(vbuf(0));
+      __syncthreads();  // V^T tile staged; K tile free
+      const bool more = kt + kBK < S;
+      if (more) load_k(kt + kBK);  // in flight during the P.V MFMAs
+      if (active) pv(o, vbuf(0), ph, pl);
+      if (more) store_k(kbuf(0));  // nobody reads the K buffer between the two barriers
+      __syncthreads();             // K tile staged; V^T tile free
+    }
   }
   lsum = lsum + __shfl_xor(lsum, 16);
   lsum = lsum + __shfl_xor(lsum, 32);
@@ -442,25 +504,39 @@ hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, 
   return hipGetLastError();
 }
 
+namespace {
+template <bool QPRE, bool RS>
+void launch_attn(dim3 grid, hipStream_t s, const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh,
+                 const _Float16* kl, int ldk, const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo,
+                 const int32_t* seq_off, const int32_t* voff, const sg_item* items, int G, float sscale, float* amax,
+                 const sg_attn_qpre& qp) {
+  hipLaunchKernelGGL((k_attn<QPRE, RS>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vth, vtl, ldvt, out, ldo,
+                     seq_off, voff, items, G, sscale, amax, qp);
+}
+}  // namespace
+
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
                      const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
-                     float* amax, hipStream_t s, const sg_attn_qpre* qpre) {
+                     float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre) {
   if (n_items <= 0) return hipSuccess;
-  if (hd != kHD || HKV <= 0 || H % HKV) return hipErrorInvalidValue;
+  if (hd != kHD || HKV <= 0 || H % HKV || max_len <= 0) return hipErrorInvalidValue;
   if ((ldk | ldvt) & 7 || (ldo & 3)) return hipErrorInvalidValue;
   const float sscale = scale / (kQKScale * kQKScale);
+  const dim3 grid(n_items, HKV);
+  const bool rs = max_len <= kAttnRegKeys;
   if (qpre) {
     if (!qpre->q || !qpre->cos_t || !qpre->sin_t || !qpre->row_pos || (qpre->ldq & 3) ||
         (reinterpret_cast<uintptr_t>(qpre->q) & 15) || (reinterpret_cast<uintptr_t>(qpre->w) & 15) ||
         (reinterpret_cast<uintptr_t>(qpre->cos_t) & 15) || (reinterpret_cast<uintptr_t>(qpre->sin_t) & 15))
       return hipErrorInvalidValue;  // float4 loads of Q rows, weights and table rows
-    hipLaunchKernelGGL(k_attn<true>, dim3(n_items, HKV), dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vth, vtl, ldvt,
-                       out, ldo, seq_off, voff, items, H / HKV, sscale, amax, *qpre);
+    (rs ? launch_attn<true, true> : launch_attn<true, false>)(grid, s, qh, ql, ldq, kh, kl, ldk, vth, vtl, ldvt, out,
+                                                              ldo, seq_off, voff, items, H / HKV, sscale, amax, *qpre);
   } else {
     if (ldq & 7) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_attn<false>, dim3(n_items, HKV), dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vth, vtl, ldvt,
-                       out, ldo, seq_off, voff, items, H / HKV, sscale, amax, sg_attn_qpre{});
+    (rs ? launch_attn<false, true> : launch_attn<false, false>)(grid, s, qh, ql, ldq, kh, kl, ldk, vth, vtl, ldvt,
+                                                                out, ldo, seq_off, voff, items, H / HKV, sscale, amax,
+                                                                sg_attn_qpre{});
   }
   return hipGetLastError();
 }

@@ -52,6 +52,7 @@ using sgi::HostBuf;
 struct Meta {
   int T = 0, n_seq = 0, n_items = 0, n_vtiles = 0;
   int Tp = 0;         // V^T columns: every sequence padded to whole 32-key tiles
+  int max_len = 0;    // longest sequence
   double sum_sq = 0;  // sum over sequences of S^2 (attention work)
   // device views into one buffer
   int32_t* row_seq = nullptr;
@@ -140,7 +141,11 @@ int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev,
   m.T = T;
   m.n_seq = n_seq;
   m.sum_sq = 0;
-  for (int i = 0; i < n_seq; i++) m.sum_sq += (double)(off[i + 1] - off[i]) * (off[i + 1] - off[i]);
+  m.max_len = 0;
+  for (int i = 0; i < n_seq; i++) {
+    m.sum_sq += (double)(off[i + 1] - off[i]) * (off[i + 1] - off[i]);
+    m.max_len = std::max(m.max_len, off[i + 1] - off[i]);
+  }
   m.n_items = n_items;
   m.n_vtiles = n_vt;
   m.Tp = vo[n_seq];
@@ -431,7 +436,7 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
     SG_LAUNCH(SG_K_ATTENTION, attn_flops,
               sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, vt_l, meta.Tp, att, qd, meta.seq_off,
                              meta.voff, meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale,
-                             site(l, 1), s, &qpre));
+                             site(l, 1), meta.max_len, s, &qpre));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), sgk::quantize(att, qd, T, qd, meta.row_seq, site(l, 1), a16, ar, nullptr, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), sgk::gemm_q8(a16, ar, ly.wo, ly.so, sx, o, nullptr, T, d, qd, s));
     SG_LAUNCH(SG_K_NORM, t * d * 12.0,
@@ -895,7 +900,8 @@ int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const flo
   SG_HIP(sgk::v_split_t(v, ldkv, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles, n_kv_heads, vt_h, vt_l,
                         meta.Tp, s));
   SG_HIP(sgk::attention(qs_h, qs_l, (int)qd, ks_h, ks_l, (int)kvd, vt_h, vt_l, meta.Tp, out, (int)qd, meta.seq_off,
-                        meta.voff, meta.items, meta.n_items, n_heads, n_kv_heads, head_dim, scale, nullptr, s));
+                        meta.voff, meta.items, meta.n_items, n_heads, n_kv_heads, head_dim, scale, nullptr,
+                        meta.max_len, s));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;
 }

@@ -105,6 +105,7 @@ constexpr int kGeluGroup = 32;
 constexpr float kAttnQKScale = 8.0f;  // Q and K are split after scaling by 8 (exact)
 constexpr int kAttnChunkRows = 16;    // (head, query) rows per attention chunk (one wave)
 constexpr int kAttnChunks = 8;        // chunks per attention workgroup
+constexpr int kAttnRegKeys = 512;     // longest sequence whose scores pass 1 keeps in registers
 // Columns of V^T a sequence of S keys occupies (whole 32-key tiles).
 inline int attn_key_pad(int S) { return (S + 31) / 32 * 32; }
 // V fp32 [T][ldv] -> V^T hi/lo fp16 [HKV*256][ldvt] (sequence s at column voff[s],
@@ -117,11 +118,13 @@ hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, 
 // out[T][ldo] = attention over the split operands; items: (seq, first chunk)
 // per workgroup, chunk c of a sequence = (head c / ceil(S/16), rows 16*(c % ceil(S/16))).
 // qpre != null: Q is taken from qpre (fp32, normed and rotated in the kernel
-// exactly as qknorm_rope does) and qh/ql/ldq are ignored.
+// exactly as qknorm_rope does) and qh/ql/ldq are ignored.  max_len: the
+// longest sequence of the launch (at most kAttnRegKeys selects the kernel that
+// keeps pass 1's scores in registers; the output is the same either way).
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
                      const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
-                     float* amax, hipStream_t s, const sg_attn_qpre* qpre = nullptr);
+                     float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre = nullptr);
 
 // ---- brute-force search (k_search.hip) ----
 // Storage modes, the values of brute.QuantizationMode (search/brute/quant.go:8-15).

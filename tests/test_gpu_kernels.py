@@ -298,11 +298,14 @@ def test_qknorm_rope_bit_exact(gpu_ctx, oracle):
 ATTN_REL_TOL = 1e-5
 
 
-def test_attention_vs_oracle(gpu_ctx, oracle):
+# Batches whose longest sequence has at most 512 keys run the kernel that keeps
+# pass 1's scores in registers; a longer one switches the whole launch to the
+# kernel that recomputes them.
+@pytest.mark.parametrize("lens", [[1, 31, 32, 33, 100, 517], [1, 31, 32, 33, 100, 512]])
+def test_attention_vs_oracle(gpu_ctx, oracle, lens):
     import torch
     from semantica_gpu import kernels
     rng = np.random.default_rng(31)
-    lens = [1, 31, 32, 33, 100, 517]
     off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     T = int(off[-1])
     say(f"attention lens={lens}")
@@ -318,6 +321,30 @@ def test_attention_vs_oracle(gpu_ctx, oracle):
         ref = oracle.attention(q[sl], k[sl], v[sl], 3, 1, 256)
         assert rel_err(got[sl], ref) < ATTN_REL_TOL, (i, rel_err(got[sl], ref))
         assert np.max(np.abs(got[sl] - ref)) < 1e-4 * np.max(np.abs(v[sl])), i
+
+
+def test_attention_register_scores_match_recomputed(gpu_ctx):
+    """The same sequences with and without a 600-key companion (which moves the
+    launch from register-held scores to recomputed ones) give identical bits."""
+    import torch
+    from semantica_gpu import kernels
+    rng = np.random.default_rng(77)
+    lens = [512, 1, 300, 47, 480, 33]
+    long_len = 600
+    T0 = sum(lens)
+    T = T0 + long_len
+    say(f"attention register vs recomputed scores lens={lens} + [{long_len}]")
+    q = (rng.standard_normal((T, 768)) * rng.uniform(0.5, 1.5, 768)).astype(np.float32)
+    k = (rng.standard_normal((T, 256)) * rng.uniform(0.5, 1.5, 256)).astype(np.float32)
+    v = (rng.standard_normal((T, 256)) * 2).astype(np.float32)
+    off_a = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    off_b = np.concatenate([[0], np.cumsum(lens + [long_len])]).astype(np.int32)
+    out_a = torch.empty((T0, 768), dtype=torch.float32, device="cuda")
+    out_b = torch.empty((T, 768), dtype=torch.float32, device="cuda")
+    kernels.attention(gpu_ctx, out_a, dev(q[:T0]), dev(k[:T0]), dev(v[:T0]), 3, 1, 256, off_a)
+    kernels.attention(gpu_ctx, out_b, dev(q), dev(k), dev(v), 3, 1, 256, off_b)
+    a, b = host(out_a), host(out_b)[:T0]
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 def test_attention_clamped_keys_are_exact_zero(gpu_ctx, oracle):
