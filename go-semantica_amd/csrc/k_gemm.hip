@@ -23,6 +23,8 @@
 // 16h+8..16h+15.  A and W use the same assignment, so each block's dot
 // product is complete whatever k order the matrix core applies internally.
 // Block scales are St [K/32][N] fp32 (32 consecutive columns = 128 bytes).
+#include <type_traits>
+
 #include "sg_device.h"
 #include "sg_kernels.h"
 
@@ -693,6 +695,138 @@ __global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_dl(
   gemm_epilogue<NW, 1, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
 }
 
+// Buffer-load variant of the 8-wave direct-to-LDS kernel (same tiles, same
+// arithmetic, same 3-stage ring).  Its copies are buffer_load ... lds with a
+// per-block buffer descriptor built on the scalar unit, so a copy costs no
+// vector instruction (the flat form needs a 64-bit vector add and a
+// readfirstlane per copy), and the K loop is unrolled by the ring depth so
+// every LDS fragment read is a loop-invariant vector address plus an
+// immediate (the LDS is laid out [A stages][W stages][scale stages] to keep
+// those immediates under 64 KB).  Only the FMAs of the block-serial
+// epilogue and the MFMAs stay on the vector side of the loop.
+constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor, gfx9 family
+
+template <int NW, int TN, bool GELU>
+__global__ __launch_bounds__(NW * SG_WAVE, 4) void k_gemm_q8_bl(
+    const _Float16* __restrict__ A, int a_rows, const _Float16* __restrict__ W, const float* __restrict__ St,
+    const float* __restrict__ row_scale, float* __restrict__ Y, int M, int N, int K,
+    const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
+  constexpr int STAGES = 3;
+  constexpr int BM = NW * 32, BN = TN * 32;
+  constexpr int A_BYTES = BM * 64, W_BYTES = BN * 64, S_BYTES = BN * 4;
+  constexpr int W_OFF = STAGES * A_BYTES, S_OFF = W_OFF + STAGES * W_BYTES;
+  constexpr int WROWS = BN / NW;              // weight rows each wave copies (64 B each)
+  constexpr int SLANES = BN / NW;             // scales each wave copies
+  constexpr int CPB = 2 + 1 + 1;              // copies per wave per K-block
+  static_assert(BN % NW == 0 && SLANES <= SG_WAVE, "weight tile split over the waves");
+  static_assert((STAGES - 1) * A_BYTES < 65536 && (STAGES - 1) * W_BYTES + W_BYTES < 65536 &&
+                    STAGES * S_BYTES < 65536,
+                "stage offsets fit the LDS immediate");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[S_OFF + STAGES * S_BYTES];
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  int bx, by;
+  xcd_tile(bx, by);
+  const int n0 = bx * BN;
+  const int mw = by * BM + wave * 32;
+  const int nb = K >> 5;
+  auto swz = [](int r, int c) { return c ^ ((r >> 2) & 3); };  // chunk slot of chunk c in row r
+
+  // Copy sources: byte offsets inside block b's slice of A ([a_rows][32]
+  // halves), of W ([N][32]) and of the scales ([N] floats).
+  uint32_t aoff[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int r = 16 * j + (lane >> 2);
+    aoff[j] = (uint32_t)(mw + r) * 64u + 16u * swz(r, lane & 3);
+  }
+  // One 1-KB weight copy per wave.  (A guarded loop over an array of copy
+  // offsets here made the host pass drop the kernel's launch stub.)
+  static_assert(WROWS == 16, "one 1-KB weight copy per wave");
+  const int wrow = WROWS * wave + (lane >> 2);
+  const uint32_t woff = (uint32_t)min(n0 + wrow, N - 1) * 64u + 16u * swz(wrow, lane & 3);
+  const uint32_t soff = (uint32_t)min(n0 + SLANES * wave + lane, N - 1) * 4u;
+
+  auto issue = [&](int b, int st) {
+    __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(A + (int64_t)b * a_rows * 32), 0, a_rows * 64, kBufWord3);
+    __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(W + (int64_t)b * N * 32), 0, N * 64, kBufWord3);
+    __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(St + (int64_t)b * N), 0, N * 4, kBufWord3);
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)(lds + st * A_BYTES + wave * 2048 + j * 1024), 16,
+                                               aoff[j], 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(lds + W_OFF + st * W_BYTES + WROWS * 64 * wave), 16, woff, 0,
+                                             0, 0);
+    if (lane < SLANES)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds + S_OFF + st * S_BYTES + wave * (SLANES * 4)), 4,
+                                               soff, 0, 0, 0);
+  };
+
+  // Fragment read addresses (stage 0; stage st adds st * *_BYTES).
+  const int a_row = wave * 32 + lr;
+  const uint32_t ra_lo = a_row * 64 + 16 * swz(a_row, 2 * lh), ra_hi = a_row * 64 + 16 * swz(a_row, 2 * lh + 1);
+  const uint32_t rw_lo = W_OFF + lr * 64 + 16 * swz(lr, 2 * lh), rw_hi = W_OFF + lr * 64 + 16 * swz(lr, 2 * lh + 1);
+  const uint32_t rd = S_OFF + 4 * lr;
+
+  f32x16_t acc[1][TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[0][tn][r] = 0.0f;
+  const f32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+
+  auto step = [&](auto stc, int b) {
+    constexpr int ST = decltype(stc)::value;
+    wait_vmcnt<(STAGES - 2) * CPB>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(min(b + STAGES - 1, nb - 1), (ST + STAGES - 1) % STAGES);
+    Frag fa;
+    fa.lo = *reinterpret_cast<const half8_t*>(lds + ra_lo + ST * A_BYTES);
+    fa.hi = *reinterpret_cast<const half8_t*>(lds + ra_hi + ST * A_BYTES);
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+      // rows 32tn + lr share lr's swizzle ((32tn + lr) >> 2 differs by a multiple of 8)
+      const half8_t wlo = *reinterpret_cast<const half8_t*>(lds + rw_lo + ST * W_BYTES + tn * 2048);
+      const half8_t whi = *reinterpret_cast<const half8_t*>(lds + rw_hi + ST * W_BYTES + tn * 2048);
+      const float d = *reinterpret_cast<const float*>(lds + rd + ST * S_BYTES + tn * 128);
+      f32x16_t pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa.lo, wlo, zero, 0, 0, 0);
+      pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa.hi, whi, pp, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[0][tn][r] = __builtin_fmaf(pp[r], d, acc[0][tn][r]);
+    }
+  };
+
+  issue(0, 0);
+  issue(min(1, nb - 1), 1);
+  for (int b = 0; b < nb; b += STAGES) {
+    step(std::integral_constant<int, 0>{}, b);
+    if (b + 1 < nb) step(std::integral_constant<int, 1>{}, b + 1);
+    if (b + 2 < nb) step(std::integral_constant<int, 2>{}, b + 2);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // redundant tail copies drained before exit
+  gemm_epilogue<NW, 1, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
+}
+
+template <int NW, int TN, bool GELU>
+hipError_t launch_bl(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
+                     int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
+  constexpr int BM = NW * 32, BN = TN * 32;
+  const int gm = (M + BM - 1) / BM;
+  if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
+  if ((int64_t)a_rows * 64 > INT32_MAX || (int64_t)N * 64 > INT32_MAX) return hipErrorInvalidValue;  // descriptor sizes
+  dim3 grid((N + BN - 1) / BN, gm);
+  hipLaunchKernelGGL((k_gemm_q8_bl<NW, TN, GELU>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y, M, N, K,
+                     row_seq, amax);
+  return hipGetLastError();
+}
+
 template <int NW, int TN, bool GELU, int STAGES>
 hipError_t launch_dl(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
                      int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
@@ -743,6 +877,8 @@ hipError_t launch(const _Float16* A, int a_rows, const _Float16* W, const float*
 
 // Workgroups of the 8-wave direct-to-LDS launch.
 inline int64_t dl8_blocks(int M, int N) { return (int64_t)((M + 255) / 256) * ((N + 127) / 128); }
+// The buffer-load kernel's descriptors hold a block slice's size in 32 bits.
+inline bool bl_fits(int a_rows, int N) { return (int64_t)a_rows * 64 <= INT32_MAX && (int64_t)N * 64 <= INT32_MAX; }
 
 }  // namespace
 
@@ -754,11 +890,15 @@ hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float
   if (K <= 0 || K % 32) return hipErrorInvalidValue;
   if (sums) return launch<1, 1, 1, 1, true>(A, a_rows, W, St, row_scale, Y, sums, M, N, K, s);
   // Direct-to-LDS workgroups of 8 waves (256 rows x 128 columns, 3-stage
-  // copy ring) once they cover half the compute units; below that, from 4096
+  // copy ring, buffer-load copies) once they cover half the compute units
+  // (the flat-copy form only past 32-bit descriptor sizes); below that, from 4096
   // rows, 4 waves x 64 columns with a 6-stage ring; otherwise 64x64
   // register-direct tiles, whose grid still covers the chip (tile sweeps on
   // MI355X at the model's shapes, M = 32 .. 4096).
-  if (M >= 8192 || dl8_blocks(M, N) >= 128) return launch_dl<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+  if (M >= 8192 || dl8_blocks(M, N) >= 128) {
+    if (bl_fits(a_rows, N)) return launch_bl<8, 4, false>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+    return launch_dl<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+  }
   if (M >= 4096) return launch_dl<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   return launch<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
 }
@@ -768,8 +908,11 @@ hipError_t gemm_q8_gelu(const _Float16* A, int a_rows, const _Float16* W, const 
   if (M <= 0 || Nh <= 0) return hipSuccess;
   if (K <= 0 || K % 32 || Nh % 32) return hipErrorInvalidValue;
   if (amax && !row_seq) return hipErrorInvalidValue;
-  if (M >= 8192 || dl8_blocks(M, 2 * Nh) >= 128)
+  if (M >= 8192 || dl8_blocks(M, 2 * Nh) >= 128) {
+    if (bl_fits(a_rows, 2 * Nh))
+      return launch_bl<8, 4, true>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
     return launch_dl<8, 4, true, 3>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
+  }
   return launch_sp<4, 1, 2, true>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
 }
 
