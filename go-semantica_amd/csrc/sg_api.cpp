@@ -70,7 +70,9 @@ int seq_groups(int S, int G) {
 }
 
 // Fills `host` with [row_seq | row_pos | seq_off | voff | items | vtiles] and
-// copies it to `dev` on stream s (the copy is complete when this returns).
+// copies it to `dev` on stream s, asynchronously: kernels launched on s after
+// this see the metadata, and the next stage_meta waits for the copy before it
+// rewrites `host`.
 // G: query heads per kv head.
 //
 // Workgroup order.  Workgroup i of a launch runs on XCD i % 8 (the dispatcher
@@ -136,7 +138,7 @@ int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev,
     }
   }
   SG_HIP(hipMemcpyAsync(dev.p, host.p, bytes, hipMemcpyHostToDevice, s));
-  SG_HIP(hipStreamSynchronize(s));
+  SG_TRY(host.record(s));
   int32_t* d = dev.as<int32_t>();
   m.T = T;
   m.n_seq = n_seq;

@@ -62,12 +62,29 @@ struct DevBuf {
 };
 
 // Grow-only pinned host buffer (staging for metadata / small copies).
+// Pinned host staging.  An asynchronous copy out of it is followed by
+// record(stream); wait() (called by ensure and release too) blocks until that
+// copy has read the buffer, so the next writer cannot race the DMA.
 struct HostBuf {
   void* p = nullptr;
   size_t n = 0;
+  hipEvent_t done = nullptr;
   template <typename T>
   T* as() const { return static_cast<T*>(p); }
+  int wait() {
+    if (done && hipEventSynchronize(done) != hipSuccess) return fail(SG_ERR_DEVICE, "hipEventSynchronize failed");
+    return SG_OK;
+  }
+  int record(hipStream_t s) {
+    if (!done && hipEventCreateWithFlags(&done, hipEventDisableTiming) != hipSuccess) {
+      done = nullptr;
+      return fail(SG_ERR_DEVICE, "hipEventCreateWithFlags failed");
+    }
+    if (hipEventRecord(done, s) != hipSuccess) return fail(SG_ERR_DEVICE, "hipEventRecord failed");
+    return SG_OK;
+  }
   int ensure(size_t bytes) {
+    if (wait() != SG_OK) return SG_ERR_DEVICE;
     if (bytes <= n) return SG_OK;
     if (p) (void)hipHostFree(p);
     p = nullptr;
@@ -80,6 +97,9 @@ struct HostBuf {
     return SG_OK;
   }
   void release() {
+    (void)wait();
+    if (done) (void)hipEventDestroy(done);
+    done = nullptr;
     if (p) (void)hipHostFree(p);
     p = nullptr;
     n = 0;
