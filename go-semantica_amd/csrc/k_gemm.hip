@@ -579,9 +579,9 @@ __global__ __launch_bounds__(NW* SG_WAVE) void k_gemm_q8_sp(const _Float16* __re
   gemm_epilogue<NW, TM, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
 }
 
-// Direct-to-LDS variant.  Workgroup: NW waves x 32 rows, 32*TN columns.
+// Direct-to-LDS kernel.  Workgroup: NW waves x 32 rows, 32*TN columns.
 // Every K-block's A tile (each wave's own 32 rows), weight tile and scales are
-// copied global -> LDS by global_load_lds_dwordx4/dword (no staging
+// copied global -> LDS by buffer_load_dwordx4/dword ... lds (no staging
 // registers) into a ring of STAGES buffers, STAGES-1 blocks ahead.  Each wave
 // issues the same number of copies per block, CPB (clamped, redundant past
 // the last block), so one constant s_waitcnt vmcnt covers "this wave's copies
@@ -590,128 +590,39 @@ __global__ __launch_bounds__(NW* SG_WAVE) void k_gemm_q8_sp(const _Float16* __re
 // are stored in 64-byte lines with the 16-byte chunks XOR-swizzled by row, so
 // fragment reads are conflict-free; the swizzle is applied by choosing which
 // global chunk each lane copies.  Large M uses 8 waves, 4 subtiles, 3 stages
-// (two workgroups per CU); small M uses small workgroups with a deep ring, as
-// its K loop is bound by copy latency, not by throughput.
+// (two workgroups per CU); mid-size M uses 4 waves with a deep ring, as its K
+// loop is bound by copy latency, not by throughput.
+//
+// A copy costs no vector instruction: each K-block's buffer descriptors (64-bit
+// base = this tile's part of the block slice) are built on the scalar unit,
+// the per-lane byte offsets are loop-invariant and M0 is scalar.  (The flat
+// global_load_lds form needed a 64-bit vector add and a readfirstlane per
+// copy.)  The K loop is unrolled by the ring depth, so every LDS fragment read
+// is a loop-invariant vector address plus an immediate; the LDS is laid out
+// [A stages][W stages][scale stages] to keep those immediates under 64 KB.
+// Only the MFMAs and the FMAs of the block-serial epilogue are vector work.
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-template <int NW, int TN, bool GELU, int STAGES>
-__global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_dl(
-    const _Float16* __restrict__ A, int a_rows, const _Float16* __restrict__ W, const float* __restrict__ St,
-    const float* __restrict__ row_scale, float* __restrict__ Y, int M, int N, int K,
-    const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
-  constexpr int BN = TN * 32;
-  constexpr int A_BYTES = NW * 32 * 64, W_BYTES = BN * 64, S_BYTES = BN * 4;
-  constexpr int STAGE = A_BYTES + W_BYTES + S_BYTES;
-  constexpr int WROWS = BN / NW;               // weight rows each wave copies (64 B each)
-  constexpr int WCOPIES = (WROWS + 15) / 16;   // 1-KB copies per wave for them
-  constexpr int SLANES = BN / NW;              // scales each wave copies
-  constexpr int CPB = 2 + WCOPIES + 1;         // copies per wave per K-block
-  static_assert(BN % NW == 0 && SLANES <= SG_WAVE, "weight tile split over the waves");
-  static_assert(STAGES >= 3 && (STAGES - 2) * CPB <= 63, "vmcnt covers the copies in flight");
-  __shared__ __attribute__((aligned(16))) unsigned char lds[STAGES * STAGE];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lr = lane & 31, lh = lane >> 5;
-  int bx, by;
-  xcd_tile(bx, by);
-  const int n0 = bx * BN;
-  const int mw = by * NW * 32 + wave * 32;
-  const int nb = K >> 5;
-  auto swz = [](int r, int c) { return c ^ ((r >> 2) & 3); };  // chunk slot of chunk c in row r
-
-  // Copy sources for this lane (block 0); block b adds b * (rows * 32) halves.
-  // A: two 1-KB copies per wave, lane -> row 16j + lane/4, slot lane%4.
-  const _Float16* asrc[2];
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int r = 16 * j + (lane >> 2);
-    asrc[j] = A + (int64_t)(mw + r) * 32 + 8 * swz(r, lane & 3);
-  }
-  const int64_t a_bstride = (int64_t)a_rows * 32;
-  // W: WROWS rows per wave, copy j -> rows WROWS*wave + 16j + lane/4.
-  const _Float16* wsrc[WCOPIES];
-#pragma unroll
-  for (int j = 0; j < WCOPIES; j++) {
-    const int wr = WROWS * wave + 16 * j + (lane >> 2);
-    wsrc[j] = W + (int64_t)min(n0 + wr, N - 1) * 32 + 8 * swz(wr, lane & 3);
-  }
-  const int64_t w_bstride = (int64_t)N * 32;
-  const float* ssrc = St + min(n0 + SLANES * wave + lane, N - 1);
-
-  auto issue = [&](int b, int st) {
-    unsigned char* base = lds + st * STAGE;
-#pragma unroll
-    for (int j = 0; j < 2; j++)
-      __builtin_amdgcn_global_load_lds((const void*)(asrc[j] + b * a_bstride), base + wave * 2048 + j * 1024, 16, 0,
-                                       0);
-#pragma unroll
-    for (int j = 0; j < WCOPIES; j++)
-      if (16 * j + (lane >> 2) < WROWS)
-        __builtin_amdgcn_global_load_lds((const void*)(wsrc[j] + b * w_bstride),
-                                         base + A_BYTES + WROWS * 64 * wave + j * 1024, 16, 0, 0);
-    if (lane < SLANES)
-      __builtin_amdgcn_global_load_lds((const void*)(ssrc + (int64_t)b * N),
-                                       base + A_BYTES + W_BYTES + wave * (SLANES * 4), 4, 0, 0);
-  };
-
-  f32x16_t acc[1][TN];
-#pragma unroll
-  for (int tn = 0; tn < TN; tn++)
-#pragma unroll
-    for (int r = 0; r < 16; r++) acc[0][tn][r] = 0.0f;
-
-#pragma unroll
-  for (int i = 0; i < STAGES - 1; i++) issue(min(i, nb - 1), i);
-  const f32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-  for (int b = 0; b < nb; b++) {
-    const int st = b % STAGES;
-    wait_vmcnt<(STAGES - 2) * CPB>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    issue(min(b + STAGES - 1, nb - 1), (b + STAGES - 1) % STAGES);
-    const unsigned char* base = lds + st * STAGE;
-    const unsigned char* arow = base + wave * 2048 + lr * 64;
-    Frag fa;
-    fa.lo = *reinterpret_cast<const half8_t*>(arow + 16 * swz(lr, 2 * lh));
-    fa.hi = *reinterpret_cast<const half8_t*>(arow + 16 * swz(lr, 2 * lh + 1));
-#pragma unroll
-    for (int tn = 0; tn < TN; tn++) {
-      const int rr = 32 * tn + lr;
-      const unsigned char* wrow = base + A_BYTES + rr * 64;
-      const half8_t wlo = *reinterpret_cast<const half8_t*>(wrow + 16 * swz(rr, 2 * lh));
-      const half8_t whi = *reinterpret_cast<const half8_t*>(wrow + 16 * swz(rr, 2 * lh + 1));
-      const float d = *reinterpret_cast<const float*>(base + A_BYTES + W_BYTES + 4 * rr);
-      f32x16_t pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa.lo, wlo, zero, 0, 0, 0);
-      pp = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa.hi, whi, pp, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[0][tn][r] = __builtin_fmaf(pp[r], d, acc[0][tn][r]);
-    }
-  }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // redundant tail copies drained before exit
-  gemm_epilogue<NW, 1, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
-}
-
-// Buffer-load variant of the 8-wave direct-to-LDS kernel (same tiles, same
-// arithmetic, same 3-stage ring).  Its copies are buffer_load ... lds with a
-// per-block buffer descriptor built on the scalar unit, so a copy costs no
-// vector instruction (the flat form needs a 64-bit vector add and a
-// readfirstlane per copy), and the K loop is unrolled by the ring depth so
-// every LDS fragment read is a loop-invariant vector address plus an
-// immediate (the LDS is laid out [A stages][W stages][scale stages] to keep
-// those immediates under 64 KB).  Only the FMAs of the block-serial
-// epilogue and the MFMAs stay on the vector side of the loop.
 constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor, gfx9 family
 
-template <int NW, int TN, bool GELU>
-__global__ __launch_bounds__(NW * SG_WAVE, 4) void k_gemm_q8_bl(
+// f(integral_constant<int, I>) for I = I0 .. N-1, unrolled at compile time.
+template <int I, int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
+}
+
+template <int NW, int TN, bool GELU, int STAGES>
+__global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_bl(
     const _Float16* __restrict__ A, int a_rows, const _Float16* __restrict__ W, const float* __restrict__ St,
     const float* __restrict__ row_scale, float* __restrict__ Y, int M, int N, int K,
     const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
-  constexpr int STAGES = 3;
   constexpr int BM = NW * 32, BN = TN * 32;
   constexpr int A_BYTES = BM * 64, W_BYTES = BN * 64, S_BYTES = BN * 4;
   constexpr int W_OFF = STAGES * A_BYTES, S_OFF = W_OFF + STAGES * W_BYTES;
@@ -735,28 +646,30 @@ __global__ __launch_bounds__(NW * SG_WAVE, 4) void k_gemm_q8_bl(
   const int nb = K >> 5;
   auto swz = [](int r, int c) { return c ^ ((r >> 2) & 3); };  // chunk slot of chunk c in row r
 
-  // Copy sources: byte offsets inside block b's slice of A ([a_rows][32]
-  // halves), of W ([N][32]) and of the scales ([N] floats).
+  // Copy sources: byte offsets inside this tile's part of block b: its BM
+  // rows of A's block slice ([a_rows][32] halves), its BN rows of W's
+  // ([N][32]) and its BN scales ([N] floats).  The descriptors' 64-bit bases
+  // carry the rest, so no size limit applies.
   uint32_t aoff[2];
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     const int r = 16 * j + (lane >> 2);
-    aoff[j] = (uint32_t)(mw + r) * 64u + 16u * swz(r, lane & 3);
+    aoff[j] = (uint32_t)(wave * 32 + r) * 64u + 16u * swz(r, lane & 3);
   }
   // One 1-KB weight copy per wave.  (A guarded loop over an array of copy
   // offsets here made the host pass drop the kernel's launch stub.)
   static_assert(WROWS == 16, "one 1-KB weight copy per wave");
   const int wrow = WROWS * wave + (lane >> 2);
-  const uint32_t woff = (uint32_t)min(n0 + wrow, N - 1) * 64u + 16u * swz(wrow, lane & 3);
-  const uint32_t soff = (uint32_t)min(n0 + SLANES * wave + lane, N - 1) * 4u;
+  const uint32_t woff = (uint32_t)(min(n0 + wrow, N - 1) - n0) * 64u + 16u * swz(wrow, lane & 3);
+  const uint32_t soff = (uint32_t)(min(n0 + SLANES * wave + lane, N - 1) - n0) * 4u;
 
   auto issue = [&](int b, int st) {
-    __amdgpu_buffer_rsrc_t ra =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(A + (int64_t)b * a_rows * 32), 0, a_rows * 64, kBufWord3);
+    __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(A + ((int64_t)b * a_rows + (int64_t)by * BM) * 32), 0, A_BYTES, kBufWord3);
     __amdgpu_buffer_rsrc_t rw =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(W + (int64_t)b * N * 32), 0, N * 64, kBufWord3);
+        __builtin_amdgcn_make_buffer_rsrc((void*)(W + ((int64_t)b * N + n0) * 32), 0, W_BYTES, kBufWord3);
     __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(St + (int64_t)b * N), 0, N * 4, kBufWord3);
+        __builtin_amdgcn_make_buffer_rsrc((void*)(St + (int64_t)b * N + n0), 0, S_BYTES, kBufWord3);
 #pragma unroll
     for (int j = 0; j < 2; j++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)(lds + st * A_BYTES + wave * 2048 + j * 1024), 16,
@@ -803,39 +716,25 @@ __global__ __launch_bounds__(NW * SG_WAVE, 4) void k_gemm_q8_bl(
     }
   };
 
-  issue(0, 0);
-  issue(min(1, nb - 1), 1);
-  for (int b = 0; b < nb; b += STAGES) {
-    step(std::integral_constant<int, 0>{}, b);
-    if (b + 1 < nb) step(std::integral_constant<int, 1>{}, b + 1);
-    if (b + 2 < nb) step(std::integral_constant<int, 2>{}, b + 2);
-  }
+  static_assert(STAGES >= 3 && (STAGES - 2) * CPB <= 63, "vmcnt covers the copies in flight");
+  static_for<0, STAGES - 1>([&](auto ic) { issue(min((int)decltype(ic)::value, nb - 1), decltype(ic)::value); });
+  for (int b = 0; b < nb; b += STAGES)
+    static_for<0, STAGES>([&](auto ic) {
+      if (b + decltype(ic)::value < nb) step(ic, b + decltype(ic)::value);
+    });
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // redundant tail copies drained before exit
   gemm_epilogue<NW, 1, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
 }
 
-template <int NW, int TN, bool GELU>
+template <int NW, int TN, bool GELU, int STAGES>
 hipError_t launch_bl(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
                      int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
   constexpr int BM = NW * 32, BN = TN * 32;
   const int gm = (M + BM - 1) / BM;
   if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
-  if ((int64_t)a_rows * 64 > INT32_MAX || (int64_t)N * 64 > INT32_MAX) return hipErrorInvalidValue;  // descriptor sizes
   dim3 grid((N + BN - 1) / BN, gm);
-  hipLaunchKernelGGL((k_gemm_q8_bl<NW, TN, GELU>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y, M, N, K,
+  hipLaunchKernelGGL((k_gemm_q8_bl<NW, TN, GELU, STAGES>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y, M, N, K,
                      row_seq, amax);
-  return hipGetLastError();
-}
-
-template <int NW, int TN, bool GELU, int STAGES>
-hipError_t launch_dl(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
-                     int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
-  constexpr int BM = NW * 32, BN = TN * 32;
-  const int gm = (M + BM - 1) / BM;
-  if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
-  dim3 grid((N + BN - 1) / BN, gm);
-  hipLaunchKernelGGL((k_gemm_q8_dl<NW, TN, GELU, STAGES>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y,
-                     M, N, K, row_seq, amax);
   return hipGetLastError();
 }
 
@@ -877,8 +776,6 @@ hipError_t launch(const _Float16* A, int a_rows, const _Float16* W, const float*
 
 // Workgroups of the 8-wave direct-to-LDS launch.
 inline int64_t dl8_blocks(int M, int N) { return (int64_t)((M + 255) / 256) * ((N + 127) / 128); }
-// The buffer-load kernel's descriptors hold a block slice's size in 32 bits.
-inline bool bl_fits(int a_rows, int N) { return (int64_t)a_rows * 64 <= INT32_MAX && (int64_t)N * 64 <= INT32_MAX; }
 
 }  // namespace
 
@@ -890,16 +787,13 @@ hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float
   if (K <= 0 || K % 32) return hipErrorInvalidValue;
   if (sums) return launch<1, 1, 1, 1, true>(A, a_rows, W, St, row_scale, Y, sums, M, N, K, s);
   // Direct-to-LDS workgroups of 8 waves (256 rows x 128 columns, 3-stage
-  // copy ring, buffer-load copies) once they cover half the compute units
-  // (the flat-copy form only past 32-bit descriptor sizes); below that, from 4096
+  // copy ring, buffer-load copies) once they cover half the compute units;
+  // below that, from 4096
   // rows, 4 waves x 64 columns with a 6-stage ring; otherwise 64x64
   // register-direct tiles, whose grid still covers the chip (tile sweeps on
   // MI355X at the model's shapes, M = 32 .. 4096).
-  if (M >= 8192 || dl8_blocks(M, N) >= 128) {
-    if (bl_fits(a_rows, N)) return launch_bl<8, 4, false>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
-    return launch_dl<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
-  }
-  if (M >= 4096) return launch_dl<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+  if (M >= 8192 || dl8_blocks(M, N) >= 128) return launch_bl<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+  if (M >= 4096) return launch_bl<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   return launch<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
 }
 
@@ -908,11 +802,8 @@ hipError_t gemm_q8_gelu(const _Float16* A, int a_rows, const _Float16* W, const 
   if (M <= 0 || Nh <= 0) return hipSuccess;
   if (K <= 0 || K % 32 || Nh % 32) return hipErrorInvalidValue;
   if (amax && !row_seq) return hipErrorInvalidValue;
-  if (M >= 8192 || dl8_blocks(M, 2 * Nh) >= 128) {
-    if (bl_fits(a_rows, 2 * Nh))
-      return launch_bl<8, 4, true>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
-    return launch_dl<8, 4, true, 3>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
-  }
+  if (M >= 8192 || dl8_blocks(M, 2 * Nh) >= 128)
+    return launch_bl<8, 4, true, 3>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
   return launch_sp<4, 1, 2, true>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
 }
 

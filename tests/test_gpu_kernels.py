@@ -158,11 +158,12 @@ def test_gemm_seam_async_across_streams(gpu_ctx, oracle):
 
 
 @pytest.mark.parametrize("M", [4500, 8200])
-@pytest.mark.parametrize("N,K", [(1280, 768), (768, 1152)])
+@pytest.mark.parametrize("N,K", [(1280, 768), (768, 1152), (768, 800)])
 def test_gemm_large_m(gpu_ctx, oracle, M, N, K):
     """The direct-to-LDS kernels (8 waves x 128 columns at M = 8200 and at
     4500 x 1280; 4 waves x 64 columns with a 6-stage ring at 4500 x 768;
-    ragged last tiles): first and last rows bit-exact to the block-serial
+    ragged last tiles; K = 800 leaves 25 blocks, a partial last round of the
+    ring-unrolled K loop): first and last rows bit-exact to the block-serial
     order, every row within 1e-5 of AVX2's."""
     import torch
     from semantica_gpu import kernels, synth
