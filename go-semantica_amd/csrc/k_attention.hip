@@ -38,9 +38,10 @@
 // one query and 8 keys of the tile, so row max and row sum are lane-local
 // plus two exchanges, and those 8 registers are exactly the B operand of
 // O^T += V^T P^T (one 32-key MFMA step) once V^T's keys are stored in the
-// matching order (vt_key; k_v_split_t writes that order).
+// matching order (sgd::vt_key; the V^T split writes that order).
 #include "sg_device.h"
 #include "sg_kernels.h"
+#include "sg_kv_prep.h"
 
 namespace {
 
@@ -63,12 +64,9 @@ __device__ __forceinline__ f32x4_t mfma16(half8_t a, half8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Key order inside a V^T tile row.  Lane group g (lane/16) holds the S^T
-// entries of keys 4g..4g+3 (first 16-key subtile) and 16+4g..16+4g+3
-// (second); as the B operand of a 32-key MFMA step its slots are positions
-// 8g..8g+7, so key k is stored at position 8*((k&15)>>2) + 4*(k>>4) + (k&3)
-// and position p holds key:
-__device__ __forceinline__ int vt_key(int p) { return ((p & 4) << 2) | ((p & 24) >> 1) | (p & 3); }
+// V^T tiles hold their keys in sgd::vt_key order (sg_kv_prep.h), which makes
+// the eight S^T registers a lane holds per 32-key tile the B operand of one
+// O^T += V^T P^T step.
 
 // QPRE: Q arrives as the QKV GEMM's fp32 output and each wave applies
 // attn_q_norm and RoPE to its 16 rows itself (the arithmetic of
@@ -412,55 +410,38 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
   }
 }
 
-// V [T][ldv] fp32 (kv head blockIdx.y at column 256*kvh) -> V^T hi/lo fp16
-// [HKV*256][ldvt]: sequence s occupies columns voff[s] .. voff[s] + 32*ceil(S/32),
-// keys in vt_key order inside every 32-key tile, zeros past S.  The 32 x 256
-// fp32 tile is loaded with coalesced float4 rows into LDS; a thread then owns
-// one (dim, 8-key chunk), reads its 8 keys down the LDS column and stores the
-// chunk's hi and lo halves as two 16-byte writes (4 threads cover one dim's
-// 64 contiguous bytes).
-__global__ __launch_bounds__(256) void k_v_split_t(const float* __restrict__ v, int ldv,
-                                                   const int32_t* __restrict__ seq_off,
-                                                   const int32_t* __restrict__ voff,
-                                                   const sg_item* __restrict__ vtiles, _Float16* __restrict__ vth,
-                                                   _Float16* __restrict__ vtl, int ldvt) {
-  constexpr int RS = kHD + 4;  // fp32 row stride
-  __shared__ __attribute__((aligned(16))) float tv[kBK][RS];
-  const sg_item t = vtiles[blockIdx.x];
-  const int kvh = blockIdx.y;
-  const int r0 = seq_off[t.seq], S = seq_off[t.seq + 1] - r0, k0 = t.c0;
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int u = 0; u < 8; u++) {  // 32 keys x 64 float4
-    const int idx = tid + 256 * u;
-    const int key = idx >> 6, d4 = idx & 63;
-    f32x4_t x = {0, 0, 0, 0};
-    if (k0 + key < S) x = *reinterpret_cast<const f32x4_t*>(v + (int64_t)(r0 + k0 + key) * ldv + kvh * kHD + 4 * d4);
-    *reinterpret_cast<f32x4_t*>(&tv[key][4 * d4]) = x;
-  }
-  __syncthreads();
-  const int64_t col = voff[t.seq] + k0;
-#pragma unroll
-  for (int u = 0; u < 4; u++) {  // 256 dims x 4 chunks of 8 key positions
-    const int dim = (tid >> 2) + 64 * u, c = tid & 3;
-    uint32_t hw[4], lw[4];
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-      uint32_t hb[2], lb[2];
-#pragma unroll
-      for (int e = 0; e < 2; e++) {
-        const int p = 8 * c + 2 * m + e;                   // position in the tile row
-        const int key = vt_key(p);
-        const hl16 sp = split_f16(tv[key][dim]);
-        hb[e] = __builtin_bit_cast(uint16_t, sp.hi);
-        lb[e] = __builtin_bit_cast(uint16_t, sp.lo);
-      }
-      hw[m] = hb[0] | (hb[1] << 16);
-      lw[m] = lb[0] | (lb[1] << 16);
-    }
-    const int64_t o = (int64_t)(kvh * kHD + dim) * ldvt + col + 8 * c;
-    *reinterpret_cast<uint4*>(vth + o) = uint4{hw[0], hw[1], hw[2], hw[3]};
-    *reinterpret_cast<uint4*>(vtl + o) = uint4{lw[0], lw[1], lw[2], lw[3]};
+// V^T split, one 32-key tile per workgroup (sgd::v_split_tile); kv head blockIdx.y.
+__global__ __launch_bounds__(sgd::kKvThreads) void k_v_split_t(const float* __restrict__ v, int ldv,
+                                                             const int32_t* __restrict__ seq_off,
+                                                             const int32_t* __restrict__ voff,
+                                                             const sg_item* __restrict__ vtiles,
+                                                             _Float16* __restrict__ vth, _Float16* __restrict__ vtl,
+                                                             int ldvt) {
+  __shared__ __attribute__((aligned(16))) float tv[kBK][sgd::kVtRowStride];
+  sgd::v_split_tile(vtiles[blockIdx.x], blockIdx.y, tv, v, ldv, seq_off, voff, vth, vtl, ldvt);
+}
+
+// K's QK-norm/RoPE split and V's V^T split in one launch: workgroups
+// [0, nkb) take 32 (token, kv head) rows of K each, the rest one (V tile,
+// kv head) each, so the two halves' loads and stores overlap.
+__global__ __launch_bounds__(sgd::kKvThreads) void k_kv_prep(
+    const float* __restrict__ k, const float* __restrict__ v, int ldkv, const float* __restrict__ kw, int HKV, int T,
+    const int32_t* __restrict__ row_pos, const float* __restrict__ cos_t, const float* __restrict__ sin_t, float eps,
+    _Float16* __restrict__ ks_h, _Float16* __restrict__ ks_l, int ldks, int nkb, const int32_t* __restrict__ seq_off,
+    const int32_t* __restrict__ voff, const sg_item* __restrict__ vtiles, int n_vtiles, _Float16* __restrict__ vth,
+    _Float16* __restrict__ vtl, int ldvt) {
+  __shared__ __attribute__((aligned(16))) float tv[kBK][sgd::kVtRowStride];
+  const int b = blockIdx.x;
+  if (b < nkb) {  // workgroup-uniform
+    const int64_t g = (int64_t)b * sgd::kKvRows + (threadIdx.x >> 3);
+    float* tile = &tv[0][0] + (threadIdx.x / SG_WAVE) * (8 * 40);  // 8 x 40 floats per wave
+    // No query heads (H = 0): the Q arguments are never read.  (Passing null
+    // for them crashed this compiler's device pass.)
+    sgd::qk_split_group(g, threadIdx.x & 7, (threadIdx.x >> 3) & 7, tile, k, ldkv, k, ldkv, kw, kw, 0, HKV, T,
+                        row_pos, cos_t, sin_t, eps, ks_h, ks_l, ldks, ks_h, ks_l, ldks);
+  } else {
+    const int vb = b - nkb;
+    sgd::v_split_tile(vtiles[vb % n_vtiles], vb / n_vtiles, tv, v, ldkv, seq_off, voff, vth, vtl, ldvt);
   }
 }
 
@@ -493,6 +474,22 @@ hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int3
   if ((ldv & 3) || (ldvt & 7)) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_v_split_t, dim3(n_vtiles, HKV), dim3(256), 0, s, v, ldv, seq_off, voff, vtiles, vth, vtl,
                      ldvt);
+  return hipGetLastError();
+}
+
+hipError_t kv_prep(const float* k, const float* v, int ldkv, const float* kw, int HKV, int T, const int32_t* row_pos,
+                   const float* cos_t, const float* sin_t, float eps, _Float16* ks_h, _Float16* ks_l, int ldks,
+                   const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vth,
+                   _Float16* vtl, int ldvt, hipStream_t s) {
+  if (T <= 0 || n_vtiles <= 0 || HKV <= 0) return hipSuccess;
+  if ((ldkv & 3) || (ldks & 7) || (ldvt & 7) || (reinterpret_cast<uintptr_t>(k) & 15) ||
+      (reinterpret_cast<uintptr_t>(v) & 15) || (kw && (reinterpret_cast<uintptr_t>(kw) & 15)))
+    return hipErrorInvalidValue;  // float4 loads of K and V rows and of the weights
+  const int64_t nkb = ((int64_t)T * HKV + sgd::kKvRows - 1) / sgd::kKvRows;
+  const int64_t nb = nkb + (int64_t)n_vtiles * HKV;
+  if (nb > INT32_MAX) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_kv_prep, dim3((unsigned)nb), dim3(sgd::kKvThreads), 0, s, k, v, ldkv, kw, HKV, T, row_pos, cos_t,
+                     sin_t, eps, ks_h, ks_l, ldks, (int)nkb, seq_off, voff, vtiles, n_vtiles, vth, vtl, ldvt);
   return hipGetLastError();
 }
 

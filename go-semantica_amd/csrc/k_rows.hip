@@ -8,6 +8,7 @@
 // squares is reproduced bit for bit (see sg_rmsnorm8 in sg_device.h).
 #include "sg_device.h"
 #include "sg_kernels.h"
+#include "sg_kv_prep.h"
 
 namespace {
 
@@ -449,54 +450,11 @@ __global__ __launch_bounds__(kThreads) void k_qknorm_rope_split(
     const float* __restrict__ kw, int H, int HKV, int T, const int32_t* __restrict__ row_pos,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, float eps, _Float16* __restrict__ qs_h,
     _Float16* __restrict__ qs_l, int ldqs, _Float16* __restrict__ ks_h, _Float16* __restrict__ ks_l, int ldks) {
-  constexpr int NC = 8, HALF = 128;
+  static_assert(kThreads == sgd::kKvThreads && kRowsPerBlock == sgd::kKvRows, "one 8-lane group per row");
   __shared__ __attribute__((aligned(16))) float tiles[kThreads / SG_WAVE][8 * 40];
   const int64_t g = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
-  const int j = threadIdx.x & 7, r = (threadIdx.x >> 3) & 7;
-  const int per = H + HKV;
-  if (g >= (int64_t)T * per) return;  // whole 8-lane groups
-  const int t = (int)(g / per), hh = (int)(g % per);
-  const float* src = hh < H ? q + (int64_t)t * ldq + hh * 256 : k + (int64_t)t * ldk + (hh - H) * 256;
-  f32x4_t x[NC];
-#pragma unroll
-  for (int c = 0; c < NC; c++) x[c] = *reinterpret_cast<const f32x4_t*>(src + 32 * c + 4 * j);
-  const float* wn = hh < H ? qw : kw;
-  if (wn) sg_rmsnorm8_f4<NC>(x, wn, tiles[threadIdx.x / SG_WAVE], r, j, eps);
-  const int pos = row_pos[t];
-  const float* cr = cos_t + (int64_t)pos * HALF + 4 * j;
-  const float* sr = sin_t + (int64_t)pos * HALF + 4 * j;
-#pragma unroll
-  for (int c = 0; c < NC / 2; c++) {
-    const f32x4_t cv = *reinterpret_cast<const f32x4_t*>(cr + 32 * c);
-    const f32x4_t sv = *reinterpret_cast<const f32x4_t*>(sr + 32 * c);
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const float v0 = x[c][u], v1 = x[c + NC / 2][u];
-      const float a = v0 * cv[u], b = v1 * sv[u], cc = v0 * sv[u], dd = v1 * cv[u];
-      x[c][u] = a - b;
-      x[c + NC / 2][u] = cc + dd;
-    }
-  }
-  _Float16 *dh, *dl;
-  if (hh < H) {
-    dh = qs_h + (int64_t)t * ldqs + hh * 256;
-    dl = qs_l + (int64_t)t * ldqs + hh * 256;
-  } else {
-    dh = ks_h + (int64_t)t * ldks + (hh - H) * 256;
-    dl = ks_l + (int64_t)t * ldks + (hh - H) * 256;
-  }
-#pragma unroll
-  for (int c = 0; c < NC; c++) {
-    half4_t hv, lv;
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const hl16 sp = split_f16(x[c][u] * sgk::kAttnQKScale);
-      hv[u] = sp.hi;
-      lv[u] = sp.lo;
-    }
-    *reinterpret_cast<half4_t*>(dh + 32 * c + 4 * j) = hv;
-    *reinterpret_cast<half4_t*>(dl + 32 * c + 4 * j) = lv;
-  }
+  sgd::qk_split_group(g, threadIdx.x & 7, (threadIdx.x >> 3) & 7, tiles[threadIdx.x / SG_WAVE], q, ldq, k, ldk, qw,
+                      kw, H, HKV, T, row_pos, cos_t, sin_t, eps, qs_h, qs_l, ldqs, ks_h, ks_l, ldks);
 }
 
 // ------------------------------------------------------------ GELU * up --

@@ -427,13 +427,12 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d),
               sgk::norm_quantize(h, ly.attn_norm, eps, T, d, meta.row_seq, site(l, 0), a16, ar, sx, s));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), sgk::gemm_q8(a16, ar, ly.wqkv, ly.sqkv, sx, qkv, nullptr, T, nqkv, d, s));
-    // K's QK-norm + RoPE here (H = 0: K rows only); Q's inside the attention kernel.
-    SG_LAUNCH(SG_K_NORM, t * kvd * 8.0,
-              sgk::qknorm_rope(nullptr, nqkv, qkv + qd, nqkv, ly.q_norm, ly.k_norm, 0, c.num_kv_heads, T,
-                               meta.row_pos, m->cos_t, m->sin_t, eps, nullptr, nullptr, 0, ks_h, ks_l, kvd, s));
-    SG_LAUNCH(SG_K_NORM, t * kvd * 8.0,
-              sgk::v_split_t(qkv + qd + kvd, nqkv, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles,
-                             c.num_kv_heads, vt_h, vt_l, meta.Tp, s));
+    // K's QK-norm + RoPE + split and V's V^T split in one launch; Q's norm and
+    // RoPE run inside the attention kernel.
+    SG_LAUNCH(SG_K_NORM, t * kvd * 16.0,
+              sgk::kv_prep(qkv + qd, qkv + qd + kvd, nqkv, ly.k_norm, c.num_kv_heads, T, meta.row_pos, m->cos_t,
+                           m->sin_t, eps, ks_h, ks_l, kvd, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles, vt_h,
+                           vt_l, meta.Tp, s));
     const sg_attn_qpre qpre{qkv, nqkv, ly.q_norm, m->cos_t, m->sin_t, meta.row_pos, eps};
     SG_LAUNCH(SG_K_ATTENTION, attn_flops,
               sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, vt_l, meta.Tp, att, qd, meta.seq_off,

@@ -112,6 +112,12 @@ inline int attn_key_pad(int S) { return (S + 31) / 32 * 32; }
 // keys permuted within 32-key tiles, zero past S); vtiles: (seq, key0) per 32 keys.
 hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles,
                      int n_vtiles, int HKV, _Float16* vth, _Float16* vtl, int ldvt, hipStream_t s);
+// qknorm_rope's K-only split (H = 0) and v_split_t in one launch: K and V
+// share the row stride ldkv (columns of the QKV output).
+hipError_t kv_prep(const float* k, const float* v, int ldkv, const float* kw, int HKV, int T, const int32_t* row_pos,
+                   const float* cos_t, const float* sin_t, float eps, _Float16* ks_h, _Float16* ks_l, int ldks,
+                   const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vth,
+                   _Float16* vtl, int ldvt, hipStream_t s);
 // rows x cols of x -> hi/lo fp16 of x*scale (row stride ldo).
 hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, _Float16* hi, _Float16* lo, int ldo,
                       hipStream_t s);
