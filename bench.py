@@ -339,15 +339,18 @@ def main():
             k["GB_s"] = round(p["work"] / (p["ms"] * 1e-3) / 1e9, 1)
         kernels[name] = k
 
-    # Algorithmic HBM bytes of one step's GEMMs (fp16 A, fp16 W, fp32 block scales,
+    # Algorithmic HBM bytes of one step's GEMMs (A and W operands, fp32 block scales,
     # fp32 row scales, fp32 output; the gate/up GEMM writes only g = geluquick(gate)*up).
+    # The operands are int8 from 4096 tokens (the library's int8-operand GEMMs), fp16
+    # integers below.
     c = mdl.config
     d, ff, T = c["embed_dim"], c["interm_dim"], B * S
     hd = d // c["num_heads"]
     qd, kvd = c["num_heads"] * hd, c["num_kv_heads"] * hd
+    ob = 1 if T >= 4096 else 2
 
     def gemm_bytes(N, K, out_cols):
-        return T * K * 2 + N * K * 2 + N * (K // 32) * 4 + T * 4 + T * out_cols * 4
+        return T * K * ob + N * K * ob + N * (K // 32) * 4 + T * 4 + T * out_cols * 4
 
     step_gemm_bytes = c["num_layers"] * (gemm_bytes(qd + 2 * kvd, d, qd + 2 * kvd) + gemm_bytes(d, qd, d) +
                                           gemm_bytes(2 * ff, d, ff) + gemm_bytes(d, ff, d))

@@ -28,6 +28,9 @@
 #include "sg_device.h"
 #include "sg_kernels.h"
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
+
 namespace {
 
 struct Frag {
@@ -738,6 +741,113 @@ hipError_t launch_bl(const _Float16* A, int a_rows, const _Float16* W, const flo
   return hipGetLastError();
 }
 
+// int8-operand form of k_gemm_q8_bl: A and W hold the int8 values
+// themselves (A [K/32][a_rows][32], W [K/32][N][32]), and one
+// v_mfma_i32_32x32x32_i8 per subtile and block gives the exact block sum
+// P_b as int32 (|P_b| <= 516,128, so its conversion to float is exact); the
+// per-block FMA is unchanged, so the outputs are bit-identical to the fp16
+// form.  Half the bytes are copied and read from LDS, one MFMA replaces two,
+// and 16 converts per subtile and block are added.  LDS per stage:
+// A [2 halves][BM rows][16 B], W [2][BN][16 B], scales [BN]: lane l of an
+// MFMA operand reads row l % 32, bytes 16*(l / 32) .. +15 of its 32-byte
+// block, so each fragment read is 1 KB of contiguous LDS.  Copies: NW / 2
+// waves per half, each copying 64 A rows (one 1-KB copy) and, with 32
+// lanes, 32 W rows (BN = 16 * NW); the other scheme (scalar descriptors,
+// ring unrolled by STAGES, one vmcnt per block) is k_gemm_q8_bl's.
+template <int NW, int TN, bool GELU, int STAGES>
+__global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_i8(
+    const int8_t* __restrict__ A, int a_rows, const int8_t* __restrict__ W, const float* __restrict__ St,
+    const float* __restrict__ row_scale, float* __restrict__ Y, int M, int N, int K,
+    const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
+  constexpr int NWH = NW / 2;
+  constexpr int BM = NW * 32, BN = TN * 32;
+  static_assert(NW % 2 == 0 && TN == NWH, "copy split: 64 A rows and 32 W rows per wave and half");
+  constexpr int A_BYTES = BM * 32, W_BYTES = BN * 32, S_BYTES = BN * 4;
+  constexpr int W_OFF = STAGES * A_BYTES, S_OFF = W_OFF + STAGES * W_BYTES;
+  constexpr int SLANES = BN / NW;  // scales each wave copies
+  constexpr int CPB = 3;           // copies per wave per K-block
+  static_assert(STAGES >= 3 && (STAGES - 2) * CPB <= 63, "vmcnt covers the copies in flight");
+  static_assert(STAGES * A_BYTES < 65536 && STAGES * W_BYTES < 65536 && STAGES * S_BYTES < 65536,
+                "stage offsets fit the LDS immediate");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[S_OFF + STAGES * S_BYTES];
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  int bx, by;
+  xcd_tile(bx, by);
+  const int n0 = bx * BN;
+  const int mw = by * BM + wave * 32;
+  const int nb = K >> 5;
+  const int ch = wave / NWH, cr = wave % NWH;  // this wave's copy half and row group
+  const uint32_t aoff = (uint32_t)(64 * cr + lane) * 32u + 16u * ch;
+  const uint32_t woff = (uint32_t)(min(n0 + 32 * cr + lr, N - 1) - n0) * 32u + 16u * ch;
+  const uint32_t soff = (uint32_t)(min(n0 + SLANES * wave + lane, N - 1) - n0) * 4u;
+  auto issue = [&](int b, int st) {
+    __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(A + ((int64_t)b * a_rows + (int64_t)by * BM) * 32), 0, A_BYTES, kBufWord3);
+    __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(W + ((int64_t)b * N + n0) * 32), 0, W_BYTES, kBufWord3);
+    __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(St + (int64_t)b * N + n0), 0, S_BYTES, kBufWord3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr)(lds + st * A_BYTES + ch * (BM * 16) + 64 * cr * 16), 16,
+                                             aoff, 0, 0, 0);
+    if (lane < 32)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rw, (lds_ptr)(lds + W_OFF + st * W_BYTES + ch * (BN * 16) + 32 * cr * 16), 16, woff, 0, 0, 0);
+    if (lane < SLANES)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds + S_OFF + st * S_BYTES + wave * (SLANES * 4)), 4,
+                                               soff, 0, 0, 0);
+  };
+  // Fragment read addresses (stage 0; stage st adds st * *_BYTES).
+  const uint32_t ra_f = lh * (BM * 16) + (wave * 32 + lr) * 16;
+  const uint32_t rw_f = W_OFF + lh * (BN * 16) + lr * 16;
+  const uint32_t rd = S_OFF + 4 * lr;
+
+  f32x16_t acc[1][TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; tn++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[0][tn][r] = 0.0f;
+  const i32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  auto step = [&](auto stc, int b) {
+    constexpr int ST = decltype(stc)::value;
+    wait_vmcnt<(STAGES - 2) * CPB>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(min(b + STAGES - 1, nb - 1), (ST + STAGES - 1) % STAGES);
+    const i32x4_t fa = *reinterpret_cast<const i32x4_t*>(lds + ra_f + ST * A_BYTES);
+#pragma unroll
+    for (int tn = 0; tn < TN; tn++) {
+      const i32x4_t fw = *reinterpret_cast<const i32x4_t*>(lds + rw_f + ST * W_BYTES + tn * 512);
+      const float d = *reinterpret_cast<const float*>(lds + rd + ST * S_BYTES + tn * 128);
+      const i32x16_t pp = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fw, zero, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[0][tn][r] = __builtin_fmaf((float)pp[r], d, acc[0][tn][r]);
+    }
+  };
+  static_for<0, STAGES - 1>([&](auto ic) { issue(min((int)decltype(ic)::value, nb - 1), decltype(ic)::value); });
+  for (int b = 0; b < nb; b += STAGES)
+    static_for<0, STAGES>([&](auto ic) {
+      if (b + decltype(ic)::value < nb) step(ic, b + decltype(ic)::value);
+    });
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // redundant tail copies drained before exit
+  gemm_epilogue<NW, 1, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
+}
+
+template <int NW, int TN, bool GELU, int STAGES>
+hipError_t launch_i8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* rs, float* Y, int M,
+                     int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
+  constexpr int BM = NW * 32, BN = TN * 32;
+  const int gm = (M + BM - 1) / BM;
+  if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
+  dim3 grid((N + BN - 1) / BN, gm);
+  hipLaunchKernelGGL((k_gemm_q8_i8<NW, TN, GELU, STAGES>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y,
+                     M, N, K, row_seq, amax);
+  return hipGetLastError();
+}
+
 template <int NW, int TM, int TN, bool GELU = false>
 hipError_t launch_sp(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
                      int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
@@ -795,6 +905,22 @@ hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float
   if (M >= 8192 || dl8_blocks(M, N) >= 128) return launch_bl<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   if (M >= 4096) return launch_bl<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   return launch<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
+}
+
+hipError_t gemm_q8_i8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
+                      int M, int N, int K, hipStream_t s) {
+  if (M <= 0 || N <= 0) return hipSuccess;
+  if (K <= 0 || K % 32) return hipErrorInvalidValue;
+  if (M >= 8192 || dl8_blocks(M, N) >= 128) return launch_i8<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+  return launch_i8<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+}
+
+hipError_t gemm_q8_gelu_i8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale,
+                           float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s) {
+  if (M <= 0 || Nh <= 0) return hipSuccess;
+  if (K <= 0 || K % 32 || Nh % 32) return hipErrorInvalidValue;
+  if (amax && !row_seq) return hipErrorInvalidValue;
+  return launch_i8<8, 4, true, 3>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
 }
 
 hipError_t gemm_q8_gelu(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* row_scale,

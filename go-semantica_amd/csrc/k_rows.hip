@@ -6,6 +6,8 @@
 // rows): lane j of the group owns elements j, j+8, j+16, ... which is the lane
 // structure of the reference's AVX2 fp32 dot product, so RMSNorm's sum of
 // squares is reproduced bit for bit (see sg_rmsnorm8 in sg_device.h).
+#include <type_traits>
+
 #include "sg_device.h"
 #include "sg_kernels.h"
 #include "sg_kv_prep.h"
@@ -22,7 +24,8 @@ __device__ __forceinline__ uint16_t rd_u16(const uint8_t* p) { return (uint16_t)
 // One thread per Q8_0 block: 2-byte fp16 scale + 32 int8 values
 // (GGUF Q8_0 layout; extractQ8_0Scales model_int8.go:543-569 reads the same bytes).
 __global__ void k_repack_q8_0(const uint8_t* __restrict__ raw, int rows, int cols, _Float16* __restrict__ w16,
-                              float* __restrict__ st, int ld, int row_off, int grp, int gstride) {
+                              int8_t* __restrict__ w8, float* __restrict__ st, int ld, int row_off, int grp,
+                              int gstride) {
   const int nb = cols / 32;
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= (int64_t)rows * nb) return;
@@ -37,6 +40,29 @@ __global__ void k_repack_q8_0(const uint8_t* __restrict__ raw, int rows, int col
 #pragma unroll
     for (int t = 0; t < 8; t++) v[t] = (_Float16)(float)(int8_t)blk[2 + i + t];
     *reinterpret_cast<half8_t*>(dst + i) = v;
+  }
+  if (w8) {  // the same values as int8, same layout
+    int8_t* d8 = w8 + ((int64_t)b * ld + dr) * 32;
+#pragma unroll
+    for (int i = 0; i < 32; i++) d8[i] = (int8_t)blk[2 + i];
+  }
+}
+
+// int8 x[M][K] -> block-major int8 y[K/32][a_rows][32]: one thread moves a
+// 16-byte half block (vec: x 16-byte aligned; otherwise byte by byte).
+__global__ void k_i8_blocked(const int8_t* __restrict__ x, int M, int K, int8_t* __restrict__ y, int a_rows,
+                             bool vec) {
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int kq = K / 16;
+  if (id >= (int64_t)M * kq) return;
+  const int m = (int)(id / kq), q = (int)(id % kq);
+  const int8_t* src = x + (int64_t)m * K + 16 * q;
+  int8_t* dst = y + ((int64_t)(q >> 1) * a_rows + m) * 32 + 16 * (q & 1);
+  if (vec) {
+    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; i++) dst[i] = src[i];
   }
 }
 
@@ -209,17 +235,34 @@ __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__
   }
 }
 
+// Four codes of one K-block piece of the GEMM operand: fp16-encoded integers
+// (8 bytes) or int8 (4 bytes).
+template <typename OutT>
+__device__ __forceinline__ void store_codes4(OutT* p, const float (&c)[4]) {
+  if constexpr (std::is_same<OutT, int8_t>::value) {
+    uint32_t u = 0;
+#pragma unroll
+    for (int t = 0; t < 4; t++) u |= (uint32_t)(uint8_t)(int8_t)(int)c[t] << (8 * t);
+    *reinterpret_cast<uint32_t*>(p) = u;
+  } else {
+    half4_t hv;
+#pragma unroll
+    for (int t = 0; t < 4; t++) hv[t] = (_Float16)c[t];
+    *reinterpret_cast<half4_t*>(p) = hv;
+  }
+}
+
 // The next GEMM's operand straight from the residual stream: xn = RMSNorm(h; w)
 // recomputed with the lanes and order k_post_res_norm / k_embed_norm used
 // when they folded max|xn| into amax (so every value, and the scale, is the
 // one the unfused path quantizes), then quantized as k_quantize does
 // (model_int8.go:194-199 / :216-221: RMSNorm, then QuantizeSymmetricINT8 of
 // the normed sequence).  Saves writing xn and reading it back.
-template <int NC>
+template <int NC, typename OutT>
 __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restrict__ h, const float* __restrict__ w,
                                                             float eps, int T, const int32_t* __restrict__ row_seq,
                                                             const float* __restrict__ amax,
-                                                            _Float16* __restrict__ qf, int a_rows,
+                                                            OutT* __restrict__ qf, int a_rows,
                                                             float* __restrict__ row_scale) {
   constexpr int D = NC * 32;
   __shared__ __attribute__((aligned(16))) float tiles[kThreads / SG_WAVE][8 * 40];
@@ -239,13 +282,13 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
   }
   if (j == 0) row_scale[row] = scale;
   // chunk c is K-block c; lane j holds its elements 4j..4j+3
-  _Float16* qr = qf + (int64_t)row * 32 + 4 * j;
+  OutT* qr = qf + (int64_t)row * 32 + 4 * j;
 #pragma unroll
   for (int c = 0; c < NC; c++) {
-    half4_t hv;
+    float cv[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) hv[t] = (_Float16)sg_quant_code(x[c][t], inv);
-    *reinterpret_cast<half4_t*>(qr + (int64_t)c * a_rows * 32) = hv;
+    for (int t = 0; t < 4; t++) cv[t] = sg_quant_code(x[c][t], inv);
+    store_codes4(qr + (int64_t)c * a_rows * 32, cv);
   }
 }
 
@@ -253,11 +296,11 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
 // group per row, lane j handling elements 32c + 4j .. + 3 of every chunk c
 // (chunk c is K-block c), so a wave's stores cover 8 consecutive rows' 64-byte
 // block pieces: 512 contiguous bytes per instruction.
-template <int NC>
+template <int NC, typename OutT>
 __global__ __launch_bounds__(kThreads) void k_quantize_blocked(const float* __restrict__ x, int ldx, int rows,
                                                                const int32_t* __restrict__ row_seq,
                                                                const float* __restrict__ amax,
-                                                               _Float16* __restrict__ qf, int a_rows,
+                                                               OutT* __restrict__ qf, int a_rows,
                                                                float* __restrict__ row_scale) {
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7;
@@ -273,13 +316,13 @@ __global__ __launch_bounds__(kThreads) void k_quantize_blocked(const float* __re
   f32x4_t v[NC];  // every load in flight before the first store
 #pragma unroll
   for (int c = 0; c < NC; c++) v[c] = xr[8 * c];
-  _Float16* qr = qf + (int64_t)row * 32 + 4 * j;
+  OutT* qr = qf + (int64_t)row * 32 + 4 * j;
 #pragma unroll
   for (int c = 0; c < NC; c++) {
-    half4_t hv;
+    float cv[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) hv[t] = (_Float16)sg_quant_code(v[c][t], inv);
-    *reinterpret_cast<half4_t*>(qr + (int64_t)c * a_rows * 32) = hv;
+    for (int t = 0; t < 4; t++) cv[t] = sg_quant_code(v[c][t], inv);
+    store_codes4(qr + (int64_t)c * a_rows * 32, cv);
   }
 }
 
@@ -579,11 +622,11 @@ inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1)
 
 namespace sgk {
 
-hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, float* st, int ld, int row_off,
-                       int grp, int gstride, hipStream_t s) {
+hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, int8_t* w8, float* st, int ld,
+                       int row_off, int grp, int gstride, hipStream_t s) {
   const int64_t n = (int64_t)rows * (cols / 32);
   if (grp <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(n, 256)), dim3(256), 0, s, raw, rows, cols, w16, st, ld,
+  hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(n, 256)), dim3(256), 0, s, raw, rows, cols, w16, w8, st, ld,
                      row_off, grp, gstride);
   return hipGetLastError();
 }
@@ -603,6 +646,15 @@ hipError_t i8_to_f16_blocked(const int8_t* x, int M, int K, _Float16* y, int a_r
     return hipGetLastError();
   }
   hipLaunchKernelGGL(k_i8_to_f16_blocked, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, M, K, y, a_rows);
+  return hipGetLastError();
+}
+
+hipError_t i8_blocked(const int8_t* x, int M, int K, int8_t* y, int a_rows, hipStream_t s) {
+  const int64_t n = (int64_t)M * K;
+  if (n <= 0) return hipSuccess;
+  if (K % 32 || a_rows < M) return hipErrorInvalidValue;
+  const bool vec = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  hipLaunchKernelGGL(k_i8_blocked, dim3(blocks_for(n / 16, 256)), dim3(256), 0, s, x, M, K, y, a_rows, vec);
   return hipGetLastError();
 }
 
@@ -650,11 +702,11 @@ hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* 
   if (f16 && (ldx & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
     switch (cols) {  // the widths the forward quantizes: hidden, attention output, FFN
       case 768:
-        hipLaunchKernelGGL(k_quantize_blocked<24>, dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0, s, x,
+        hipLaunchKernelGGL((k_quantize_blocked<24, _Float16>), dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0, s, x,
                            ldx, rows, row_seq, amax, f16, a_rows, row_scale);
         return hipGetLastError();
       case 1152:
-        hipLaunchKernelGGL(k_quantize_blocked<36>, dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0, s, x,
+        hipLaunchKernelGGL((k_quantize_blocked<36, _Float16>), dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0, s, x,
                            ldx, rows, row_seq, amax, f16, a_rows, row_scale);
         return hipGetLastError();
       default:
@@ -675,9 +727,37 @@ hipError_t norm_quantize(const float* h, const float* w, float eps, int T, int d
   if (T <= 0) return hipSuccess;
   if (a_rows < T) return hipErrorInvalidValue;
   SG_DISPATCH_NPL(d, NPL,
-                  hipLaunchKernelGGL(k_norm_quantize<NPL / 4>, dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads), 0,
-                                     s, h, w, eps, T, row_seq, amax, f16, a_rows, row_scale));
+                  hipLaunchKernelGGL((k_norm_quantize<NPL / 4, _Float16>), dim3(blocks_for(T, kRowsPerBlock)),
+                                     dim3(kThreads), 0, s, h, w, eps, T, row_seq, amax, f16, a_rows, row_scale));
   return hipGetLastError();
+}
+
+hipError_t norm_quantize_i8(const float* h, const float* w, float eps, int T, int d, const int32_t* row_seq,
+                            const float* amax, int8_t* q8, int a_rows, float* row_scale, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  if (a_rows < T) return hipErrorInvalidValue;
+  SG_DISPATCH_NPL(d, NPL,
+                  hipLaunchKernelGGL((k_norm_quantize<NPL / 4, int8_t>), dim3(blocks_for(T, kRowsPerBlock)),
+                                     dim3(kThreads), 0, s, h, w, eps, T, row_seq, amax, q8, a_rows, row_scale));
+  return hipGetLastError();
+}
+
+hipError_t quantize_i8(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
+                       int8_t* q8, int a_rows, float* row_scale, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if ((ldx & 3) || (reinterpret_cast<uintptr_t>(x) & 15) || a_rows < rows) return hipErrorInvalidValue;
+  switch (cols) {  // the widths the forward quantizes: attention output, FFN
+    case 768:
+      hipLaunchKernelGGL((k_quantize_blocked<24, int8_t>), dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0,
+                         s, x, ldx, rows, row_seq, amax, q8, a_rows, row_scale);
+      return hipGetLastError();
+    case 1152:
+      hipLaunchKernelGGL((k_quantize_blocked<36, int8_t>), dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0,
+                         s, x, ldx, rows, row_seq, amax, q8, a_rows, row_scale);
+      return hipGetLastError();
+    default:
+      return hipErrorInvalidValue;
+  }
 }
 
 hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s) {

@@ -31,15 +31,18 @@ inline int gemm_pad_rows(int M) { return (M + kGemmRowPad - 1) / kGemmRowPad * k
 
 // ---- load-time repack (k_rows.hip) ----
 // Raw Q8_0 rows [rows][cols/32][34 B] -> block-major fp16 integer weights
-// w16[b][dst(r)][32] (ld rows per block) and fp32 block scales (IEEE
-// converter) st[b][dst(r)] (ld per block), dst(r) = row_off + (r / grp) * gstride
+// w16[b][dst(r)][32] (ld rows per block), the same values as int8 in w8
+// (optional, same layout) and fp32 block scales (IEEE converter)
+// st[b][dst(r)] (ld per block), dst(r) = row_off + (r / grp) * gstride
 // + r % grp (grp = rows, gstride = 0: plain row_off + r).
-hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, float* st, int ld, int row_off,
-                       int grp, int gstride, hipStream_t s);
+hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, int8_t* w8, float* st, int ld,
+                       int row_off, int grp, int gstride, hipStream_t s);
 // token_embd: int8 values q[v][d] and per-block scales (gguf halving converter) sc[v][d/32].
 hipError_t repack_embd(const uint8_t* raw, int vocab, int d, int8_t* q, float* sc, hipStream_t s);
 // int8 x[M][K] -> block-major fp16 y[K/32][a_rows][32].
 hipError_t i8_to_f16_blocked(const int8_t* x, int M, int K, _Float16* y, int a_rows, hipStream_t s);
+// int8 x[M][K] -> block-major int8 y[K/32][a_rows][32] (gemm_q8_i8's operand).
+hipError_t i8_blocked(const int8_t* x, int M, int K, int8_t* y, int a_rows, hipStream_t s);
 hipError_t fill_f32(float* p, float v, int64_t n, hipStream_t s);
 
 // ---- per-row kernels (k_rows.hip) ----
@@ -58,6 +61,13 @@ hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* 
 // operand f16[d/32][a_rows][32] and row_scale[T] (quantize's arithmetic).
 hipError_t norm_quantize(const float* h, const float* w, float eps, int T, int d, const int32_t* row_seq,
                          const float* amax, _Float16* f16, int a_rows, float* row_scale, hipStream_t s);
+// int8-operand forms (gemm_q8_i8): the same codes stored as int8
+// q8[cols/32][a_rows][32].  quantize_i8 takes the forward's widths (768,
+// 1152) with 16-byte aligned rows.
+hipError_t norm_quantize_i8(const float* h, const float* w, float eps, int T, int d, const int32_t* row_seq,
+                            const float* amax, int8_t* q8, int a_rows, float* row_scale, hipStream_t s);
+hipError_t quantize_i8(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
+                       int8_t* q8, int a_rows, float* row_scale, hipStream_t s);
 hipError_t absmax_rows(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, float* amax,
                        hipStream_t s);
 hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s);
@@ -100,6 +110,14 @@ hipError_t gemm_q8_gelu(const _Float16* A, int a_rows, const _Float16* W, const 
 // Gate/up interleaving used by gemm_q8_gelu: source row r of a matrix goes to
 // row row_off + (r / 32) * 64 + r % 32 (gate: row_off 0, up: row_off 32).
 constexpr int kGeluGroup = 32;
+// int8-operand forms of gemm_q8 / gemm_q8_gelu (same outputs, bit for bit):
+// A int8 [K/32][a_rows][32], W int8 [K/32][N][32].  The forward and the
+// kernel seam take them from kI8MinRows rows.
+constexpr int kI8MinRows = 4096;
+hipError_t gemm_q8_i8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
+                      int M, int N, int K, hipStream_t s);
+hipError_t gemm_q8_gelu_i8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale,
+                           float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s);
 
 // ---- attention (k_attention.hip) ----
 constexpr float kAttnQKScale = 8.0f;  // Q and K are split after scaling by 8 (exact)

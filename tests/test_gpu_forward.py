@@ -253,7 +253,10 @@ def test_config2_full_size_properties(full_gpu):
 
 
 def _batch_invariance(gpu, toks, off, out_dim, y, rows):
-    """Each listed sequence embedded alone is bit-identical to its row of the packed batch."""
+    """Each listed sequence embedded alone is bit-identical to its row of the packed batch.
+    A batch of 4096 tokens or more runs the int8-operand GEMMs and a sequence alone
+    (under 4096 tokens) the fp16-operand ones, so this also pins the two forms to
+    each other."""
     for i in rows:
         a, b = int(off[i]), int(off[i + 1])
         alone = gpu.forward_packed(toks[a:b], np.array([0, b - a], np.int32), out_dim)[0]
