@@ -380,7 +380,7 @@ def main():
                    "weights": "random Q8_0 (int8 U[-127,127], fp16 |N(0,1e-3)|) seed 5; norms U[0.5,1.5] seed 2"},
         "roofline": {"bound": "mfma", "achieved": round(gemm_tops, 2), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(gemm_tops / INT8_PEAK_TOPS, 4), "traffic": traffic,
-                     "kernel": "k_gemm_q8_bl (all Q8_0 GEMM launches; int8 TOP/s)",
+                     "kernel": ("k_gemm_q8_i8" if T >= 4096 else "k_gemm_q8_bl / k_gemm_q8") + " (all Q8_0 GEMM launches; int8 TOP/s)",
                      "avg_launch_ms": round(g["ms"] / max(g["launches"], 1), 4),
                      "algorithmic_bytes_per_launch": round(step_gemm_bytes * a.steps / max(g["launches"], 1)),
                      "hbm_view": {"achieved": round(gemm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
