@@ -157,6 +157,33 @@ def test_gemm_seam_async_across_streams(gpu_ctx, oracle):
         assert np.array_equal(got[::97].view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("M", [300, 4500])
+def test_gemm_unaligned_activations(gpu_ctx, M):
+    """int8 activations at an odd address take the byte-wise relayout (fp16
+    operands below 4096 rows, int8 operands from there): same bits as the
+    aligned call."""
+    import torch
+    from semantica_gpu import kernels, synth
+    N, K = 768, 768
+    rng = np.random.default_rng(M)
+    say(f"gemm unaligned activations M={M}")
+    raw = synth.q8_0_random(rng, N, K)
+    xq = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    rs = rng.uniform(1e-3, 2.0, size=M).astype(np.float32)
+    w = kernels.Q8Weight(gpu_ctx, raw, N, K)
+    buf = torch.zeros(M * K + 1, dtype=torch.int8, device="cuda")
+    buf[1:] = torch.from_numpy(xq.reshape(-1)).cuda()
+    x_odd = buf[1:].view(M, K)
+    assert x_odd.data_ptr() % 16 != 0
+    y0 = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    y1 = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    kernels.matmul_q8_0(gpu_ctx, y0, w, dev(xq), dev(rs))
+    kernels.matmul_q8_0(gpu_ctx, y1, w, x_odd, dev(rs))
+    a, b = host(y0), host(y1)
+    w.close()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 @pytest.mark.parametrize("M", [4500, 8200])
 @pytest.mark.parametrize("N,K", [(1280, 768), (768, 1152), (768, 800)])
 def test_gemm_large_m(gpu_ctx, oracle, M, N, K):
