@@ -86,8 +86,7 @@ constexpr int kVBuf = 2 * kHD * kVStride;  // halves of one V^T tile buffer [hi/
 template <bool QPRE, bool RS>
 __global__ __launch_bounds__(kNT, 2) void k_attn(
     const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
-    const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vth, const _Float16* __restrict__ vtl,
-    int ldvt, float* __restrict__ out, int ldo, const int32_t* __restrict__ seq_off,
+    const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vt, int ldvt, float* __restrict__ out, int ldo, const int32_t* __restrict__ seq_off,
     const int32_t* __restrict__ voff, const sg_item* __restrict__ items, int G, float sscale,
     float* __restrict__ amax, sg_attn_qpre qp) {
   // Two-pass: one K and one V^T buffer.  RS: two K buffers in pass 1, two V^T
@@ -138,12 +137,13 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
       *reinterpret_cast<half8_t*>(kb + ((u >> 1) * kBK + (tid >> 5) + 16 * (u & 1)) * kKStride + 8 * (tid & 31)) =
           stg[u];
   };
-  const int64_t vrow0 = (int64_t)(kvh * kHD + (tid >> 2)) * ldvt + vo + 8 * (tid & 3);
+  // V^T tile at column c of a dim row: halves 2c .. 2c+31 hi, 2c+32 .. 2c+63 lo.
+  const int64_t vrow0 = (int64_t)(kvh * kHD + (tid >> 2)) * ldvt + 2 * vo + 8 * (tid & 3);
   auto load_v = [&](int kt) {
 #pragma unroll
     for (int u = 0; u < 4; u++) {
-      const int64_t o = vrow0 + (int64_t)(128 * (u & 1)) * ldvt + kt;
-      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 1) ? vtl : vth) + o);
+      const int64_t o = vrow0 + (int64_t)(128 * (u & 1)) * ldvt + 2 * kt + 32 * (u >> 1);
+      stg[u] = *reinterpret_cast<const half8_t*>(vt + o);
     }
   };
   auto store_v = [&](_Float16* vb) {
@@ -415,10 +415,9 @@ __global__ __launch_bounds__(sgd::kKvThreads) void k_v_split_t(const float* __re
                                                              const int32_t* __restrict__ seq_off,
                                                              const int32_t* __restrict__ voff,
                                                              const sg_item* __restrict__ vtiles,
-                                                             _Float16* __restrict__ vth, _Float16* __restrict__ vtl,
-                                                             int ldvt) {
+                                                             _Float16* __restrict__ vt, int ldvt) {
   __shared__ __attribute__((aligned(16))) float tv[kBK][sgd::kVtRowStride];
-  sgd::v_split_tile(vtiles[blockIdx.x], blockIdx.y, tv, v, ldv, seq_off, voff, vth, vtl, ldvt);
+  sgd::v_split_tile(vtiles[blockIdx.x], blockIdx.y, tv, v, ldv, seq_off, voff, vt, ldvt);
 }
 
 // K's QK-norm/RoPE split and V's V^T split in one launch: workgroups
@@ -428,8 +427,7 @@ __global__ __launch_bounds__(sgd::kKvThreads) void k_kv_prep(
     const float* __restrict__ k, const float* __restrict__ v, int ldkv, const float* __restrict__ kw, int HKV, int T,
     const int32_t* __restrict__ row_pos, const float* __restrict__ cos_t, const float* __restrict__ sin_t, float eps,
     _Float16* __restrict__ ks_h, _Float16* __restrict__ ks_l, int ldks, int nkb, const int32_t* __restrict__ seq_off,
-    const int32_t* __restrict__ voff, const sg_item* __restrict__ vtiles, int n_vtiles, _Float16* __restrict__ vth,
-    _Float16* __restrict__ vtl, int ldvt) {
+    const int32_t* __restrict__ voff, const sg_item* __restrict__ vtiles, int n_vtiles, _Float16* __restrict__ vt, int ldvt) {
   __shared__ __attribute__((aligned(16))) float tv[kBK][sgd::kVtRowStride];
   const int b = blockIdx.x;
   if (b < nkb) {  // workgroup-uniform
@@ -441,7 +439,7 @@ __global__ __launch_bounds__(sgd::kKvThreads) void k_kv_prep(
                         row_pos, cos_t, sin_t, eps, ks_h, ks_l, ldks, ks_h, ks_l, ldks);
   } else {
     const int vb = b - nkb;
-    sgd::v_split_tile(vtiles[vb % n_vtiles], vb / n_vtiles, tv, v, ldkv, seq_off, voff, vth, vtl, ldvt);
+    sgd::v_split_tile(vtiles[vb % n_vtiles], vb / n_vtiles, tv, v, ldkv, seq_off, voff, vt, ldvt);
   }
 }
 
@@ -469,18 +467,17 @@ __global__ __launch_bounds__(256) void k_split_rows(const float* __restrict__ x,
 namespace sgk {
 
 hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles,
-                     int n_vtiles, int HKV, _Float16* vth, _Float16* vtl, int ldvt, hipStream_t s) {
+                     int n_vtiles, int HKV, _Float16* vt, int ldvt, hipStream_t s) {
   if (n_vtiles <= 0) return hipSuccess;
   if ((ldv & 3) || (ldvt & 7)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_v_split_t, dim3(n_vtiles, HKV), dim3(256), 0, s, v, ldv, seq_off, voff, vtiles, vth, vtl,
+  hipLaunchKernelGGL(k_v_split_t, dim3(n_vtiles, HKV), dim3(256), 0, s, v, ldv, seq_off, voff, vtiles, vt,
                      ldvt);
   return hipGetLastError();
 }
 
 hipError_t kv_prep(const float* k, const float* v, int ldkv, const float* kw, int HKV, int T, const int32_t* row_pos,
                    const float* cos_t, const float* sin_t, float eps, _Float16* ks_h, _Float16* ks_l, int ldks,
-                   const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vth,
-                   _Float16* vtl, int ldvt, hipStream_t s) {
+                   const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vt, int ldvt, hipStream_t s) {
   if (T <= 0 || n_vtiles <= 0 || HKV <= 0) return hipSuccess;
   if ((ldkv & 3) || (ldks & 7) || (ldvt & 7) || (reinterpret_cast<uintptr_t>(k) & 15) ||
       (reinterpret_cast<uintptr_t>(v) & 15) || (kw && (reinterpret_cast<uintptr_t>(kw) & 15)))
@@ -489,7 +486,7 @@ hipError_t kv_prep(const float* k, const float* v, int ldkv, const float* kw, in
   const int64_t nb = nkb + (int64_t)n_vtiles * HKV;
   if (nb > INT32_MAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_kv_prep, dim3((unsigned)nb), dim3(sgd::kKvThreads), 0, s, k, v, ldkv, kw, HKV, T, row_pos, cos_t,
-                     sin_t, eps, ks_h, ks_l, ldks, (int)nkb, seq_off, voff, vtiles, n_vtiles, vth, vtl, ldvt);
+                     sin_t, eps, ks_h, ks_l, ldks, (int)nkb, seq_off, voff, vtiles, n_vtiles, vt, ldvt);
   return hipGetLastError();
 }
 
@@ -504,16 +501,16 @@ hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, 
 namespace {
 template <bool QPRE, bool RS>
 void launch_attn(dim3 grid, hipStream_t s, const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh,
-                 const _Float16* kl, int ldk, const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo,
+                 const _Float16* kl, int ldk, const _Float16* vt, int ldvt, float* out, int ldo,
                  const int32_t* seq_off, const int32_t* voff, const sg_item* items, int G, float sscale, float* amax,
                  const sg_attn_qpre& qp) {
-  hipLaunchKernelGGL((k_attn<QPRE, RS>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vth, vtl, ldvt, out, ldo,
+  hipLaunchKernelGGL((k_attn<QPRE, RS>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
                      seq_off, voff, items, G, sscale, amax, qp);
 }
 }  // namespace
 
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
-                     const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo, const int32_t* seq_off,
+                     const _Float16* vt, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
                      float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre) {
   if (n_items <= 0) return hipSuccess;
@@ -527,11 +524,11 @@ hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Flo
         (reinterpret_cast<uintptr_t>(qpre->q) & 15) || (reinterpret_cast<uintptr_t>(qpre->w) & 15) ||
         (reinterpret_cast<uintptr_t>(qpre->cos_t) & 15) || (reinterpret_cast<uintptr_t>(qpre->sin_t) & 15))
       return hipErrorInvalidValue;  // float4 loads of Q rows, weights and table rows
-    (rs ? launch_attn<true, true> : launch_attn<true, false>)(grid, s, qh, ql, ldq, kh, kl, ldk, vth, vtl, ldvt, out,
+    (rs ? launch_attn<true, true> : launch_attn<true, false>)(grid, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out,
                                                               ldo, seq_off, voff, items, H / HKV, sscale, amax, *qpre);
   } else {
     if (ldq & 7) return hipErrorInvalidValue;
-    (rs ? launch_attn<false, true> : launch_attn<false, false>)(grid, s, qh, ql, ldq, kh, kl, ldk, vth, vtl, ldvt,
+    (rs ? launch_attn<false, true> : launch_attn<false, false>)(grid, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt,
                                                                 out, ldo, seq_off, voff, items, H / HKV, sscale, amax,
                                                                 sg_attn_qpre{});
   }

@@ -405,7 +405,7 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
   _Float16* ks_h = m->ks.as<_Float16>();
   _Float16* ks_l = ks_h + (size_t)T * kvd;
   _Float16* vt_h = m->vt.as<_Float16>();
-  _Float16* vt_l = vt_h + (size_t)kvd * meta.Tp;
+  const int ldvt = 2 * meta.Tp;  // per dim: each 32-key tile's hi then lo halves
   float* sx = m->sx.as<float>();
   float* amax = m->amax.as<float>();
   auto site = [&](int l, int k) { return amax + ((size_t)4 * l + k) * ns; };
@@ -450,10 +450,10 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
     SG_LAUNCH(SG_K_NORM, t * kvd * 16.0,
               sgk::kv_prep(qkv + qd, qkv + qd + kvd, nqkv, ly.k_norm, c.num_kv_heads, T, meta.row_pos, m->cos_t,
                            m->sin_t, eps, ks_h, ks_l, kvd, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles, vt_h,
-                           vt_l, meta.Tp, s));
+                           ldvt, s));
     const sg_attn_qpre qpre{qkv, nqkv, ly.q_norm, m->cos_t, m->sin_t, meta.row_pos, eps};
     SG_LAUNCH(SG_K_ATTENTION, attn_flops,
-              sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, vt_l, meta.Tp, att, qd, meta.seq_off,
+              sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, ldvt, att, qd, meta.seq_off,
                              meta.voff, meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale,
                              site(l, 1), meta.max_len, s, &qpre));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), quant(att, qd, site(l, 1)));
@@ -937,12 +937,11 @@ int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const flo
   _Float16* ks_h = qs_l + T * qd;
   _Float16* ks_l = ks_h + T * kvd;
   _Float16* vt_h = ks_l + T * kvd;
-  _Float16* vt_l = vt_h + kvd * (size_t)meta.Tp;
+  const int ldvt = 2 * meta.Tp;  // per dim: each 32-key tile's hi then lo halves
   SG_HIP(sgk::split_rows(q, ldq, meta.T, (int)qd, sgk::kAttnQKScale, qs_h, qs_l, (int)qd, s));
   SG_HIP(sgk::split_rows(k, ldkv, meta.T, (int)kvd, sgk::kAttnQKScale, ks_h, ks_l, (int)kvd, s));
-  SG_HIP(sgk::v_split_t(v, ldkv, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles, n_kv_heads, vt_h, vt_l,
-                        meta.Tp, s));
-  SG_HIP(sgk::attention(qs_h, qs_l, (int)qd, ks_h, ks_l, (int)kvd, vt_h, vt_l, meta.Tp, out, (int)qd, meta.seq_off,
+  SG_HIP(sgk::v_split_t(v, ldkv, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles, n_kv_heads, vt_h, ldvt, s));
+  SG_HIP(sgk::attention(qs_h, qs_l, (int)qd, ks_h, ks_l, (int)kvd, vt_h, ldvt, out, (int)qd, meta.seq_off,
                         meta.voff, meta.items, meta.n_items, n_heads, n_kv_heads, head_dim, scale, nullptr,
                         meta.max_len, s));
   SG_HIP(hipStreamSynchronize(s));

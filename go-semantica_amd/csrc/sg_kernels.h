@@ -126,16 +126,18 @@ constexpr int kAttnChunks = 8;        // chunks per attention workgroup
 constexpr int kAttnRegKeys = 512;     // longest sequence whose scores pass 1 keeps in registers
 // Columns of V^T a sequence of S keys occupies (whole 32-key tiles).
 inline int attn_key_pad(int S) { return (S + 31) / 32 * 32; }
-// V fp32 [T][ldv] -> V^T hi/lo fp16 [HKV*256][ldvt] (sequence s at column voff[s],
-// keys permuted within 32-key tiles, zero past S); vtiles: (seq, key0) per 32 keys.
+// V fp32 [T][ldv] -> V^T fp16 [HKV*256][ldvt] (sequence s at key column voff[s],
+// keys permuted within 32-key tiles, zero past S; the tile at key column c of
+// a dim row holds its hi halves at 2c .. 2c+31 and its lo halves at 2c+32 ..
+// 2c+63, so ldvt >= 2 * key columns); vtiles: (seq, key0) per 32 keys.
 hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles,
-                     int n_vtiles, int HKV, _Float16* vth, _Float16* vtl, int ldvt, hipStream_t s);
+                     int n_vtiles, int HKV, _Float16* vt, int ldvt, hipStream_t s);
 // qknorm_rope's K-only split (H = 0) and v_split_t in one launch: K and V
 // share the row stride ldkv (columns of the QKV output).
 hipError_t kv_prep(const float* k, const float* v, int ldkv, const float* kw, int HKV, int T, const int32_t* row_pos,
                    const float* cos_t, const float* sin_t, float eps, _Float16* ks_h, _Float16* ks_l, int ldks,
-                   const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vth,
-                   _Float16* vtl, int ldvt, hipStream_t s);
+                   const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vt,
+                   int ldvt, hipStream_t s);
 // rows x cols of x -> hi/lo fp16 of x*scale (row stride ldo).
 hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, _Float16* hi, _Float16* lo, int ldo,
                       hipStream_t s);
@@ -146,7 +148,7 @@ hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, 
 // longest sequence of the launch (at most kAttnRegKeys selects the kernel that
 // keeps pass 1's scores in registers; the output is the same either way).
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
-                     const _Float16* vth, const _Float16* vtl, int ldvt, float* out, int ldo, const int32_t* seq_off,
+                     const _Float16* vt, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
                      float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre = nullptr);
 

@@ -80,17 +80,18 @@ __device__ __forceinline__ void qk_split_group(int64_t g, int j, int r, float* t
 }
 
 // One 32-key tile of V [T][ldv] fp32 (kv head kvh at column 256*kvh) -> V^T
-// hi/lo fp16 [HKV*256][ldvt]: sequence s occupies columns voff[s] ..
+// fp16 [HKV*256][ldvt]: sequence s occupies key columns voff[s] ..
 // voff[s] + 32*ceil(S/32), keys in vt_key order inside every 32-key tile,
-// zeros past S.  The 32 x 256 fp32 tile is loaded with coalesced float4 rows
-// into LDS (tv: [32][kVtRowStride]); a thread then owns one (dim, 8-key
-// chunk), reads its 8 keys down the LDS column and stores the chunk's hi and
-// lo halves as two 16-byte writes (4 threads cover one dim's 64 contiguous
-// bytes).  Every thread of the workgroup must call this (it holds a barrier).
+// zeros past S; the tile at key column c of a dim row is halves 2c .. 2c+31
+// (hi) and 2c+32 .. 2c+63 (lo), so ldvt >= 2 * (key columns).  The 32 x 256
+// fp32 tile is loaded with coalesced float4 rows into LDS (tv:
+// [32][kVtRowStride]); a thread then owns one (dim, 8-key chunk), reads its 8
+// keys down the LDS column and stores the chunk's hi and lo halves as two
+// 16-byte writes (4 threads cover one dim's 128 contiguous bytes).  Every
+// thread of the workgroup must call this (it holds a barrier).
 __device__ __forceinline__ void v_split_tile(sg_item t, int kvh, float (*tv)[kVtRowStride], const float* __restrict__ v,
                                              int ldv, const int32_t* __restrict__ seq_off,
-                                             const int32_t* __restrict__ voff, _Float16* __restrict__ vth,
-                                             _Float16* __restrict__ vtl, int ldvt) {
+                                             const int32_t* __restrict__ voff, _Float16* __restrict__ vt, int ldvt) {
   constexpr int kHD = 256;
   const int r0 = seq_off[t.seq], S = seq_off[t.seq + 1] - r0, k0 = t.c0;
   const int tid = threadIdx.x;
@@ -122,9 +123,9 @@ __device__ __forceinline__ void v_split_tile(sg_item t, int kvh, float (*tv)[kVt
       hw[m] = hb[0] | (hb[1] << 16);
       lw[m] = lb[0] | (lb[1] << 16);
     }
-    const int64_t o = (int64_t)(kvh * kHD + dim) * ldvt + col + 8 * c;
-    *reinterpret_cast<uint4*>(vth + o) = uint4{hw[0], hw[1], hw[2], hw[3]};
-    *reinterpret_cast<uint4*>(vtl + o) = uint4{lw[0], lw[1], lw[2], lw[3]};
+    const int64_t o = (int64_t)(kvh * kHD + dim) * ldvt + 2 * col + 8 * c;
+    *reinterpret_cast<uint4*>(vt + o) = uint4{hw[0], hw[1], hw[2], hw[3]};
+    *reinterpret_cast<uint4*>(vt + o + 32) = uint4{lw[0], lw[1], lw[2], lw[3]};
   }
 }
 
