@@ -185,172 +185,6 @@ __global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8(const _Float16* __r
   }
 }
 
-// LDS-pipelined variant: the workgroup copies each K-block's A tile (BM rows x
-// 64 B, contiguous in the block-major layout) and W tile (BN x 64 B) plus the
-// BN block scales into an LDS buffer with one coalesced 32-byte read per
-// thread per tile; waves read their MFMA fragments from LDS.  Two register
-// stages keep the global reads two blocks ahead of the compute, and each
-// byte is fetched once per workgroup instead of once per wave.
-template <int WM, int WN, int TM, int TN>
-__global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8_lds(const _Float16* __restrict__ A, int a_rows,
-                                                                 const _Float16* __restrict__ W,
-                                                                 const float* __restrict__ St,
-                                                                 const float* __restrict__ row_scale,
-                                                                 float* __restrict__ Y, int M, int N, int K) {
-  constexpr int NT = WM * WN * SG_WAVE;
-  constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
-  constexpr int A_CH = BM * 2, W_CH = BN * 2;     // 32-byte chunks per tile
-  constexpr int A_PT = (A_CH + NT - 1) / NT, W_PT = (W_CH + NT - 1) / NT;
-  __shared__ __attribute__((aligned(16))) _Float16 As[2][BM * 32];
-  __shared__ __attribute__((aligned(16))) _Float16 Ws[2][BN * 32];
-  __shared__ float Ss[2][BN];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-  int bx, by;
-  xcd_tile(bx, by);
-  const int m0 = by * BM, n0 = bx * BN;
-  const int lr = lane & 31, lh = lane >> 5;
-  const int nb = K >> 5;
-  const int64_t a_bstride = (int64_t)a_rows * 32, w_bstride = (int64_t)N * 32;
-
-  struct Reg {
-    half8_t a[A_PT][2], w[W_PT][2];
-    float s;
-  };
-  auto gload = [&](Reg& r, int b) {
-    const _Float16* ab = A + b * a_bstride + (int64_t)m0 * 32;
-#pragma unroll
-    for (int i = 0; i < A_PT; i++) {
-      const int c = tid + i * NT;
-      if (c < A_CH) {
-        r.a[i][0] = *reinterpret_cast<const half8_t*>(ab + c * 16);
-        r.a[i][1] = *reinterpret_cast<const half8_t*>(ab + c * 16 + 8);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < W_PT; i++) {
-      const int c = tid + i * NT;
-      if (c < W_CH) {
-        int row = n0 + (c >> 1);
-        row = row < N ? row : N - 1;
-        const _Float16* wb = W + b * w_bstride + (int64_t)row * 32 + (c & 1) * 16;
-        r.w[i][0] = *reinterpret_cast<const half8_t*>(wb);
-        r.w[i][1] = *reinterpret_cast<const half8_t*>(wb + 8);
-      }
-    }
-    if (tid < BN) {
-      const int col = n0 + tid < N ? n0 + tid : N - 1;
-      r.s = St[(int64_t)b * N + col];
-    }
-  };
-  auto lstore = [&](const Reg& r, int buf) {
-#pragma unroll
-    for (int i = 0; i < A_PT; i++) {
-      const int c = tid + i * NT;
-      if (c < A_CH) {
-        *reinterpret_cast<half8_t*>(&As[buf][c * 16]) = r.a[i][0];
-        *reinterpret_cast<half8_t*>(&As[buf][c * 16 + 8]) = r.a[i][1];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < W_PT; i++) {
-      const int c = tid + i * NT;
-      if (c < W_CH) {
-        *reinterpret_cast<half8_t*>(&Ws[buf][c * 16]) = r.w[i][0];
-        *reinterpret_cast<half8_t*>(&Ws[buf][c * 16 + 8]) = r.w[i][1];
-      }
-    }
-    if (tid < BN) Ss[buf][tid] = r.s;
-  };
-
-  f32x16_t acc[TM][TN];
-#pragma unroll
-  for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-    for (int tn = 0; tn < TN; tn++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[tm][tn][r] = 0.0f;
-
-  auto compute = [&](int buf) {
-    const f32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
-    Frag fa[TM], fw[TN];
-    float d[TN];
-#pragma unroll
-    for (int tm = 0; tm < TM; tm++) {
-      const _Float16* p = &As[buf][(wm * TM * 32 + tm * 32 + lr) * 32 + 16 * lh];
-      fa[tm].lo = *reinterpret_cast<const half8_t*>(p);
-      fa[tm].hi = *reinterpret_cast<const half8_t*>(p + 8);
-    }
-#pragma unroll
-    for (int tn = 0; tn < TN; tn++) {
-      const int cl = wn * TN * 32 + tn * 32 + lr;
-      const _Float16* p = &Ws[buf][cl * 32 + 16 * lh];
-      fw[tn].lo = *reinterpret_cast<const half8_t*>(p);
-      fw[tn].hi = *reinterpret_cast<const half8_t*>(p + 8);
-      d[tn] = Ss[buf][cl];
-    }
-    f32x16_t p[TM][TN];
-#pragma unroll
-    for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-      for (int tn = 0; tn < TN; tn++) {
-        p[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[tm].lo, fw[tn].lo, zero, 0, 0, 0);
-        p[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[tm].hi, fw[tn].hi, p[tm][tn], 0, 0, 0);
-      }
-#pragma unroll
-    for (int tm = 0; tm < TM; tm++)
-#pragma unroll
-      for (int tn = 0; tn < TN; tn++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[tm][tn][r] = __builtin_fmaf(p[tm][tn][r], d[tn], acc[tm][tn][r]);
-  };
-
-  // Pipeline: LDS buffer (b & 1) holds block b; registers r0/r1 hold the
-  // global reads of blocks b+1 and b+2 (alternating).
-  Reg r0, r1;
-  gload(r0, 0);
-  if (nb > 1) gload(r1, 1);
-  lstore(r0, 0);
-  if (nb > 2) gload(r0, 2);
-  __syncthreads();
-  for (int b = 0; b < nb; b += 2) {
-    compute(0);
-    if (b + 1 < nb) {
-      lstore(r1, 1);
-      if (b + 3 < nb) gload(r1, b + 3);
-    }
-    __syncthreads();
-    if (b + 1 >= nb) break;
-    compute(1);
-    if (b + 2 < nb) {
-      lstore(r0, 0);
-      if (b + 4 < nb) gload(r0, b + 4);
-    }
-    __syncthreads();
-  }
-
-#pragma unroll
-  for (int tm = 0; tm < TM; tm++) {
-    const int mb = m0 + wm * TM * 32 + tm * 32;
-    float rs[16];
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
-      rs[r] = row_scale[row < M ? row : M - 1];
-    }
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
-#pragma unroll
-      for (int tn = 0; tn < TN; tn++) {
-        const int col = n0 + wn * TN * 32 + tn * 32 + lr;
-        if (row < M && col < N) Y[(int64_t)row * N + col] = acc[tm][tn][r] * rs[r];
-      }
-    }
-  }
-}
-
 // Split-path variant: a workgroup of NW waves covers NW*TM*32 rows x TN*32
 // columns.  Each wave streams its own A fragments straight from global
 // memory (through the vector L1), while the workgroup's small W tile of each
@@ -857,18 +691,6 @@ hipError_t launch_sp(const _Float16* A, int a_rows, const _Float16* W, const flo
   dim3 grid((N + BN - 1) / BN, gm);
   hipLaunchKernelGGL((k_gemm_q8_sp<NW, TM, TN, GELU>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y, M, N,
                      K, row_seq, amax);
-  return hipGetLastError();
-}
-
-template <int WM, int WN, int TM, int TN>
-hipError_t launch_lds(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* rs, float* Y,
-                      int M, int N, int K, hipStream_t s) {
-  constexpr int BM = WM * TM * 32, BN = WN * TN * 32;
-  const int gm = (M + BM - 1) / BM;
-  if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
-  dim3 grid((N + BN - 1) / BN, gm);
-  hipLaunchKernelGGL((k_gemm_q8_lds<WM, WN, TM, TN>), grid, dim3(WM * WN * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y,
-                     M, N, K);
   return hipGetLastError();
 }
 
