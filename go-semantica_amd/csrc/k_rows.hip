@@ -745,7 +745,8 @@ hipError_t norm_quantize_i8(const float* h, const float* w, float eps, int T, in
 hipError_t quantize_i8(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
                        int8_t* q8, int a_rows, float* row_scale, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  if ((ldx & 3) || (reinterpret_cast<uintptr_t>(x) & 15) || a_rows < rows) return hipErrorInvalidValue;
+  if ((ldx & 3) || (reinterpret_cast<uintptr_t>(x) & 15) || a_rows < rows || !quantize_i8_width(cols))
+    return hipErrorInvalidValue;
   switch (cols) {  // the widths the forward quantizes: attention output, FFN
     case 768:
       hipLaunchKernelGGL((k_quantize_blocked<24, int8_t>), dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0,

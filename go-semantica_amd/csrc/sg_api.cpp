@@ -419,7 +419,7 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
   // From kI8MinRows tokens the GEMM operands are int8 (the quantizers store the
   // same codes as int8, the GEMMs read the int8 weight copies): half the
   // operand bytes, one MFMA per block instead of two, the same output bits.
-  const bool i8 = T >= sgk::kI8MinRows;
+  const bool i8 = T >= sgk::kI8MinRows && sgk::quantize_i8_width(qd) && sgk::quantize_i8_width(ff);
   int8_t* a8 = reinterpret_cast<int8_t*>(a16);
   auto norm_q = [&](const float* w, float* am) {
     return i8 ? sgk::norm_quantize_i8(h, w, eps, T, d, meta.row_seq, am, a8, ar, sx, s)

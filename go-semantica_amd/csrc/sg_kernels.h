@@ -68,6 +68,8 @@ hipError_t norm_quantize_i8(const float* h, const float* w, float eps, int T, in
                             const float* amax, int8_t* q8, int a_rows, float* row_scale, hipStream_t s);
 hipError_t quantize_i8(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
                        int8_t* q8, int a_rows, float* row_scale, hipStream_t s);
+// Row widths quantize_i8 takes (other models keep the fp16-operand route).
+inline bool quantize_i8_width(int cols) { return cols == 768 || cols == 1152; }
 hipError_t absmax_rows(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, float* amax,
                        hipStream_t s);
 hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s);
