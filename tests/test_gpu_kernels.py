@@ -75,15 +75,17 @@ def test_gemm_fp32_config1(gpu_ctx, oracle, N, K):
     assert rel_err(got, avx2) <= 1e-5
 
 
-@pytest.mark.parametrize("M", [1, 33, 2048, 4500, 8200])
-def test_ffn_gate_up_fused_bit_exact(gpu_ctx, oracle, M):
+@pytest.mark.parametrize("M,K", [(1, 768), (33, 768), (2048, 768), (4500, 768), (8200, 768), (4500, 800)])
+def test_ffn_gate_up_fused_bit_exact(gpu_ctx, oracle, M, K):
     """The fused gate/up GEMM with GELUQuick * up in its epilogue equals the
     unfused GEMMs followed by the GELU kernel bit for bit, and the first rows
-    equal the oracle's block-serial GEMMs + geluquick * up."""
+    equal the oracle's block-serial GEMMs + geluquick * up.  From 4096 rows
+    both sides take the int8-operand kernels; K = 800 leaves a partial last
+    round of the ring-unrolled K loop."""
     import torch
     from semantica_gpu import kernels, synth
-    N, K = 1152, 768
-    rng = np.random.default_rng(M)
+    N = 1152
+    rng = np.random.default_rng(M + K)
     say(f"ffn gate/up fused M={M} N={N} K={K}")
     raw_g, raw_u = synth.q8_0_random(rng, N, K), synth.q8_0_random(rng, N, K)
     xq = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
