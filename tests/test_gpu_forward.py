@@ -292,6 +292,24 @@ def test_config4_full_size_properties(full_gpu):
     _batch_invariance(full_gpu, toks, off, 256, y, (0, 1, 100, 255))
 
 
+def test_operand_route_threshold(full_gpu):
+    """4096 packed tokens (the first size on the int8-operand GEMMs) against the
+    same sequences alone (fp16 operands) and 4095 tokens (fp16 operands): equal
+    bits for every shared sequence."""
+    from semantica_gpu import synth
+    lens = [2048, 1, 2047]
+    off = synth.offsets_from_lengths(lens)
+    toks = synth.token_ids(int(off[-1]), 262144, seed=9)
+    say(f"operand route threshold lens={lens} (T={int(off[-1])})")
+    y = full_gpu.forward_packed(toks, off, 768)
+    _batch_invariance(full_gpu, toks, off, 768, y, range(3))
+    off2 = synth.offsets_from_lengths([2048, 2047])
+    toks2 = np.concatenate([toks[:2048], toks[2049:]])
+    y2 = full_gpu.forward_packed(toks2, off2, 768)
+    assert np.array_equal(y2[0].view(np.uint32), y[0].view(np.uint32))
+    assert np.array_equal(y2[1].view(np.uint32), y[2].view(np.uint32))
+
+
 def test_embed_texts_end_to_end(tiny_gpu, tiny_model):
     """pkg/ggufembed over text (api.go:94-209): OpenBytes of one GGUF image
     carrying the weights and a tokenizer vocabulary; EmbedInputs with mixed
