@@ -170,7 +170,9 @@ int sg_profile_read(sg_model *model, sg_profile *out);
  * return after their work on `stream` has completed. */
 
 /* Repacks one raw Q8_0 matrix [out_dim][in_dim/32][34 B] (host pointer) into
- * the device layout used by the GEMM.  in_dim must be a multiple of 32.
+ * the device layouts used by the GEMM (fp16-encoded and int8 copies of the
+ * values, 3 bytes per weight, plus the block scales).  in_dim must be a
+ * multiple of 32.
  * (extractQ8_0Scales model_int8.go:543-569 + the weight bytes it views.) */
 int sg_q8_weight_create(sg_ctx *ctx, const void *q8, int32_t out_dim, int32_t in_dim,
                         sg_q8_weight **out);
