@@ -110,6 +110,34 @@ def test_ffn_gate_up_fused_bit_exact(gpu_ctx, oracle, M, K):
     assert np.array_equal(g_host[:m].view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("M", [6, 4104, 8200])
+def test_gemm_order_pins(gpu_ctx, M):
+    """The hand-derived order vectors of tests/gemm_pins.py: row i and
+    column j hold pin i % 6's activations and pin j's weights, and the
+    diagonal outputs must equal each pin's block-serial value exactly (which
+    the VNNI, AVX2 and arm64 orders each miss on at least one pin).  M = 6
+    runs the register-direct kernel, 4104 and 8200 the two int8-operand
+    tilings."""
+    import torch
+    import gemm_pins
+    from semantica_gpu import kernels, synth
+    pins = gemm_pins.PINS
+    n = len(pins)
+    ops = [p.operands() for p in pins]
+    x = np.concatenate([o[0] for o in ops])
+    raw = synth.q8_0_from_parts(np.concatenate([o[2] for o in ops]), np.concatenate([o[1] for o in ops]))
+    xq = x[np.arange(M) % n]
+    say(f"gemm order pins M={M} N={n} K=64")
+    w = kernels.Q8Weight(gpu_ctx, raw.reshape(n, -1), n, 64)
+    y = torch.empty((M, n), dtype=torch.float32, device="cuda")
+    kernels.matmul_q8_0(gpu_ctx, y, w, dev(xq), dev(np.ones(M, np.float32)))
+    got = host(y)
+    w.close()
+    for r in range(M):
+        p = pins[r % n]
+        assert got[r, r % n] == float(p.expected["block_serial"]), (M, r, p.name, got[r, r % n])
+
+
 def test_gemm_ragged_m_and_extremes(gpu_ctx, oracle):
     """M not a multiple of any tile; blocks at +-127 extremes; per-row scales."""
     import torch

@@ -137,6 +137,62 @@ def test_matmul_orders_vs_float64(oracle):
         assert np.all(np.abs(a - b) <= 1e-3 * np.maximum(1.0, np.maximum(np.abs(a), np.abs(b))))
 
 
+def _pin_eval(oracle, pin, order_name):
+    from semantica_gpu.synth import q8_0_from_parts
+    x, w, d = pin.operands()
+    raw = q8_0_from_parts(d, w)
+    code = {"vnni": oracle.ORDER_VNNI, "avx2": oracle.ORDER_AVX2, "block_serial": oracle.ORDER_BLOCK_SERIAL,
+            "arm64": oracle.ORDER_ARM64}[order_name]
+    return float(oracle.matmul(raw, x, np.float32(1.0), 1, code)[0, 0])
+
+
+@pytest.mark.parametrize("scalar", [False, True])
+def test_matmul_orders_pinned_by_hand_vectors(oracle, scalar):
+    """Each accumulation order reproduces the hand-derived value of every
+    vector in tests/gemm_pins.py (derivations in each vector's docstring),
+    with the AVX2 speed-up paths and with the scalar definitions."""
+    import gemm_pins
+    lib = oracle.load()
+    lib.sgo_force_scalar(1 if scalar else 0)
+    try:
+        for pin in gemm_pins.PINS:
+            for o in gemm_pins.ORDERS:
+                got = _pin_eval(oracle, pin, o)
+                assert got == float(pin.expected[o]), (pin.name, o, got, pin.expected[o])
+    finally:
+        lib.sgo_force_scalar(0)
+
+
+def test_matmul_pins_separate_the_orders():
+    """For every order there is a vector on which its value differs from all
+    three other orders' values, so swapping in another order's lane bytes,
+    rounding or accumulator fails a pin."""
+    import gemm_pins
+    for o in gemm_pins.ORDERS:
+        unique = [p.name for p in gemm_pins.PINS
+                  if all(p.expected[o] != p.expected[q] for q in gemm_pins.ORDERS if q != o)]
+        assert unique, f"no vector tells {o} apart from the other orders"
+
+
+def test_matmul_pins_catch_single_mistakes():
+    """An exact-arithmetic model with the reference's configuration of each
+    order reproduces the hand values; changing any one knob (lane bytes,
+    hsum tree, fused vs. mul+add) changes at least one pinned value."""
+    import gemm_pins
+    from gemm_pins import CONFIG, PINS, model
+    for o, cfg in CONFIG.items():
+        for pin in PINS:
+            assert model(pin, *cfg) == pin.expected[o], (o, pin.name)
+        lane, tree, fused = cfg
+        mutants = [(lm, tree, fused) for lm in gemm_pins.LANE_MAPS if lm != lane]
+        mutants.append((lane, tree, not fused))
+        if lane != "single":
+            mutants += [(lane, t, fused) for t in ("pairs", "seq")]
+        for mcfg in mutants:
+            caught = [p.name for p in PINS if model(p, *mcfg) != p.expected[o]]
+            assert caught, f"{o}: mutation {mcfg} passes every pin"
+
+
 def test_matmul_simd_equals_scalar(oracle):
     """The AVX2 speed-up paths must give the scalar definition's bits."""
     lib = oracle.load()
@@ -145,7 +201,7 @@ def test_matmul_simd_equals_scalar(oracle):
     rng = np.random.default_rng(5)
     raw, _, _ = _rand_q8(rng, 96, 768, 1e-4, 1e-3)
     x = rng.integers(-127, 128, size=(9, 768), dtype=np.int8)
-    for order in (0, 1):
+    for order in (0, 1, 2, 3):
         fast = oracle.matmul(raw, x, np.float32(0.013), 96, order)
         lib.sgo_force_scalar(1)
         try:
@@ -415,3 +471,36 @@ def test_forward_batch_equals_singles(oracle, tiny_model):
     for i in range(len(lens)):
         rc, ys = m.forward(toks[off[i]:off[i + 1]], 256)
         assert np.array_equal(ys, yb[i])
+
+
+def test_forward_taps_teacher_forcing(oracle, tiny_model):
+    """The tapped forward equals the plain one; forcing each layer's attention
+    output with the oracle's own values changes nothing, bit for bit; forcing
+    one perturbed value changes that layer's residual stream and all later
+    ones (so the injected values are really the ones used)."""
+    from semantica_gpu import synth
+    m = oracle.OracleModel(tiny_model)
+    lens = [5, 17, 1, 33]
+    off = synth.offsets_from_lengths(lens)
+    toks = synth.token_ids(int(off[-1]), tiny_model.config["vocab_size"], seed=3)
+    L = tiny_model.config["num_layers"]
+    for order in (oracle.ORDER_BLOCK_SERIAL, oracle.ORDER_VNNI):
+        rc, plain = m.forward_batch(toks, off, 768, order=order, n_threads=2)
+        assert rc == 0
+        rc, out, taps = m.forward_taps(toks, off, 768, L, qkv=True, att=True, h=True, order=order, n_threads=2)
+        assert rc == 0 and np.array_equal(out.view(np.uint32), plain.view(np.uint32))
+        for i in range(len(lens)):  # h after the last layer is the stop_layer tap
+            rc, hs = m.forward(toks[off[i]:off[i + 1]], 768, order=order, stop_layer=L)
+            assert np.array_equal(hs.view(np.uint32), taps["h"][L - 1, off[i]:off[i + 1]].view(np.uint32))
+        rc, out2, taps2 = m.forward_taps(toks, off, 768, L, att_in=taps["att"], qkv=True, att=True, h=True,
+                                         order=order, n_threads=2)
+        assert rc == 0 and np.array_equal(out2.view(np.uint32), out.view(np.uint32))
+        for k in ("qkv", "att", "h"):
+            assert np.array_equal(taps2[k].view(np.uint32), taps[k].view(np.uint32)), k
+    bad = taps["att"].copy()
+    bad[0, 20, 100] = np.nextafter(bad[0, 20, 100], np.float32(np.inf)) * np.float32(1.5)
+    rc, out3, taps3 = m.forward_taps(toks, off, 768, L, att_in=bad, h=True, order=oracle.ORDER_VNNI, n_threads=2)
+    seq = int(np.searchsorted(off, 20, side="right")) - 1
+    a, b = off[seq], off[seq + 1]
+    assert not np.array_equal(taps3["h"][0, a:b], taps["h"][0, a:b])
+    assert not np.array_equal(out3[seq], out[seq])
