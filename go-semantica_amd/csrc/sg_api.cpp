@@ -388,9 +388,15 @@ int validate_config(const sg_model_config& c) {
 // Work figures are the algorithmic ones: 2*M*N*K int8 ops per GEMM,
 // 4*H*hd*S^2 flops per sequence for attention, and bytes read + written at
 // the reference's dtypes (fp32 activations, int8 quantized) elsewhere.
-// stop >= 0: return after `stop` layers with the residual stream copied to d_out.
+// Per-layer copies for sg_forward_trace: layer l's rows at l * T rows.
+struct Trace {
+  float *qkv = nullptr, *att = nullptr, *h = nullptr;
+};
+
+// stop >= 0: return after `stop` layers with the residual stream copied to
+// d_out (when non-null).  tr: per-layer copies of the first `stop` layers.
 int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_dim, float* d_out, hipStream_t s,
-                int stop = -1) {
+                int stop = -1, const Trace* tr = nullptr) {
   const sg_model_config& c = m->cfg;
   const int T = meta.T, ns = meta.n_seq, d = c.embed_dim, ff = c.interm_dim, L = c.num_layers;
   const int qd = m->qd, kvd = m->kvd, nqkv = m->nqkv;
@@ -429,6 +435,10 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
     return i8 ? sgk::quantize_i8(x, cols, T, cols, meta.row_seq, am, a8, ar, sx, s)
               : sgk::quantize(x, cols, T, cols, meta.row_seq, am, a16, ar, nullptr, sx, s);
   };
+  auto tap = [&](float* dst, const float* src, int l, int cols) {
+    return hipMemcpyAsync(dst + (size_t)l * T * cols, src, sizeof(float) * (size_t)T * cols, hipMemcpyDeviceToDevice,
+                          s);
+  };
   auto gemm = [&](const _Float16* w16, const int8_t* w8, const float* st, float* y, int N, int K) {
     return i8 ? sgk::gemm_q8_i8(a8, ar, w8, st, sx, y, T, N, K, s)
               : sgk::gemm_q8(a16, ar, w16, st, sx, y, nullptr, T, N, K, s);
@@ -445,6 +455,7 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
     // The pre-norm's output xn is never stored: recomputed from h while quantizing.
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.attn_norm, site(l, 0)));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), gemm(ly.wqkv, ly.wqkv8, ly.sqkv, qkv, nqkv, d));
+    if (tr && tr->qkv) SG_HIP(tap(tr->qkv, qkv, l, nqkv));
     // K's QK-norm + RoPE + split and V's V^T split in one launch; Q's norm and
     // RoPE run inside the attention kernel.
     SG_LAUNCH(SG_K_NORM, t * kvd * 16.0,
@@ -456,6 +467,7 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
               sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, ldvt, att, qd, meta.seq_off,
                              meta.voff, meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale,
                              site(l, 1), meta.max_len, s, &qpre));
+    if (tr && tr->att) SG_HIP(tap(tr->att, att, l, qd));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), quant(att, qd, site(l, 1)));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), gemm(ly.wo, ly.wo8, ly.so, o, d, qd));
     SG_LAUNCH(SG_K_NORM, t * d * 12.0,
@@ -470,9 +482,10 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
     SG_LAUNCH(SG_K_NORM, t * d * (last ? 16.0 : 12.0),
               sgk::post_res_norm(o, h, ly.post_ffw, last ? m->out_norm : m->layers[l + 1].attn_norm, eps, T, d,
                                  last ? xn : nullptr, meta.row_seq, last ? nullptr : site(l + 1, 0), s));
+    if (tr && tr->h) SG_HIP(tap(tr->h, h, l, d));
   }
   if (stop >= 0) {
-    SG_HIP(hipMemcpyAsync(d_out, h, sizeof(float) * (size_t)T * d, hipMemcpyDeviceToDevice, s));
+    if (d_out) SG_HIP(hipMemcpyAsync(d_out, h, sizeof(float) * (size_t)T * d, hipMemcpyDeviceToDevice, s));
     return SG_OK;
   }
   SG_LAUNCH(SG_K_POOL, 4.0 * out_dim * (t + ns), sgk::pool_l2(d_out, xn, d, out_dim, meta.seq_off, ns, s));
@@ -517,14 +530,14 @@ int ensure_workspace(sg_model* m, int T, int n_seq, int Tp) {
 }
 
 int forward_device_locked(sg_model* m, const int32_t* d_tokens, const int32_t* off, int n_seq, int out_dim,
-                          float* d_out, hipStream_t s, int stop = -1) {
+                          float* d_out, hipStream_t s, int stop = -1, const Trace* tr = nullptr) {
   SG_TRY(check_forward_args(m, off, n_seq, out_dim));
   SG_TRY(set_device(m->ctx));
   const int T = off[n_seq];
   Meta meta;
   SG_TRY(stage_meta(off, n_seq, m->cfg.num_heads / m->cfg.num_kv_heads, m->meta_h, m->meta_d, s, meta));
   SG_TRY(ensure_workspace(m, T, n_seq, meta.Tp));
-  SG_TRY(run_forward(m, d_tokens, meta, out_dim, d_out, s, stop));
+  SG_TRY(run_forward(m, d_tokens, meta, out_dim, d_out, s, stop, tr));
   SG_TRY(m->io_h.ensure(64));
   SG_HIP(hipMemcpyAsync(m->io_h.p, m->err.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
   SG_HIP(hipStreamSynchronize(s));
@@ -682,6 +695,20 @@ int sg_forward_hidden(sg_model* m, const int32_t* d_tokens, const int32_t* seq_o
   std::lock_guard<std::mutex> lk(m->mu);
   return forward_device_locked(m, d_tokens, seq_offsets, n_seq, m->cfg.embed_dim, d_hidden, pick(m->ctx, stream),
                                n_layers);
+}
+
+int sg_forward_trace(sg_model* m, const int32_t* d_tokens, const int32_t* seq_offsets, int32_t n_seq,
+                     int32_t n_layers, float* d_qkv, float* d_att, float* d_h, void* stream) {
+  if (!m || !d_tokens) return fail(SG_ERR_INVALID, "NULL argument");
+  if (n_layers < 1 || n_layers > m->cfg.num_layers)
+    return fail(SG_ERR_INVALID, "n_layers %d out of range (1..%d)", n_layers, m->cfg.num_layers);
+  std::lock_guard<std::mutex> lk(m->mu);
+  Trace tr;
+  tr.qkv = d_qkv;
+  tr.att = d_att;
+  tr.h = d_h;
+  return forward_device_locked(m, d_tokens, seq_offsets, n_seq, m->cfg.embed_dim, nullptr, pick(m->ctx, stream),
+                               n_layers, &tr);
 }
 
 int sg_forward(sg_model* m, const int32_t* tokens, const int32_t* off, int32_t n_seq, int32_t out_dim, float* out) {

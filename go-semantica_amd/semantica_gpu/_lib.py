@@ -105,6 +105,7 @@ _PROTOS = {
     "sg_forward": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp]),
     "sg_forward_device": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
     "sg_forward_hidden": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _vp]),
+    "sg_forward_trace": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _vp, _vp, _vp]),
     "sg_profile_enable": (ctypes.c_int, [_vp, ctypes.c_int]),
     "sg_profile_read": (ctypes.c_int, [_vp, ctypes.POINTER(Profile)]),
     "sg_q8_weight_create": (ctypes.c_int, [_vp, _vp, _i32, _i32, _pp]),

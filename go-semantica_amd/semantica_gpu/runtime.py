@@ -193,6 +193,16 @@ class Model:
                                               len(offsets) - 1, n_layers, ctypes.c_void_p(d_hidden_ptr),
                                               ctypes.c_void_p(stream) if stream else None))
 
+    def forward_trace(self, d_tokens_ptr: int, offsets: np.ndarray, n_layers: int, d_qkv_ptr: int = 0,
+                      d_att_ptr: int = 0, d_h_ptr: int = 0, stream: int = 0):
+        """sg_forward_trace: per-layer Q|K|V, attention output and residual stream
+        into [n_layers, T, cols] device buffers (0 skips one)."""
+        offsets = np.ascontiguousarray(offsets, np.int32)
+        vp = lambda x: ctypes.c_void_p(x) if x else None  # noqa: E731
+        _lib.check(self.lib.sg_forward_trace(self.handle, ctypes.c_void_p(d_tokens_ptr), _ptr(offsets),
+                                             len(offsets) - 1, n_layers, vp(d_qkv_ptr), vp(d_att_ptr), vp(d_h_ptr),
+                                             vp(stream)))
+
     def profile_enable(self, on: bool = True):
         _lib.check(self.lib.sg_profile_enable(self.handle, 1 if on else 0))
 

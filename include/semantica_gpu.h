@@ -134,6 +134,20 @@ int sg_forward_device(sg_model *model, const int32_t *d_tokens, const int32_t *s
 int sg_forward_hidden(sg_model *model, const int32_t *d_tokens, const int32_t *seq_offsets,
                       int32_t n_seq, int32_t n_layers, float *d_hidden, void *stream);
 
+/* Per-layer trace of the batched forward, for parity checks: runs the first
+ * n_layers layers (1..num_layers) as sg_forward_hidden does and writes, for
+ * each layer l, rows l*T .. l*T + T - 1 (T = seq_offsets[n_seq]) of
+ *   d_qkv [n_layers][T][q_dim + 2*kv_dim]: the Q|K|V GEMM output, before
+ *         QK-norm and RoPE (runAttentionINT8, model_int8.go:357-372),
+ *   d_att [n_layers][T][q_dim]: the attention output before it is quantized
+ *         (model_int8.go:481-507),
+ *   d_h   [n_layers][T][embed_dim]: the residual stream after the layer
+ *         (model_int8.go:232).
+ * Any of the three may be NULL.  No counterpart in the reference, which keeps
+ * these values internal to forwardINT8WithDim (model_int8.go:148-256). */
+int sg_forward_trace(sg_model *model, const int32_t *d_tokens, const int32_t *seq_offsets, int32_t n_seq,
+                     int32_t n_layers, float *d_qkv, float *d_att, float *d_h, void *stream);
+
 /* ---- measurement hook ---------------------------------------------------
  * No counterpart in the reference (its benchmark only times whole Embed
  * calls, cmd/benchmark/main.go:553-715).  While enabled, sg_forward*

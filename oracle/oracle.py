@@ -28,6 +28,11 @@ class Config(ctypes.Structure):
                 ("rope_base", ctypes.c_float)]
 
 
+class Taps(ctypes.Structure):
+    _fields_ = [("att_in", ctypes.c_void_p), ("qkv", ctypes.c_void_p), ("att", ctypes.c_void_p),
+                ("h", ctypes.c_void_p), ("n_layers", ctypes.c_int32), ("layer_rows", ctypes.c_int64)]
+
+
 class Layer(ctypes.Structure):
     _fields_ = [(n, ctypes.c_void_p) for n in (
         "attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down",
@@ -68,6 +73,8 @@ def load():
         "sgo_model_free": (None, [vp]),
         "sgo_forward": (ctypes.c_int, [vp, vp, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int]),
         "sgo_forward_batch": (ctypes.c_int, [vp, vp, vp, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int]),
+        "sgo_forward_taps": (ctypes.c_int, [vp, vp, vp, ctypes.c_int, ctypes.c_int, vp, ctypes.c_int, ctypes.c_int,
+                                            ctypes.POINTER(Taps)]),
         "sgo_simd_level": (ctypes.c_int, []),
         "sgo_force_scalar": (None, [ctypes.c_int]),
         "sgo_bf_normalize": (None, [vp, ctypes.c_int]),
@@ -271,6 +278,7 @@ class OracleModel:
     def __init__(self, model):
         c = model.config
         self.config = c
+        self.model = model
         hd = c["embed_dim"] // c["num_heads"]
         self._keep = []
 
@@ -319,3 +327,31 @@ class OracleModel:
         rc = load().sgo_forward_batch(self.handle, _p(tokens), _p(offsets), n, target_dim, _p(out), order,
                                       n_threads)
         return rc, out
+
+    def forward_taps(self, tokens, offsets, target_dim: int, n_layers: int, att_in=None, qkv=False, att=False,
+                     h=True, order: int = ORDER_BLOCK_SERIAL, n_threads: int = 8):
+        """Batched forward with per-layer taps over the packed rows (see
+        sgo_taps): returns (rc, out [n_seq, target_dim], dict of the requested
+        arrays, each [n_layers, T, cols]).  att_in [n_layers, T, q_dim]
+        replaces each layer's attention output (teacher forcing)."""
+        c = self.config
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        offsets = np.ascontiguousarray(offsets, np.int32)
+        n, T = offsets.size - 1, int(offsets[-1])
+        hd = c["embed_dim"] // c["num_heads"]
+        qd, kvd = c["num_heads"] * hd, c["num_kv_heads"] * hd
+        taps = Taps(None, None, None, None, n_layers, T)
+        arrays = {}
+        if att_in is not None:
+            att_in = np.ascontiguousarray(att_in, np.float32)
+            if att_in.shape != (n_layers, T, qd):
+                raise ValueError(f"att_in must be [{n_layers}, {T}, {qd}]")
+            taps.att_in = att_in.ctypes.data
+        for name, want, cols in (("qkv", qkv, qd + 2 * kvd), ("att", att, qd), ("h", h, c["embed_dim"])):
+            if want:
+                arrays[name] = np.zeros((n_layers, T, cols), np.float32)
+                setattr(taps, name, arrays[name].ctypes.data)
+        out = np.empty((n, target_dim), np.float32)
+        rc = load().sgo_forward_taps(self.handle, _p(tokens), _p(offsets), n, target_dim, _p(out), order, n_threads,
+                                     ctypes.byref(taps))
+        return rc, out, arrays

@@ -203,6 +203,34 @@ static float q8_dot_avx2(const int8_t *xr, const uint8_t *wr, const float *sc, i
   _mm256_storeu_ps(l, acc);
   return hsum8(l);
 }
+
+/* One accumulator over whole-block sums (block-serial fma, or arm64's
+ * mul + add): the int32 block sum is exact whatever order its products are
+ * added in, so it is formed with VPMADDWD and an integer reduction. */
+__attribute__((target("avx2,fma")))
+static float q8_dot_serial_avx2(const int8_t *xr, const uint8_t *wr, const float *sc, int nb, int fused) {
+  float acc = 0.0f;
+  for (int b = 0; b < nb; b++) {
+    const __m128i *wp = (const __m128i *)(wr + (int64_t)b * 34 + 2);
+    const __m128i *xp = (const __m128i *)(xr + (int64_t)b * 32);
+    __m256i plo = _mm256_madd_epi16(_mm256_cvtepi8_epi16(_mm_loadu_si128(xp)),
+                                    _mm256_cvtepi8_epi16(_mm_loadu_si128(wp)));
+    __m256i phi = _mm256_madd_epi16(_mm256_cvtepi8_epi16(_mm_loadu_si128(xp + 1)),
+                                    _mm256_cvtepi8_epi16(_mm_loadu_si128(wp + 1)));
+    __m256i s8 = _mm256_add_epi32(plo, phi);
+    __m128i t = _mm_add_epi32(_mm256_castsi256_si128(s8), _mm256_extracti128_si256(s8, 1));
+    t = _mm_add_epi32(t, _mm_shuffle_epi32(t, 0x4E));
+    t = _mm_add_epi32(t, _mm_shuffle_epi32(t, 0xB1));
+    int32_t p = _mm_cvtsi128_si32(t);
+    if (fused) {
+      acc = fmaf((float)p, sc[b], acc);
+    } else {
+      float prod = (float)p * sc[b];
+      acc = acc + prod;
+    }
+  }
+  return acc;
+}
 #endif
 
 /* matMulQ8_0INT8SerialRange, quantize.go:390-458 (whole blocks only):
@@ -212,7 +240,8 @@ void sgo_matmul_q8_0_int8(float *dst, const uint8_t *w, const float *scales,
                           int batch, int in_dim, int out_dim, int order) {
   int nb = in_dim / 32;
   int64_t row_bytes = (int64_t)nb * 34;
-  int simd = sgo_simd_level() && (order == SGO_ORDER_VNNI || order == SGO_ORDER_AVX2);
+  int simd = sgo_simd_level();
+  int serial = order == SGO_ORDER_BLOCK_SERIAL || order == SGO_ORDER_ARM64;
   const int JT = 64; /* column tile: keeps a weight tile hot while rows stream */
   for (int j0 = 0; j0 < out_dim; j0 += JT) {
     int j1 = j0 + JT < out_dim ? j0 + JT : out_dim;
@@ -224,6 +253,7 @@ void sgo_matmul_q8_0_int8(float *dst, const uint8_t *w, const float *scales,
         const float *sc = scales + (int64_t)j * nb;
         float v;
 #if SGO_X86
+        if (simd && serial) v = q8_dot_serial_avx2(xr, wr, sc, nb, order == SGO_ORDER_BLOCK_SERIAL); else
         if (simd) v = q8_dot_avx2(xr, wr, sc, nb, order); else
 #endif
         v = q8_dot_scalar(xr, wr, sc, nb, order);
@@ -560,12 +590,13 @@ static void gemm_seq(float *dst, const q8w *t, const int8_t *x, float xs, int S,
 }
 
 /* forwardINT8WithDim, runtime/model_int8.go:148-256; runAttentionINT8 :349-507;
- * runMLPINT8 :510-538 */
-int sgo_forward(const sgo_model *m, const int32_t *tokens, int S, int target_dim,
-                float *out, int order, int stop_layer) {
+ * runMLPINT8 :510-538.  `tp` (may be NULL) adds the taps of sgo_forward_taps:
+ * row r of layer l of a tap array sits at row l * tp->layer_rows + r. */
+static int forward_core(const sgo_model *m, const int32_t *tokens, int S, int target_dim,
+                        float *out, int order, int stop_layer, const sgo_taps *tp) {
   const sgo_config *c = &m->cfg;
   int d = c->embed_dim, H = c->num_heads, HKV = c->num_kv_heads, hd = c->head_dim;
-  int qd = H * hd, kvd = HKV * hd, ff = c->interm_dim;
+  int qd = H * hd, kvd = HKV * hd, ff = c->interm_dim, nqkv = qd + 2 * kvd;
   if (target_dim <= 0 || target_dim > d) return -4; /* ForwardWithDim model.go:661-667 */
   if (S == 0) return -1;
   if (S > c->max_seq_len) return -2;
@@ -596,6 +627,8 @@ int sgo_forward(const sgo_model *m, const int32_t *tokens, int S, int target_dim
   for (int l = 0; l < L; l++) {
     const sgo_layer *ly = &m->layers[l];
     const q8w *t = m->lw + l * 7;
+    int tap = tp && l < tp->n_layers;
+    int64_t lrow = tap ? (int64_t)l * tp->layer_rows : 0;
     memcpy(resid, hidden, sizeof(float) * Sd);
     norm_rows(hidden, ly->attn_norm, S, d, eps);
     float xs = sgo_quantize_symmetric(hidden, (int64_t)Sd, xq);
@@ -603,6 +636,13 @@ int sgo_forward(const sgo_model *m, const int32_t *tokens, int S, int target_dim
     gemm_seq(q, &t[0], xq, xs, S, rs, order);
     gemm_seq(k, &t[1], xq, xs, S, rs, order);
     gemm_seq(v, &t[2], xq, xs, S, rs, order);
+    if (tap && tp->qkv)
+      for (int s = 0; s < S; s++) {
+        float *dst = tp->qkv + (lrow + s) * nqkv;
+        memcpy(dst, q + (int64_t)s * qd, sizeof(float) * qd);
+        memcpy(dst + qd, k + (int64_t)s * kvd, sizeof(float) * kvd);
+        memcpy(dst + qd + kvd, v + (int64_t)s * kvd, sizeof(float) * kvd);
+      }
     if (ly->attn_q_norm)
       for (int s = 0; s < S; s++)
         for (int h = 0; h < H; h++) {
@@ -618,7 +658,12 @@ int sgo_forward(const sgo_model *m, const int32_t *tokens, int S, int target_dim
     sgo_rope_apply(q, S, H, hd, m->cos_tab, m->sin_tab);
     sgo_rope_apply(k, S, HKV, hd, m->cos_tab, m->sin_tab);
     float ascale = 1.0f / (float)sqrt((double)hd); /* model.go:475 */
-    sgo_attention(att, q, k, v, S, H, HKV, hd, ascale);
+    if (!(tap && tp->att_in) || tp->att) {
+      sgo_attention(att, q, k, v, S, H, HKV, hd, ascale);
+      if (tap && tp->att) memcpy(tp->att + lrow * qd, att, sizeof(float) * (size_t)S * qd);
+    }
+    /* teacher forcing: the rest of the layer runs on the injected attention output */
+    if (tap && tp->att_in) memcpy(att, tp->att_in + lrow * qd, sizeof(float) * (size_t)S * qd);
     float as = sgo_quantize_symmetric(att, (int64_t)S * qd, xq);
     gemm_seq(hidden, &t[3], xq, as, S, rs, order);
     norm_rows(hidden, ly->post_attention_norm, S, d, eps);
@@ -635,6 +680,7 @@ int sgo_forward(const sgo_model *m, const int32_t *tokens, int S, int target_dim
     gemm_seq(hidden, &t[6], xq, gs, S, rs, order);
     norm_rows(hidden, ly->post_ffw_norm, S, d, eps);
     for (size_t i = 0; i < Sd; i++) hidden[i] = hidden[i] + resid[i];
+    if (tap && tp->h) memcpy(tp->h + lrow * d, hidden, sizeof(float) * Sd);
   }
 
   if (L < c->num_layers || stop_layer == c->num_layers) {
@@ -649,27 +695,45 @@ int sgo_forward(const sgo_model *m, const int32_t *tokens, int S, int target_dim
   return 0;
 }
 
+int sgo_forward(const sgo_model *m, const int32_t *tokens, int S, int target_dim,
+                float *out, int order, int stop_layer) {
+  return forward_core(m, tokens, S, target_dim, out, order, stop_layer, NULL);
+}
+
 typedef struct {
   const sgo_model *m;
   const int32_t *tokens, *off;
   int begin, end, dim, order;
   float *out;
+  const sgo_taps *taps; /* packed over the batch; NULL: none */
   int err;
 } fwd_job;
 
 static void *fwd_worker(void *p) {
   fwd_job *j = (fwd_job *)p;
+  const sgo_config *c = &j->m->cfg;
+  int qd = c->num_heads * c->head_dim, nqkv = qd + 2 * c->num_kv_heads * c->head_dim;
   for (int s = j->begin; s < j->end; s++) {
-    int r = sgo_forward(j->m, j->tokens + j->off[s], j->off[s + 1] - j->off[s], j->dim,
-                        j->out + (int64_t)s * j->dim, j->order, -1);
+    sgo_taps t, *tp = NULL;
+    if (j->taps) { /* this sequence's rows of every packed tap array */
+      int64_t r0 = j->off[s];
+      t = *j->taps;
+      if (t.att_in) t.att_in += r0 * qd;
+      if (t.qkv) t.qkv += r0 * nqkv;
+      if (t.att) t.att += r0 * qd;
+      if (t.h) t.h += r0 * c->embed_dim;
+      tp = &t;
+    }
+    int r = forward_core(j->m, j->tokens + j->off[s], j->off[s + 1] - j->off[s], j->dim,
+                         j->out + (int64_t)s * j->dim, j->order, -1, tp);
     if (r && !j->err) j->err = r;
   }
   return NULL;
 }
 
 /* embedPrompts api.go:237-295: workers = min(n_threads, n), contiguous ranges */
-int sgo_forward_batch(const sgo_model *m, const int32_t *tokens, const int32_t *off,
-                      int n, int dim, float *out, int order, int n_threads) {
+static int forward_batch(const sgo_model *m, const int32_t *tokens, const int32_t *off,
+                         int n, int dim, float *out, int order, int n_threads, const sgo_taps *taps) {
   if (n <= 0) return 0;
   int workers = n_threads < n ? n_threads : n;
   if (workers < 1) workers = 1;
@@ -680,7 +744,7 @@ int sgo_forward_batch(const sgo_model *m, const int32_t *tokens, const int32_t *
   for (int w = 0; w < workers; w++) {
     int b = w * per, e = b + per < n ? b + per : n;
     if (b >= n) break;
-    jobs[w] = (fwd_job){m, tokens, off, b, e, dim, order, out, 0};
+    jobs[w] = (fwd_job){m, tokens, off, b, e, dim, order, out, taps, 0};
     pthread_create(&th[w], NULL, fwd_worker, &jobs[w]);
     used++;
   }
@@ -691,4 +755,14 @@ int sgo_forward_batch(const sgo_model *m, const int32_t *tokens, const int32_t *
   }
   free(jobs); free(th);
   return err;
+}
+
+int sgo_forward_batch(const sgo_model *m, const int32_t *tokens, const int32_t *off,
+                      int n, int dim, float *out, int order, int n_threads) {
+  return forward_batch(m, tokens, off, n, dim, out, order, n_threads, NULL);
+}
+
+int sgo_forward_taps(const sgo_model *m, const int32_t *tokens, const int32_t *off,
+                     int n, int dim, float *out, int order, int n_threads, const sgo_taps *taps) {
+  return forward_batch(m, tokens, off, n, dim, out, order, n_threads, taps);
 }

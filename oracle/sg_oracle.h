@@ -121,6 +121,24 @@ int sgo_forward(const sgo_model *m, const int32_t *tokens, int seq_len, int targ
 int sgo_forward_batch(const sgo_model *m, const int32_t *tokens, const int32_t *seq_offsets,
                       int n_seq, int target_dim, float *out, int order, int n_threads);
 
+/* Per-layer taps of the batched forward (a checker's view; the reference keeps
+ * these internal).  Arrays are packed over the batch like the GPU library's
+ * trace: row r (0..T-1, sequences concatenated) of layer l at row
+ * l * layer_rows + r, with layer_rows = T.  Only layers < n_layers are tapped.
+ *   att_in: replaces each layer's attention output before it is quantized
+ *           (teacher forcing: model_int8.go:349-507 continues on these values)
+ *   qkv:    Q|K|V GEMM outputs per row, before QK-norm and RoPE
+ *   att:    the oracle's own attention output (computed even when forced)
+ *   h:      the residual stream after the layer (model_int8.go:232) */
+typedef struct sgo_taps {
+  const float *att_in;
+  float *qkv, *att, *h;
+  int32_t n_layers;
+  int64_t layer_rows;
+} sgo_taps;
+int sgo_forward_taps(const sgo_model *m, const int32_t *tokens, const int32_t *seq_offsets,
+                     int n_seq, int target_dim, float *out, int order, int n_threads, const sgo_taps *taps);
+
 /* 1 when the AVX2+FMA fast paths are in use on this host (results are
  * bit-identical to the scalar definitions either way). */
 int sgo_simd_level(void);

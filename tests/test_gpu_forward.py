@@ -1,6 +1,12 @@
 """End-to-end parity of the batched GPU forward with the oracle's restatement
 of forwardINT8WithDim (runtime/model_int8.go:148-256).
 
+Parity is proven in two parts.  Teacher forcing (_teacher_forced) shows
+every kernel except attention's two products bit-exact at full depth, and
+attention within 1e-5 at every layer.  End to end, against the path the
+reference takes on the GPU box's host (AVX-512 VNNI), north_star's
+1e-3 / 0.9999 bar is reported per case, and the envelope below is asserted.
+
 Why the end-to-end criterion is an envelope and not a fixed 1e-3 / 0.9999:
 every layer re-quantizes four activations to int8 with a per-sequence scale
 (model_int8.go:197,219,503,533), so a last-bit difference anywhere upstream
@@ -27,6 +33,12 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 REF_ORDERS = {"avx2": 1, "block_fma": 2, "arm64": 3}
+# north_star's end-to-end bar.  It is reported per case against the path the
+# reference takes on an AVX-512-VNNI host; the reference's own other paths
+# are reported against it too.  What is asserted at that depth is the
+# envelope below, and, under teacher forcing, bit-identity of every kernel
+# except attention (_teacher_forced).
+NORTH_STAR_MAX_ABS, NORTH_STAR_COS = 1e-3, 0.9999
 
 
 def say(*a):
@@ -54,6 +66,13 @@ def _check_envelope(got, oracle_model, toks, off, dim, tag, threads=16):
     say(f"{tag}: gpu-vs-vnni max-abs max {g_mad.max():.2e} mean {g_mad.mean():.2e} 1-cos max {g_dc.max():.2e} "
         f"mean {g_dc.mean():.2e} | reference spread max-abs max {e_mad.max():.2e} mean {e_mad.mean():.2e} "
         f"1-cos max {e_dc.max():.2e} mean {e_dc.mean():.2e}")
+
+    def verdict(mad, dc):
+        ok = mad.max() <= NORTH_STAR_MAX_ABS and dc.max() <= 1.0 - NORTH_STAR_COS
+        return "met" if ok else "NOT met"
+    say(f"{tag}: north_star bar (max-abs <= {NORTH_STAR_MAX_ABS:g}, cos >= {NORTH_STAR_COS}) against the VNNI path: "
+        f"GPU {verdict(g_mad, g_dc)}; the reference's own AVX2 / block-FMA / arm64 paths: "
+        + ", ".join(f"{n} {verdict(*e)}" for n, e in zip(REF_ORDERS, env)))
     # The spread comes from int8 re-quantization flips, whose number per
     # sequence is random; a systematic error would sit far above these bounds.
     assert g_mad.max() <= 2.0 * e_mad.max() + 1e-4
@@ -195,6 +214,111 @@ def test_device_path_reports_bad_token(tiny_gpu):
     with pytest.raises(SemanticaError) as ei:
         tiny_gpu.forward_device(toks.data_ptr(), np.array([0, 3], np.int32), 768, out.data_ptr())
     assert ei.value.code == _lib.SG_ERR_TOKEN
+
+
+def _teacher_forced(gpu, om, toks, off, dim, n_layers, tag, seam_layers=(), threads=16):
+    """Teacher-forced parity at every layer.  The GPU's per-layer trace
+    (sg_forward_trace) gives each layer's Q|K|V GEMM output, attention output
+    and residual stream.  The oracle (block-serial GEMM order) then reruns the
+    forward with each layer's attention output replaced by the GPU's, so both
+    sides feed identical values into everything after attention.  Asserted:
+      * Q|K|V and the residual stream after every layer are bit-identical:
+        every kernel other than attention's two products is exact, at any
+        depth (embedding, pre-norm + quantize, the GEMMs, post-norm +
+        residual, GELU * up and its quantize);
+      * the oracle's own attention on those (bit-identical) inputs is within
+        1e-5 relative of the GPU's, per sequence and layer;
+      * for `seam_layers`, the forward's fused attention prologue (Q's
+        QK-norm + RoPE + split) and K/V^T preparation give the same bits as the
+        kernel seam's k_qknorm_rope (bit-exact to the oracle) + sg_attention;
+      * with all layers traced, the final embeddings are bit-identical too.
+    Returns the per-layer maxima of the attention relative error."""
+    import torch
+    from semantica_gpu import kernels
+    c = om.config
+    T, d = int(off[-1]), c["embed_dim"]
+    hd = d // c["num_heads"]
+    qd, kvd = c["num_heads"] * hd, c["num_kv_heads"] * hd
+    d_tok = torch.from_numpy(np.ascontiguousarray(toks)).cuda()
+    qkv = torch.empty((n_layers, T, qd + 2 * kvd), dtype=torch.float32, device="cuda")
+    att = torch.empty((n_layers, T, qd), dtype=torch.float32, device="cuda")
+    h = torch.empty((n_layers, T, d), dtype=torch.float32, device="cuda")
+    say(f"{tag}: GPU trace of {n_layers} layers, {len(off) - 1} sequences, {T} tokens")
+    gpu.forward_trace(d_tok.data_ptr(), off, n_layers, qkv.data_ptr(), att.data_ptr(), h.data_ptr())
+    torch.cuda.synchronize()
+    for l in seam_layers:
+        q = qkv[l, :, :qd].contiguous()
+        k = qkv[l, :, qd:qd + kvd].contiguous()
+        v = qkv[l, :, qd + kvd:].contiguous()
+        ly = om_layers(om)[l]
+        qn = torch.from_numpy(ly["attn_q_norm"]).cuda()
+        kn = torch.from_numpy(ly["attn_k_norm"]).cuda()
+        kernels.qknorm_rope(gpu.ctx, q, k, qn, kn, c["num_heads"], c["num_kv_heads"], hd, c["norm_eps"],
+                            c["rope_base"], c["max_seq_len"], off)
+        seam = torch.empty((T, qd), dtype=torch.float32, device="cuda")
+        kernels.attention(gpu.ctx, seam, q, k, v, c["num_heads"], c["num_kv_heads"], hd, off)
+        torch.cuda.synchronize()
+        same = torch.equal(seam.view(torch.int32), att[l].view(torch.int32))
+        say(f"  layer {l}: fused prologue vs seam QK-norm/RoPE + attention bit-identical: {same}")
+        assert same, l
+    g_qkv, g_att, g_h = qkv.cpu().numpy(), att.cpu().numpy(), h.cpu().numpy()
+    del qkv, att, h
+    full = n_layers == c["num_layers"]
+    g_out = gpu.forward_packed(toks, off, dim) if full else None
+    rc, o_out, arr = om.forward_taps(toks, off, dim, n_layers, att_in=g_att, qkv=True, att=True, h=True,
+                                     n_threads=threads)
+    assert rc == 0
+    att_err = []
+    for l in range(n_layers):
+        assert np.array_equal(arr["qkv"][l].view(np.uint32), g_qkv[l].view(np.uint32)), f"{tag}: Q|K|V layer {l}"
+        assert np.array_equal(arr["h"][l].view(np.uint32), g_h[l].view(np.uint32)), f"{tag}: h after layer {l}"
+        rel = [np.linalg.norm(g_att[l, a:b].astype(np.float64) - arr["att"][l, a:b]) /
+               max(np.linalg.norm(arr["att"][l, a:b].astype(np.float64)), 1e-30) for a, b in zip(off[:-1], off[1:])]
+        att_err.append(max(rel))
+    say(f"{tag}: Q|K|V and h bit-identical after each of {n_layers} layers; attention rel err per layer "
+        f"max {max(att_err):.2e} (layers: {' '.join(f'{e:.1e}' for e in att_err)})")
+    assert max(att_err) <= 1e-5
+    if full:
+        assert np.array_equal(o_out.view(np.uint32), g_out.view(np.uint32)), f"{tag}: final embeddings"
+        say(f"{tag}: final embeddings (dim {dim}) bit-identical under teacher forcing")
+    return att_err
+
+
+def om_layers(om):
+    return om.model.layers
+
+
+def test_teacher_forced_config0(full_gpu, full_oracle):
+    """Config 0 shape (32-token rows, seed 0), 8 rows, all 24 layers."""
+    from semantica_gpu import synth
+    toks = synth.token_ids(8 * 32, 262144, seed=0)
+    off = np.arange(0, 8 * 32 + 1, 32, dtype=np.int32)
+    _teacher_forced(full_gpu, full_oracle, toks, off, 768, 24, "c0 forced", seam_layers=(0, 23))
+
+
+def test_teacher_forced_config4_slice(full_gpu, full_oracle):
+    """Config 4's first 24 ragged rows (log-uniform lengths, seed 1), 256 dims, all 24 layers."""
+    from semantica_gpu import synth
+    lens = synth.lengths_log_uniform(256, 8, 512, seed=1)[:24]
+    off = synth.offsets_from_lengths(lens)
+    toks = synth.token_ids(int(off[-1]), 262144, seed=1)
+    _teacher_forced(full_gpu, full_oracle, toks, off, 256, 24, "c4 slice forced", seam_layers=(5,))
+
+
+def test_teacher_forced_long_sequences(gpu_ctx, oracle):
+    """Config 3's lengths past 512 keys (the recomputing attention kernel), 4 layers."""
+    from semantica_gpu import Model, synth
+    cfg = dict(synth.EMBEDDINGGEMMA_300M, num_layers=4, vocab_size=8192)
+    mdl = synth.make_model(cfg, seed_weights=9)
+    lens = [1500, 2048, 1024, 600]
+    off = synth.offsets_from_lengths(lens)
+    toks = synth.token_ids(int(off[-1]), 8192, seed=4)
+    m = Model(gpu_ctx, mdl)
+    try:
+        _teacher_forced(m, oracle.OracleModel(mdl), toks, off, 768, 4, "c3 lengths forced", seam_layers=(1,),
+                        threads=4)
+    finally:
+        m.close()
 
 
 def test_config0_envelope(full_gpu, full_oracle):
