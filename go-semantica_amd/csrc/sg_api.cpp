@@ -212,14 +212,6 @@ hipStream_t ctx_stream(const sg_ctx* c, void* stream) {
 }
 }  // namespace sgi
 
-struct sg_q8_weight {
-  sg_ctx* ctx = nullptr;
-  int N = 0, K = 0;
-  _Float16* w = nullptr;  // block-major [K/32][N][32]
-  int8_t* w8 = nullptr;   // the same values as int8, same layout
-  float* st = nullptr;    // [K/32][N]
-};
-
 namespace {
 
 struct LayerDev {
@@ -561,6 +553,7 @@ int sg_init(int device_ordinal, sg_ctx** out) {
   if (device_ordinal < 0 || device_ordinal >= n)
     return fail(SG_ERR_INVALID, "device %d out of range (%d devices)", device_ordinal, n);
   SG_HIP(hipSetDevice(device_ordinal));
+  SG_TRY(sgi::noalloc_setup(device_ordinal));
   sg_ctx* c = new sg_ctx;
   c->device = device_ordinal;
   // A blocking stream (default flags and priority): it orders with the legacy

@@ -19,6 +19,10 @@ __attribute__((visibility("hidden"))) int fail(int code, const char* fmt, ...);
 __attribute__((visibility("hidden"))) int ctx_device(const sg_ctx* c);
 __attribute__((visibility("hidden"))) hipStream_t ctx_stream(const sg_ctx* c, void* stream);
 
+// Resolves, once per device and with that device current, the device address
+// of the allocation-free entry points' static scratch (sg_noalloc.hip).
+__attribute__((visibility("hidden"))) int noalloc_setup(int device);
+
 // A tokenizer's vocabulary and settings (tokenizer.New's arguments plus the
 // special ids LoadFromGGUF sets).  types empty = every token normal.
 struct TokenizerSpec {
@@ -106,6 +110,15 @@ struct HostBuf {
   }
 };
 }  // namespace sgi
+
+// A Q8_0 weight matrix repacked on the device (kernel seam).
+struct sg_q8_weight {
+  sg_ctx* ctx = nullptr;
+  int N = 0, K = 0;
+  _Float16* w = nullptr;  // block-major [K/32][N][32]
+  int8_t* w8 = nullptr;   // the same values as int8, same layout
+  float* st = nullptr;    // [K/32][N]
+};
 
 #define SG_HIP(call)                                                                                     \
   do {                                                                                                   \

@@ -74,6 +74,14 @@ def matmul_q8_0(ctx, dst, w: Q8Weight, x, row_scale, stream=None):
                                            _stream(stream)))
 
 
+def matmul_q8_0_noalloc(ctx, dst, w: Q8Weight, x, row_scale, stream=None):
+    """matmul_q8_0 with the operand relayout in the library's fixed per-device
+    scratch (sg_matmul_q8_0_int8_noalloc): no device allocation."""
+    _check_dev(dst, x, row_scale)
+    _lib.check(ctx.lib.sg_matmul_q8_0_int8_noalloc(ctx.handle, _vp(dst), w.handle, _vp(x), _vp(row_scale),
+                                                   x.shape[0], _stream(stream)))
+
+
 def ffn_gate_up(ctx, dst, w_gate: Q8Weight, w_up: Q8Weight, x, row_scale, stream=None):
     """geluquick(x @ w_gate) * (x @ w_up) in one GEMM (model_int8.go:520-535)."""
     _check_dev(dst, x, row_scale)

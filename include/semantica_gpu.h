@@ -208,6 +208,19 @@ int sg_quantize_act(sg_ctx *ctx, const float *x, int32_t rows, int32_t cols,
 int sg_matmul_q8_0_int8(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const int8_t *x,
                         const float *row_scale, int32_t batch, void *stream);
 
+/* sg_matmul_q8_0_int8 without any device allocation: the same kernels and the
+ * same results, with the activation operand relaid in a fixed per-device
+ * array of SG_NOALLOC_SCRATCH_BYTES (resolved by sg_init, held until the
+ * process ends) instead of a library-grown buffer.  No counterpart in the
+ * reference: for callers that cannot allocate (HIP graph capture, serving
+ * loops).  Limit: gemm_pad(batch) x in_dim bytes from 4096 rows (int8
+ * operands), twice that below (fp16 operands), where gemm_pad rounds up to
+ * 256 rows; larger inputs return SG_ERR_INVALID before any launch.  Calls
+ * that overlap on one device (e.g. on two streams) race on the array. */
+#define SG_NOALLOC_SCRATCH_BYTES (64u << 20)
+int sg_matmul_q8_0_int8_noalloc(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const int8_t *x,
+                                const float *row_scale, int32_t batch, void *stream);
+
 /* The exact int32 block dot products of the same GEMM, out[batch][out_dim][in_dim/32]
  * (what matmulInnerLoop* converts with VCVTDQ2PS, simd_amd64.s:290). */
 int sg_q8_block_sums(sg_ctx *ctx, int32_t *out, const sg_q8_weight *w, const int8_t *x,
