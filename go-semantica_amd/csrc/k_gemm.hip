@@ -438,10 +438,15 @@ __global__ __launch_bounds__(NW* SG_WAVE) void k_gemm_q8_sp(const _Float16* __re
 // is a loop-invariant vector address plus an immediate; the LDS is laid out
 // [A stages][W stages][scale stages] to keep those immediates under 64 KB.
 // Only the MFMAs and the FMAs of the block-serial epilogue are vector work.
+// Publishes a ring stage: this wave's copies older than the last N have
+// landed (vmcnt) and its own LDS fragment reads have completed (lgkmcnt), so
+// after the following barrier no wave still reads the stage the next copies
+// overwrite.  (The compiler may place the last MFMAs of the previous step, and
+// their lgkmcnt waits, after an s_barrier, so the read wait is explicit.)
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N <= 63, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
 }
 
 constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor, gfx9 family

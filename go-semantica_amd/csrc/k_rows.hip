@@ -114,6 +114,18 @@ __global__ void k_fill(float* __restrict__ p, float v, int64_t n) {
   if (i < n) p[i] = v;
 }
 
+__global__ void k_fill_i32(int32_t* __restrict__ p, int32_t v, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// The first row r < T whose token is outside [0, vocab), folded into *first
+// (atomicMin; *first starts at T or above).
+__global__ void k_first_bad_token(const int32_t* __restrict__ tokens, int T, int vocab, int32_t* __restrict__ first) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r < T && (tokens[r] < 0 || tokens[r] >= vocab)) atomicMin(first, r);
+}
+
 // ------------------------------------------------------------- embedding --
 
 // Embedding (model_int8.go:166-184): h = float32(q) * d' (d' through the
@@ -125,7 +137,7 @@ __device__ __forceinline__ int gather_row(const int32_t* tokens, int row, const 
   constexpr int D = NPL * 8;
   int id = tokens[row];
   if (id < 0 || id >= vocab) {
-    if (j == 0) atomicOr(err, 1);
+    if (j == 0) atomicMin(err, row);  // the first offending row (rows run in request order)
     id = 0;  // keep the access in bounds; the call reports SG_ERR_TOKEN
   }
   const int8_t* qr = eq + (int64_t)id * D;
@@ -661,6 +673,18 @@ hipError_t i8_blocked(const int8_t* x, int M, int K, int8_t* y, int a_rows, hipS
 hipError_t fill_f32(float* p, float v, int64_t n, hipStream_t s) {
   if (n <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_fill, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, v, n);
+  return hipGetLastError();
+}
+
+hipError_t fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_fill_i32, dim3(blocks_for(n, 256)), dim3(256), 0, s, p, v, n);
+  return hipGetLastError();
+}
+
+hipError_t first_bad_token(const int32_t* tokens, int T, int vocab, int32_t* first, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_first_bad_token, dim3(blocks_for(T, 256)), dim3(256), 0, s, tokens, T, vocab, first);
   return hipGetLastError();
 }
 

@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -437,7 +438,7 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
   };
 
   SG_LAUNCH(SG_K_OTHER, 4.0 * 4 * L * ns, sgk::fill_f32(amax, 0.0f, (int64_t)4 * L * ns, s));
-  SG_LAUNCH(SG_K_OTHER, 4.0, sgk::fill_f32(m->err.as<float>(), 0.0f, 1, s));
+  SG_LAUNCH(SG_K_OTHER, 4.0, sgk::fill_i32(m->err.as<int32_t>(), INT32_MAX, 1, s));
   SG_LAUNCH(SG_K_NORM, t * (34.0 * d / 32 + 4.0 * d),
             sgk::embed_norm(d_tokens, T, m->emb_q, m->emb_s, c.vocab_size, d, m->sqrt_d, m->layers[0].attn_norm,
                             eps, meta.row_seq, h, nullptr, site(0, 0), m->err.as<int32_t>(), s));
@@ -484,21 +485,50 @@ int run_forward(sg_model* m, const int32_t* d_tokens, const Meta& meta, int out_
   return SG_OK;
 }
 
-// Reference error cases (forwardINT8WithDim model_int8.go:150-155 per
-// sequence, ForwardWithDim model.go:661-667 for the dimension).
-int check_forward_args(const sg_model* m, const int32_t* off, int n_seq, int out_dim) {
+// Reference error cases.  ForwardWithDim (model.go:661-667) checks the
+// dimension first; then every request carries its own error
+// (forwardINT8WithDim, model_int8.go:150-171: empty, too long, then its first
+// out-of-range token) and embedPrompts returns the first request's error in
+// request order (api.go:286-292).  Here: the dimension and the offsets'
+// shape, then *len_err_seq = the first sequence that is empty or too long
+// (n_seq if none).  Token errors of the sequences before it come first; the
+// caller checks them on the device.
+int check_forward_args(const sg_model* m, const int32_t* off, int n_seq, int out_dim, int* len_err_seq) {
   const sg_model_config& c = m->cfg;
   if (out_dim <= 0 || out_dim > c.embed_dim)
     return fail(SG_ERR_DIM, "target dimension %d out of range (1..%d)", out_dim, c.embed_dim);
   if (!off || n_seq <= 0) return fail(SG_ERR_INVALID, "no sequences");
   if (off[0] != 0) return fail(SG_ERR_INVALID, "seq_offsets[0] must be 0");
+  for (int i = 0; i < n_seq; i++)
+    if (off[i + 1] < off[i]) return fail(SG_ERR_INVALID, "seq_offsets must be non-decreasing");
+  *len_err_seq = n_seq;
   for (int i = 0; i < n_seq; i++) {
     const int S = off[i + 1] - off[i];
-    if (S < 0) return fail(SG_ERR_INVALID, "seq_offsets must be non-decreasing");
-    if (S == 0) return fail(SG_ERR_EMPTY, "empty input");
-    if (S > c.max_seq_len) return fail(SG_ERR_TOO_LONG, "sequence too long: %d > %d", S, c.max_seq_len);
+    if (S == 0 || S > c.max_seq_len) {
+      *len_err_seq = i;
+      break;
+    }
   }
   return SG_OK;
+}
+
+int length_error(const sg_model* m, int S) {
+  if (S == 0) return fail(SG_ERR_EMPTY, "empty input");
+  return fail(SG_ERR_TOO_LONG, "sequence too long: %d > %d", S, m->cfg.max_seq_len);
+}
+
+// *row (device, written by an embedding kernel or first_bad_token) -> the
+// reference's message with the offending id, or SG_OK when no row was recorded.
+int token_error(sg_model* m, const int32_t* d_tokens, hipStream_t s) {
+  SG_TRY(m->io_h.ensure(64));
+  int32_t* h = m->io_h.as<int32_t>();
+  SG_HIP(hipMemcpyAsync(h, m->err.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  SG_HIP(hipStreamSynchronize(s));
+  if (h[0] == INT32_MAX) return SG_OK;
+  const int32_t row = h[0];
+  SG_HIP(hipMemcpyAsync(h + 1, d_tokens + row, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+  SG_HIP(hipStreamSynchronize(s));
+  return fail(SG_ERR_TOKEN, "token ID out of range: %d", h[1]);
 }
 
 int ensure_workspace(sg_model* m, int T, int n_seq, int Tp) {
@@ -523,19 +553,24 @@ int ensure_workspace(sg_model* m, int T, int n_seq, int Tp) {
 
 int forward_device_locked(sg_model* m, const int32_t* d_tokens, const int32_t* off, int n_seq, int out_dim,
                           float* d_out, hipStream_t s, int stop = -1, const Trace* tr = nullptr) {
-  SG_TRY(check_forward_args(m, off, n_seq, out_dim));
+  int len_err_seq = n_seq;
+  SG_TRY(check_forward_args(m, off, n_seq, out_dim, &len_err_seq));
   SG_TRY(set_device(m->ctx));
+  if (len_err_seq < n_seq) {  // the tokens of the sequences before it decide first
+    SG_TRY(m->err.ensure(64));
+    SG_HIP(sgk::fill_i32(m->err.as<int32_t>(), INT32_MAX, 1, s));
+    SG_HIP(sgk::first_bad_token(d_tokens, off[len_err_seq], m->cfg.vocab_size, m->err.as<int32_t>(), s));
+    SG_TRY(token_error(m, d_tokens, s));
+    return length_error(m, off[len_err_seq + 1] - off[len_err_seq]);
+  }
   const int T = off[n_seq];
   Meta meta;
   SG_TRY(stage_meta(off, n_seq, m->cfg.num_heads / m->cfg.num_kv_heads, m->meta_h, m->meta_d, s, meta));
   SG_TRY(ensure_workspace(m, T, n_seq, meta.Tp));
   SG_TRY(run_forward(m, d_tokens, meta, out_dim, d_out, s, stop, tr));
-  SG_TRY(m->io_h.ensure(64));
-  SG_HIP(hipMemcpyAsync(m->io_h.p, m->err.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
   SG_HIP(hipStreamSynchronize(s));
   if (m->prof.on) SG_TRY(m->prof.fold());
-  if (*m->io_h.as<int32_t>() != 0) return fail(SG_ERR_TOKEN, "token ID out of range");
-  return SG_OK;
+  return token_error(m, d_tokens, s);
 }
 
 }  // namespace
@@ -852,6 +887,44 @@ int sg_matmul_q8_0_int8(sg_ctx* ctx, float* dst, const sg_q8_weight* w, const in
   return matmul_common(ctx, dst, nullptr, w, x, row_scale, batch, stream);
 }
 
+int sg_matmul_q8_0_int8_bench(sg_ctx* ctx, float* dst, const sg_q8_weight* w, const int8_t* x, const float* row_scale,
+                              int32_t batch, int32_t reps, void* stream, float* us_per_launch) {
+  if (!ctx || !w || !x || !dst || !row_scale || !us_per_launch) return fail(SG_ERR_INVALID, "NULL argument");
+  if (batch <= 0 || reps <= 0) return fail(SG_ERR_INVALID, "batch and reps must be positive");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  SG_TRY(set_device(ctx));
+  hipStream_t s = pick(ctx, stream);
+  const int ar = sgk::gemm_pad_rows(batch);
+  const bool i8 = batch >= sgk::kI8MinRows;
+  SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)ar * w->K));
+  SG_TRY(gemm_scratch_begin(ctx, s));
+  if (i8)
+    SG_HIP(sgk::i8_blocked(x, batch, w->K, ctx->f16.as<int8_t>(), ar, s));
+  else
+    SG_HIP(sgk::i8_to_f16_blocked(x, batch, w->K, ctx->f16.as<_Float16>(), ar, s));
+  auto gemm = [&]() {
+    return i8 ? sgk::gemm_q8_i8(ctx->f16.as<int8_t>(), ar, w->w8, w->st, row_scale, dst, batch, w->N, w->K, s)
+              : sgk::gemm_q8(ctx->f16.as<_Float16>(), ar, w->w, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s);
+  };
+  SG_HIP(gemm());  // warm
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    if (e0) (void)hipEventDestroy(e0);
+    return fail(SG_ERR_DEVICE, "hipEventCreate failed");
+  }
+  hipError_t e = hipEventRecord(e0, s);
+  for (int i = 0; i < reps && e == hipSuccess; i++) e = gemm();
+  if (e == hipSuccess) e = hipEventRecord(e1, s);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  SG_HIP(e);
+  *us_per_launch = ms * 1000.0f / (float)reps;
+  return gemm_scratch_end(ctx, s);
+}
+
 int sg_q8_block_sums(sg_ctx* ctx, int32_t* out, const sg_q8_weight* w, const int8_t* x, int32_t batch, void* stream) {
   return matmul_common(ctx, nullptr, out, w, x, nullptr, batch, stream);
 }
@@ -984,14 +1057,10 @@ int sg_embed_tokens(sg_model* m, float* dst, const int32_t* d_tokens, int32_t n_
   SG_TRY(set_device(m->ctx));
   hipStream_t s = pick(m->ctx, stream);
   SG_TRY(m->err.ensure(64));
-  SG_TRY(m->io_h.ensure(64));
-  SG_HIP(sgk::fill_f32(m->err.as<float>(), 0.0f, 1, s));
+  SG_HIP(sgk::fill_i32(m->err.as<int32_t>(), INT32_MAX, 1, s));
   SG_HIP(sgk::embed_only(d_tokens, n_tokens, m->emb_q, m->emb_s, m->cfg.vocab_size, m->cfg.embed_dim, m->sqrt_d, dst,
                          m->err.as<int32_t>(), s));
-  SG_HIP(hipMemcpyAsync(m->io_h.p, m->err.p, sizeof(int32_t), hipMemcpyDeviceToHost, s));
-  SG_HIP(hipStreamSynchronize(s));
-  if (*m->io_h.as<int32_t>() != 0) return fail(SG_ERR_TOKEN, "token ID out of range");
-  return SG_OK;
+  return token_error(m, d_tokens, s);
 }
 
 int sg_pool_l2(sg_ctx* ctx, float* out, const float* x, int32_t ldx, int32_t out_dim, const int32_t* off, int32_t n_seq,

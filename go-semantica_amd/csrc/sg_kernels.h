@@ -44,10 +44,15 @@ hipError_t i8_to_f16_blocked(const int8_t* x, int M, int K, _Float16* y, int a_r
 // int8 x[M][K] -> block-major int8 y[K/32][a_rows][32] (gemm_q8_i8's operand).
 hipError_t i8_blocked(const int8_t* x, int M, int K, int8_t* y, int a_rows, hipStream_t s);
 hipError_t fill_f32(float* p, float v, int64_t n, hipStream_t s);
+hipError_t fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s);
+// The first row r < T with tokens[r] outside [0, vocab), folded into *first by
+// atomicMin (the embedding kernels record theirs the same way).
+hipError_t first_bad_token(const int32_t* tokens, int T, int vocab, int32_t* first, hipStream_t s);
 
 // ---- per-row kernels (k_rows.hip) ----
 // Embedding gather * sqrt(d) -> h; then RMSNorm(w) -> xn (stored when xn != null) and
-// per-sequence max|xn| -> amax.
+// per-sequence max|xn| -> amax.  A token outside [0, vocab) is read as token 0
+// and its row folded into *err by atomicMin (*err starts at INT32_MAX).
 hipError_t embed_norm(const int32_t* tokens, int T, const int8_t* eq, const float* es, int vocab, int d,
                       float sqrt_d, const float* w, float eps, const int32_t* row_seq, float* h, float* xn,
                       float* amax, int32_t* err, hipStream_t s);

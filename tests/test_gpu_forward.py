@@ -205,16 +205,35 @@ def test_forward_errors(tiny_gpu):
     assert tiny_gpu.forward_batch([[3, 4, 5]], 768).shape == (1, 768)
 
 
-def test_device_path_reports_bad_token(tiny_gpu):
+def test_device_path_errors_match_host_path(tiny_gpu):
+    """sg_forward_device (tokens already in HBM) reports the same error as the
+    host path, in the reference's request order (api.go:286-292: the first
+    request with an error wins; model_int8.go:150-171: within a request,
+    empty / too long before its first out-of-range token), with the
+    offending id in the message."""
     import torch
     from semantica_gpu import SemanticaError, _lib
-    say("device-path token validation")
-    toks = torch.tensor([3, 4, 99999], dtype=torch.int32, device="cuda")
-    out = torch.empty((1, 768), dtype=torch.float32, device="cuda")
-    with pytest.raises(SemanticaError) as ei:
-        tiny_gpu.forward_device(toks.data_ptr(), np.array([0, 3], np.int32), 768, out.data_ptr())
-    assert ei.value.code == _lib.SG_ERR_TOKEN
-
+    say("device-path error order")
+    cases = [  # (sequences, expected code, expected message)
+        ([[3, 4], [9, 4096, 2], [5] * 2049], _lib.SG_ERR_TOKEN, "token ID out of range: 4096"),
+        ([[5] * 2049, [9, 4096]], _lib.SG_ERR_TOO_LONG, "sequence too long: 2049 > 2048"),
+        ([[3], [], [1, -3]], _lib.SG_ERR_EMPTY, "empty input"),
+        ([[1, -5, 2, 300000]], _lib.SG_ERR_TOKEN, "token ID out of range: -5"),
+        ([[1, 2], [7, 8, 99999], [4, -1]], _lib.SG_ERR_TOKEN, "token ID out of range: 99999"),
+        ([[1, 2], [7, 8], [], [4, -1]], _lib.SG_ERR_EMPTY, "empty input"),
+    ]
+    for seqs, code, msg in cases:
+        toks = np.array([t for q in seqs for t in q], np.int32)
+        off = np.cumsum([0] + [len(q) for q in seqs]).astype(np.int32)
+        d_tok = torch.from_numpy(toks if toks.size else np.zeros(1, np.int32)).cuda()
+        out = torch.empty((len(seqs), 768), dtype=torch.float32, device="cuda")
+        with pytest.raises(SemanticaError) as eh:
+            tiny_gpu.forward_packed(toks, off, 768)
+        with pytest.raises(SemanticaError) as ed:
+            tiny_gpu.forward_device(d_tok.data_ptr(), off, 768, out.data_ptr())
+        say(f"  {[len(q) for q in seqs]}: host '{eh.value.message}' device '{ed.value.message}'")
+        assert (eh.value.code, eh.value.message) == (ed.value.code, ed.value.message) == (code, msg)
+    assert tiny_gpu.forward_batch([[3, 4, 5]], 768).shape == (1, 768)
 
 def _teacher_forced(gpu, om, toks, off, dim, n_layers, tag, seam_layers=(), threads=16):
     """Teacher-forced parity at every layer.  The GPU's per-layer trace
