@@ -39,8 +39,11 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--seq-len", type=int, default=512)
-    ap.add_argument("--cpu-threads", type=int, default=0, help="0: min(16, host CPUs)")
-    ap.add_argument("--cpu-seqs", type=int, default=0, help="0: 6 x cpu threads")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="0: min(16, host CPUs) -- 16 is one GPU's CPU share on the GPU boxes")
+    ap.add_argument("--cpu-warmup", type=int, default=2, help="c2 CPU warm-up runs (the reference's: 5)")
+    ap.add_argument("--cpu-runs", type=int, default=8,
+                    help="c2 CPU timed runs, P50 reported (the reference's: 20; 8 keeps the sample near 20 s)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-search", action="store_true", help="skip the brute-force search measurement")
     ap.add_argument("--no-extras", action="store_true",
@@ -57,27 +60,88 @@ def parse():
     return ap.parse_args()
 
 
-def cpu_baseline(model, toks, seq_len, threads, n_seq):
-    """The oracle's forward (AVX2 restatement of the reference's VNNI Go path,
-    one worker per sequence like embedPrompts) on n_seq of the workload's rows."""
+def _cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _p50(values):
+    """calculateStats's P50 (cmd/benchmark/main.go:571-600): sorted[int(n * 0.5)]."""
+    v = sorted(values)
+    return v[min(int(len(v) * 0.5), len(v) - 1)]
+
+
+def cpu_baseline(model, toks, seq_len, threads, c2_warmup, c2_runs):
+    """The oracle's forward (C restatement of the reference's INT8 Go path; the
+    VNNI accumulation order on AVX-512 VNNI intrinsics when the host has them,
+    as simd_amd64.go:41-45 dispatches) timed on this host.
+      c2: runs of `threads` 512-token rows of the workload, one worker per
+          sequence as embedPrompts fans out (api.go:237-295); embeddings/s from
+          the P50 run time after c2_warmup warm-up runs.
+      c0: one 32-token sequence (the first 32 tokens of the workload), its GEMMs
+          split into column chunks over `threads` threads like
+          matMulQ8_0INT8Tiled (model_int8.go:258-346); 5 warm-ups, P50 of 20
+          runs (measureSingleDocLatency, cmd/benchmark/main.go:553-637).
+    CPU time is getrusage(RUSAGE_SELF) over each run."""
+    import resource
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle
-    if n_seq * seq_len > toks.size:
-        raise ValueError(f"CPU sample of {n_seq} sequences exceeds the workload")
+    lib = oracle.load()
     om = oracle.OracleModel(model)
+
+    def timed(fn):
+        r0, t0 = resource.getrusage(resource.RUSAGE_SELF), time.perf_counter()
+        rc = fn()
+        t1, r1 = time.perf_counter(), resource.getrusage(resource.RUSAGE_SELF)
+        if rc != 0:
+            raise RuntimeError(f"oracle forward failed: {rc}")
+        return t1 - t0, (r1.ru_utime - r0.ru_utime) + (r1.ru_stime - r0.ru_stime)
+
+    n_seq = threads
+    if n_seq * seq_len > toks.size:
+        raise ValueError("CPU sample exceeds the workload")
     off = np.arange(0, n_seq * seq_len + 1, seq_len, dtype=np.int32)
     sample = np.ascontiguousarray(toks[: n_seq * seq_len])
-    om.forward_batch(sample[:seq_len], off[:2], 768, n_threads=1)  # warm caches / page in weights
-    t0 = time.perf_counter()
-    rc, _ = om.forward_batch(sample, off, 768, n_threads=threads)
-    dt = time.perf_counter() - t0
+    c2 = []
+    for i in range(c2_warmup + c2_runs):
+        r = timed(lambda: om.forward_batch(sample, off, 768, n_threads=threads)[0])
+        if i >= c2_warmup:
+            c2.append(r)
+    wall2 = _p50([w for w, _ in c2])
+    cpu2 = _p50([c for _, c in c2])
+
+    off0 = np.array([0, 32], np.int32)
+    tok0 = np.ascontiguousarray(toks[:32])
+    lib.sgo_set_gemm_threads(threads)
+    try:
+        c0 = []
+        for i in range(25):
+            r = timed(lambda: om.forward_batch(tok0, off0, 768, n_threads=1)[0])
+            if i >= 5:
+                c0.append(r)
+    finally:
+        lib.sgo_set_gemm_threads(1)
     om.close()
-    if rc != 0:
-        raise RuntimeError(f"oracle forward failed: {rc}")
-    return {"value": round(n_seq / dt, 3), "unit": "embeddings/sec", "cores": threads, "kind": "port",
-            "sample": f"{n_seq} sequences x {seq_len} tokens (rows 0..{n_seq - 1} of the workload), "
-                      f"C oracle, AVX2 VNNI-order GEMM, {threads} threads, {dt:.1f} s"}
+    isa = {2: "AVX-512 VNNI", 1: "AVX2 (VNNI lane order emulated)", 0: "scalar"}[lib.sgo_simd_level()]
+    return {"value": round(n_seq / wall2, 3), "unit": "embeddings/sec", "cores": threads, "kind": "port",
+            "host": {"nproc": os.cpu_count(), "model_name": _cpu_model_name(), "threads_used": threads},
+            "c2": {"embeddings_per_s": round(n_seq / wall2, 3), "p50_run_s": round(wall2, 3),
+                   "p50_cpu_s_per_embedding": round(cpu2 / n_seq, 3), "warmup": c2_warmup, "runs": c2_runs,
+                   "run": f"{n_seq} sequences x {seq_len} tokens (rows 0..{n_seq - 1} of the workload), "
+                          f"one worker per sequence"},
+            "c0": {"p50_ms": round(_p50([w for w, _ in c0]) * 1e3, 2),
+                   "p50_cpu_ms": round(_p50([c for _, c in c0]) * 1e3, 2), "warmup": 5, "runs": 20,
+                   "run": f"1 x 32 tokens, GEMM column chunks over {threads} threads"},
+            "sample": f"C oracle (restatement of the reference's INT8 Go path), VNNI-order GEMM on {isa}, "
+                      f"{threads} threads; c2 P50 of {c2_runs} runs after {c2_warmup} warm-ups, "
+                      f"c0 P50 of 20 runs after 5 warm-ups"}
 
 
 def search_leg(ctx, n, dim, batch, top_k, steps, with_cpu, gpu_events=True):
@@ -193,13 +257,14 @@ C1_SHAPES = (("Q/O", 768, 768), ("K/V", 256, 768), ("gate/up", 1152, 768), ("dow
              ("3072x768", 3072, 768), ("768x3072", 768, 3072))
 
 
-def gemm_c1_leg(ctx, m=2048, reps=50):
+def gemm_c1_leg(ctx, m=2048, reps=200):
     """Config 1: the isolated Q8_0 GEMMs at the model's layer shapes with M = 2048
-    rows, through sg_matmul_q8_0_int8 (the kernel seam: int8 activations in,
-    fp32 out, including the operand relayout it performs).  Back-to-back calls on
-    one stream between two HIP events, so launch gaps do not dominate.  Work =
-    2*M*N*K int8 ops; bytes = int8 A + Q8_0 W (34/32 B per weight) + fp32 Y +
-    fp32 row scales, each once."""
+    rows.  The GEMM kernel alone: sg_matmul_q8_0_int8_bench relays the int8
+    activations into the operand layout once, then times `reps` back-to-back
+    launches of the kernel sg_matmul_q8_0_int8 runs, between two HIP events on
+    one stream.  Work = 2*M*N*K int8 ops; bytes = int8 A + Q8_0 W (34/32 B per
+    weight) + fp32 Y + fp32 row scales, each once.  Each shape is also set
+    against its time at the int8 peak and at 8 TB/s."""
     import numpy as np
     import torch
     from semantica_gpu import kernels, synth
@@ -213,22 +278,16 @@ def gemm_c1_leg(ctx, m=2048, reps=50):
         rs = torch.full((m,), 0.01, dtype=torch.float32, device="cuda")
         y = torch.empty((m, n), dtype=torch.float32, device="cuda")
         torch.cuda.synchronize()  # inputs made on the default stream are complete
-        with torch.cuda.stream(stream):
-            for _ in range(3):
-                kernels.matmul_q8_0(ctx, y, w, x, rs, stream=stream.cuda_stream)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(reps):
-                kernels.matmul_q8_0(ctx, y, w, x, rs, stream=stream.cuda_stream)
-            e1.record(stream)
-        e1.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / reps
+        us = kernels.matmul_q8_0_kernel_us(ctx, y, w, x, rs, reps, stream=stream.cuda_stream)
         ops, nbytes = 2.0 * m * n * k, m * k + n * k * 34 / 32 + m * n * 4 + m * 4
-        res.append({"gemm": name, "N": n, "K": k, "us": round(us, 2), "TOPS_int8": round(ops / us / 1e6, 1),
+        res.append({"gemm": name, "N": n, "K": k, "kernel_us": round(us, 2), "TOPS_int8": round(ops / us / 1e6, 1),
                     "frac_int8_peak": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
-                    "GB_s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
+                    "GB_s": round(nbytes / us / 1e3, 1), "frac_hbm": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                    "us_at_int8_peak": round(ops / INT8_PEAK_TOPS / 1e6, 2),
+                    "us_at_8TBs": round(nbytes / HBM_PEAK_GBS / 1e3, 2)})
         w.close()
-    return {"workload": f"config 1: isolated Q8_0 GEMMs, M = {m}, seed-random Q8_0 weights, {reps} back-to-back calls",
+    return {"workload": f"config 1: isolated Q8_0 GEMM kernels, M = {m}, seed-random Q8_0 weights, "
+                        f"{reps} back-to-back launches per shape (operand relayout outside the timed region)",
             "shapes": res}
 
 
@@ -400,7 +459,7 @@ def main():
     ctx.close()
     if not a.no_cpu_baseline:
         threads = a.cpu_threads or min(16, os.cpu_count() or 1)
-        line["cpu_baseline"] = cpu_baseline(mdl, toks, S, threads, min(a.cpu_seqs or 6 * threads, B))
+        line["cpu_baseline"] = cpu_baseline(mdl, toks, S, min(threads, B), a.cpu_warmup, a.cpu_runs)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -82,6 +82,16 @@ def matmul_q8_0_noalloc(ctx, dst, w: Q8Weight, x, row_scale, stream=None):
                                                    x.shape[0], _stream(stream)))
 
 
+def matmul_q8_0_kernel_us(ctx, dst, w: Q8Weight, x, row_scale, reps: int, stream=None) -> float:
+    """Average time of the GEMM kernel alone over `reps` back-to-back launches
+    (sg_matmul_q8_0_int8_bench; the operand relayout runs once, untimed)."""
+    _check_dev(dst, x, row_scale)
+    us = ctypes.c_float()
+    _lib.check(ctx.lib.sg_matmul_q8_0_int8_bench(ctx.handle, _vp(dst), w.handle, _vp(x), _vp(row_scale), x.shape[0],
+                                                 reps, _stream(stream), ctypes.byref(us)))
+    return float(us.value)
+
+
 def ffn_gate_up(ctx, dst, w_gate: Q8Weight, w_up: Q8Weight, x, row_scale, stream=None):
     """geluquick(x @ w_gate) * (x @ w_up) in one GEMM (model_int8.go:520-535)."""
     _check_dev(dst, x, row_scale)

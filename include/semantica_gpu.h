@@ -221,6 +221,15 @@ int sg_matmul_q8_0_int8(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const in
 int sg_matmul_q8_0_int8_noalloc(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const int8_t *x,
                                 const float *row_scale, int32_t batch, void *stream);
 
+/* Measurement hook for the GEMM kernel alone (no counterpart in the
+ * reference): relays x into the operand layout once, then launches the same
+ * GEMM kernel sg_matmul_q8_0_int8 uses `reps` times back to back on `stream`
+ * between two HIP events and returns the average time per launch.  dst is
+ * written as by sg_matmul_q8_0_int8.  Synchronizes the stream. */
+int sg_matmul_q8_0_int8_bench(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const int8_t *x,
+                              const float *row_scale, int32_t batch, int32_t reps, void *stream,
+                              float *us_per_launch);
+
 /* The exact int32 block dot products of the same GEMM, out[batch][out_dim][in_dim/32]
  * (what matmulInnerLoop* converts with VCVTDQ2PS, simd_amd64.s:290). */
 int sg_q8_block_sums(sg_ctx *ctx, int32_t *out, const sg_q8_weight *w, const int8_t *x,

@@ -77,6 +77,7 @@ def load():
                                             ctypes.POINTER(Taps)]),
         "sgo_simd_level": (ctypes.c_int, []),
         "sgo_force_scalar": (None, [ctypes.c_int]),
+        "sgo_set_gemm_threads": (None, [ctypes.c_int]),
         "sgo_bf_normalize": (None, [vp, ctypes.c_int]),
         "sgo_bf_quantize_i8": (None, [vp, ctypes.c_int, vp]),
         "sgo_bf_quantize_i16": (None, [vp, ctypes.c_int, vp]),

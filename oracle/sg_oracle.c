@@ -28,20 +28,26 @@
 
 static int g_force_scalar = 0;
 static int g_simd = -1;
+static int g_gemm_threads = 1;
 
 void sgo_force_scalar(int on) { g_force_scalar = on; }
 
+/* 0 scalar, 1 AVX2+FMA, 2 AVX2+FMA and AVX-512 VNNI (with VL), the ISA the
+ * reference dispatches on (simd_amd64.go:9-13,41-45). */
 int sgo_simd_level(void) {
   if (g_simd < 0) {
 #if SGO_X86
     __builtin_cpu_init();
     g_simd = (__builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma")) ? 1 : 0;
+    if (g_simd && __builtin_cpu_supports("avx512vnni") && __builtin_cpu_supports("avx512vl")) g_simd = 2;
 #else
     g_simd = 0;
 #endif
   }
   return g_force_scalar ? 0 : g_simd;
 }
+
+void sgo_set_gemm_threads(int n) { g_gemm_threads = n < 1 ? 1 : n; }
 
 static inline float bits_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static inline uint32_t f32_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
@@ -204,6 +210,28 @@ static float q8_dot_avx2(const int8_t *xr, const uint8_t *wr, const float *sc, i
   return hsum8(l);
 }
 
+/* matmulInnerLoopVNNIAsm itself (simd_amd64.s:241-304) on an AVX-512-VNNI
+ * host: VPDPBUSD of (w ^ 0x80) as unsigned bytes with x, minus 128 * sum(x)
+ * from a second VPDPBUSD with ones, VCVTDQ2PS, VFMADD231PS, then the hsum.
+ * The lane integers equal the AVX2 emulation's, so the results are the same
+ * bits; this is the path the reference takes on such a host. */
+__attribute__((target("avx2,fma,avx512vnni,avx512vl")))
+static float q8_dot_vnni512(const int8_t *xr, const uint8_t *wr, const float *sc, int nb) {
+  const __m256i sign = _mm256_set1_epi8((char)0x80), ones = _mm256_set1_epi8(1);
+  __m256 acc = _mm256_setzero_ps();
+  for (int b = 0; b < nb; b++) {
+    __m256i x = _mm256_loadu_si256((const __m256i *)(xr + (int64_t)b * 32));
+    __m256i w = _mm256_loadu_si256((const __m256i *)(wr + (int64_t)b * 34 + 2));
+    __m256i dot = _mm256_dpbusd_epi32(_mm256_setzero_si256(), _mm256_xor_si256(w, sign), x);
+    __m256i sx = _mm256_dpbusd_epi32(_mm256_setzero_si256(), ones, x);
+    dot = _mm256_sub_epi32(dot, _mm256_slli_epi32(sx, 7));
+    acc = _mm256_fmadd_ps(_mm256_cvtepi32_ps(dot), _mm256_set1_ps(sc[b]), acc);
+  }
+  float l[8];
+  _mm256_storeu_ps(l, acc);
+  return hsum8(l);
+}
+
 /* One accumulator over whole-block sums (block-serial fma, or arm64's
  * mul + add): the int32 block sum is exact whatever order its products are
  * added in, so it is formed with VPMADDWD and an integer reduction. */
@@ -233,18 +261,18 @@ static float q8_dot_serial_avx2(const int8_t *xr, const uint8_t *wr, const float
 }
 #endif
 
-/* matMulQ8_0INT8SerialRange, quantize.go:390-458 (whole blocks only):
- * dst[i*N+j] = innerLoop(...) * inputScale */
-void sgo_matmul_q8_0_int8(float *dst, const uint8_t *w, const float *scales,
-                          const int8_t *x, const float *row_scale,
-                          int batch, int in_dim, int out_dim, int order) {
+/* matMulQ8_0INT8SerialRange, quantize.go:390-458 (whole blocks only), over
+ * output columns [c0, c1): dst[i*N+j] = innerLoop(...) * inputScale */
+static void matmul_cols(float *dst, const uint8_t *w, const float *scales, const int8_t *x,
+                        const float *row_scale, int batch, int in_dim, int out_dim, int order,
+                        int c0, int c1) {
   int nb = in_dim / 32;
   int64_t row_bytes = (int64_t)nb * 34;
   int simd = sgo_simd_level();
   int serial = order == SGO_ORDER_BLOCK_SERIAL || order == SGO_ORDER_ARM64;
   const int JT = 64; /* column tile: keeps a weight tile hot while rows stream */
-  for (int j0 = 0; j0 < out_dim; j0 += JT) {
-    int j1 = j0 + JT < out_dim ? j0 + JT : out_dim;
+  for (int j0 = c0; j0 < c1; j0 += JT) {
+    int j1 = j0 + JT < c1 ? j0 + JT : c1;
     for (int i = 0; i < batch; i++) {
       const int8_t *xr = x + (int64_t)i * in_dim;
       float s = row_scale[i];
@@ -254,6 +282,7 @@ void sgo_matmul_q8_0_int8(float *dst, const uint8_t *w, const float *scales,
         float v;
 #if SGO_X86
         if (simd && serial) v = q8_dot_serial_avx2(xr, wr, sc, nb, order == SGO_ORDER_BLOCK_SERIAL); else
+        if (simd == 2 && order == SGO_ORDER_VNNI) v = q8_dot_vnni512(xr, wr, sc, nb); else
         if (simd) v = q8_dot_avx2(xr, wr, sc, nb, order); else
 #endif
         v = q8_dot_scalar(xr, wr, sc, nb, order);
@@ -261,6 +290,46 @@ void sgo_matmul_q8_0_int8(float *dst, const uint8_t *w, const float *scales,
       }
     }
   }
+}
+
+typedef struct {
+  float *dst;
+  const uint8_t *w;
+  const float *scales;
+  const int8_t *x;
+  const float *row_scale;
+  int batch, in_dim, out_dim, order, c0, c1;
+} mm_job;
+
+static void *mm_worker(void *p) {
+  mm_job *j = (mm_job *)p;
+  matmul_cols(j->dst, j->w, j->scales, j->x, j->row_scale, j->batch, j->in_dim, j->out_dim, j->order, j->c0, j->c1);
+  return NULL;
+}
+
+/* With sgo_set_gemm_threads(n > 1), the output columns are split into
+ * contiguous chunks over n threads (matMulQ8_0INT8Tiled's column tasks,
+ * model_int8.go:258-346); every element is computed exactly as serially. */
+void sgo_matmul_q8_0_int8(float *dst, const uint8_t *w, const float *scales,
+                          const int8_t *x, const float *row_scale,
+                          int batch, int in_dim, int out_dim, int order) {
+  int n = g_gemm_threads;
+  if (n > 1 && out_dim >= 128) {
+    int chunk = (out_dim + n - 1) / n;
+    chunk = (chunk + 31) / 32 * 32;
+    mm_job jobs[256];
+    pthread_t th[256];
+    int used = 0;
+    for (int c0 = 0; c0 < out_dim && used < 256; c0 += chunk) {
+      jobs[used] = (mm_job){dst, w, scales, x, row_scale, batch, in_dim, out_dim, order, c0,
+                            c0 + chunk < out_dim ? c0 + chunk : out_dim};
+      pthread_create(&th[used], NULL, mm_worker, &jobs[used]);
+      used++;
+    }
+    for (int i = 0; i < used; i++) pthread_join(th[i], NULL);
+    return;
+  }
+  matmul_cols(dst, w, scales, x, row_scale, batch, in_dim, out_dim, order, 0, out_dim);
 }
 
 void sgo_block_sums(int32_t *out, const uint8_t *w, const int8_t *x,

@@ -139,10 +139,13 @@ typedef struct sgo_taps {
 int sgo_forward_taps(const sgo_model *m, const int32_t *tokens, const int32_t *seq_offsets,
                      int n_seq, int target_dim, float *out, int order, int n_threads, const sgo_taps *taps);
 
-/* 1 when the AVX2+FMA fast paths are in use on this host (results are
- * bit-identical to the scalar definitions either way). */
+/* 1 when the AVX2+FMA fast paths are in use on this host, 2 when the VNNI
+ * order also runs on AVX-512 VNNI (results are bit-identical to the scalar
+ * definitions either way). */
 int sgo_simd_level(void);
 void sgo_force_scalar(int on);
+/* Threads per GEMM call (column chunks); 1 = serial (the default). */
+void sgo_set_gemm_threads(int n);
 
 /* Brute-force vector search (search/brute), sg_oracle_search.c.
  * Storage modes: QuantizationMode, search/brute/quant.go:8-15. */

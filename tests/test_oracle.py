@@ -193,6 +193,23 @@ def test_matmul_pins_catch_single_mistakes():
             assert caught, f"{o}: mutation {mcfg} passes every pin"
 
 
+def test_matmul_threaded_columns_equal_serial(oracle):
+    """Column chunks over threads (the reference's matMulQ8_0INT8Tiled tasks)
+    give every element the serial bits, in all four orders."""
+    lib = oracle.load()
+    rng = np.random.default_rng(17)
+    raw, _, _ = _rand_q8(rng, 1152, 768, 1e-4, 1e-3)
+    x = rng.integers(-127, 128, size=(5, 768), dtype=np.int8)
+    for order in (0, 1, 2, 3):
+        serial = oracle.matmul(raw, x, np.float32(0.02), 1152, order)
+        lib.sgo_set_gemm_threads(7)
+        try:
+            threaded = oracle.matmul(raw, x, np.float32(0.02), 1152, order)
+        finally:
+            lib.sgo_set_gemm_threads(1)
+        assert np.array_equal(serial.view(np.uint32), threaded.view(np.uint32)), order
+
+
 def test_matmul_simd_equals_scalar(oracle):
     """The AVX2 speed-up paths must give the scalar definition's bits."""
     lib = oracle.load()
