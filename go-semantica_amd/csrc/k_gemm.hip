@@ -450,6 +450,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor, gfx9 family
+constexpr float kMagic = 12582912.0f;   // 1.5 * 2^23
+constexpr int kMagicBits = 0x4B400000;  // its bit pattern
 
 // f(integral_constant<int, I>) for I = I0 .. N-1, unrolled at compile time.
 template <int I, int N, typename F>
@@ -649,7 +651,16 @@ __global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_i8(
   for (int tn = 0; tn < TN; tn++)
 #pragma unroll
     for (int r = 0; r < 16; r++) acc[0][tn][r] = 0.0f;
-  const i32x16_t zero = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  // int32 -> float without v_cvt_f32_i32 (a half-rate VALU op on gfx950): the
+  // MFMA starts from the bit pattern of 1.5 * 2^23 in every lane, so its int32
+  // result read as a float is exactly 12582912 + P_b (|P_b| <= 32 * 128 * 127
+  // < 2^22 keeps the exponent at 23 and the mantissa exact), and one
+  // full-rate subtraction gives float(P_b) exactly.  The asm keeps the
+  // constant in registers (no per-use rematerialisation).
+  i32x16_t bias;
+#pragma unroll
+  for (int r = 0; r < 16; r++) bias[r] = kMagicBits;
+  asm volatile("" : "+v"(bias));
   auto step = [&](auto stc, int b) {
     constexpr int ST = decltype(stc)::value;
     wait_vmcnt<(STAGES - 2) * CPB>();
@@ -661,9 +672,10 @@ __global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_i8(
     for (int tn = 0; tn < TN; tn++) {
       const i32x4_t fw = *reinterpret_cast<const i32x4_t*>(lds + rw_f + ST * W_BYTES + tn * 512);
       const float d = *reinterpret_cast<const float*>(lds + rd + ST * S_BYTES + tn * 128);
-      const i32x16_t pp = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fw, zero, 0, 0, 0);
+      const i32x16_t pp = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fw, bias, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 16; r++) acc[0][tn][r] = __builtin_fmaf((float)pp[r], d, acc[0][tn][r]);
+      for (int r = 0; r < 16; r++)
+        acc[0][tn][r] = __builtin_fmaf(__int_as_float(pp[r]) - kMagic, d, acc[0][tn][r]);
     }
   };
   static_for<0, STAGES - 1>([&](auto ic) { issue(min((int)decltype(ic)::value, nb - 1), decltype(ic)::value); });
