@@ -4,11 +4,13 @@ one MI355X.  Prints ONE JSON line.
 
 A step is one batched forward (sg_forward_device) over the 64 packed
 sequences, token IDs already resident in HBM, embeddings left in HBM.
-`value` is embeddings/sec over the K timed steps, which run uninstrumented.
-Then the same K steps run again with a HIP event pair around every launch (on
-the library's stream): the per-kernel-class breakdown and `roofline` come
-from that pass (event records between launches cost ~10% of the step, so
-they stay out of the timed region).  `roofline` is the Q8_0 GEMM (the
+`value` is embeddings/sec over the K timed steps, which run uninstrumented
+(the library runs a batch this size as two sequence groups on two streams,
+whose kernels overlap).  Then the same K steps run again with a HIP event
+pair around every launch: the profiled forward runs as one group on the
+library's stream, so every kernel is timed alone, and the per-kernel-class
+breakdown and `roofline` come from that pass (event records between launches
+cost ~10% of the step, so they stay out of the timed region).  `roofline` is the Q8_0 GEMM (the
 dominant kernel class): algorithmic int8 ops (2*M*N*K per launch) over the
 event-measured average launch time, against MI355X's dense int8 peak.  `traffic` is read from profiles/gemm_traffic.json (FETCH_SIZE and
 WRITE_SIZE counter passes, scaled by a copy kernel of known size).

@@ -378,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void k_rmsnorm(float* dst, const float* s
 
 // h = RMSNorm(o; w_post) + h (model_int8.go:203-210 / :225-232), then
 // xn = RMSNorm(h; w_next) -- the next pre-norm (:194/:216) or output_norm (:236).
-// Float4 row layout (sg_rmsnorm8_f4): NC chunks of 32 elements per row.
+// Float4 row layout (sg_post_res_norm_row): NC chunks of 32 elements per row.
 template <int NC>
 __global__ __launch_bounds__(kThreads) void k_post_res_norm(const float* __restrict__ o, float* __restrict__ h,
                                                             const float* __restrict__ w_post,
@@ -390,34 +390,11 @@ __global__ __launch_bounds__(kThreads) void k_post_res_norm(const float* __restr
   __shared__ __attribute__((aligned(16))) float tiles[kThreads / SG_WAVE][8 * 40];
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7, r = (threadIdx.x >> 3) & 7;
-  float* tile = tiles[threadIdx.x / SG_WAVE];
   const bool valid = row < T;
   float m = 0.0f;
-  if (valid) {
-    f32x4_t x[NC];
-    const f32x4_t* orow = reinterpret_cast<const f32x4_t*>(o + (int64_t)row * D) + j;
-#pragma unroll
-    for (int c = 0; c < NC; c++) x[c] = orow[8 * c];
-    if (w_post) sg_rmsnorm8_f4<NC>(x, w_post, tile, r, j, eps);
-    f32x4_t* hr = reinterpret_cast<f32x4_t*>(h + (int64_t)row * D) + j;
-#pragma unroll
-    for (int c = 0; c < NC; c++) {
-      const f32x4_t hv = hr[8 * c];
-#pragma unroll
-      for (int t = 0; t < 4; t++) x[c][t] = x[c][t] + hv[t];
-      hr[8 * c] = x[c];
-    }
-    if (w_next) sg_rmsnorm8_f4<NC>(x, w_next, tile, r, j, eps);
-    if (xn) {
-      f32x4_t* yr = reinterpret_cast<f32x4_t*>(xn + (int64_t)row * D) + j;
-#pragma unroll
-      for (int c = 0; c < NC; c++) yr[8 * c] = x[c];
-    }
-#pragma unroll
-    for (int c = 0; c < NC; c++)
-#pragma unroll
-      for (int t = 0; t < 4; t++) m = fmaxf(m, fabsf(x[c][t]));
-  }
+  if (valid)
+    m = sg_post_res_norm_row<NC>(o + (int64_t)row * D, h + (int64_t)row * D, w_post, w_next, eps,
+                                 xn ? xn + (int64_t)row * D : nullptr, tiles[threadIdx.x / SG_WAVE], r, j);
   if (amax) {
     m = sg_max8(m);
     const int r0 = blockIdx.x * kRowsPerBlock;

@@ -287,3 +287,41 @@ __device__ __forceinline__ void sg_rmsnorm8_f4(f32x4_t (&x)[NC], const float* __
   }
 }
 
+
+// One row of the residual post-norm (model_int8.go:203-210 / :225-232):
+// h = RMSNorm(o; w_post) + h, then xn = RMSNorm(h; w_next), the next pre-norm
+// (:194 / :216) or output_norm (:236).  An 8-lane group owns the row on the
+// float4 layout (lane j: elements 32c + 4j .. + 3); tile is the wave's
+// 8 x 40-float transpose tile and r the row's slot in it.  xn is stored when
+// xrow is non-null; returns this lane's max|xn| (max|h| without w_next).
+template <int NC>
+__device__ __forceinline__ float sg_post_res_norm_row(const float* __restrict__ orow, float* __restrict__ hrow,
+                                                      const float* __restrict__ w_post,
+                                                      const float* __restrict__ w_next, float eps,
+                                                      float* __restrict__ xrow, float* tile, int r, int j) {
+  f32x4_t x[NC];
+  const f32x4_t* op = reinterpret_cast<const f32x4_t*>(orow) + j;
+#pragma unroll
+  for (int c = 0; c < NC; c++) x[c] = op[8 * c];
+  if (w_post) sg_rmsnorm8_f4<NC>(x, w_post, tile, r, j, eps);
+  f32x4_t* hp = reinterpret_cast<f32x4_t*>(hrow) + j;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const f32x4_t hv = hp[8 * c];
+#pragma unroll
+    for (int t = 0; t < 4; t++) x[c][t] = x[c][t] + hv[t];
+    hp[8 * c] = x[c];
+  }
+  if (w_next) sg_rmsnorm8_f4<NC>(x, w_next, tile, r, j, eps);
+  if (xrow) {
+    f32x4_t* yp = reinterpret_cast<f32x4_t*>(xrow) + j;
+#pragma unroll
+    for (int c = 0; c < NC; c++) yp[8 * c] = x[c];
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; c++)
+#pragma unroll
+    for (int t = 0; t < 4; t++) m = fmaxf(m, fabsf(x[c][t]));
+  return m;
+}

@@ -235,6 +235,47 @@ def test_device_path_errors_match_host_path(tiny_gpu):
         assert (eh.value.code, eh.value.message) == (ed.value.code, ed.value.message) == (code, msg)
     assert tiny_gpu.forward_batch([[3, 4, 5]], 768).shape == (1, 768)
 
+def test_sequence_groups_match_one_stream(tiny_gpu):
+    """From 8192 tokens the forward runs as two contiguous sequence groups, each on
+    its own stream, so the kernels of the two groups overlap on the GPU.  Each
+    sequence's arithmetic is unchanged.  Ragged batches of 8k to 35k tokens are
+    bit-identical to the same batch on one stream (the profiled path runs one
+    group).  Out-of-range tokens in two later groups report the
+    earlier one, as the reference's request order does (api.go:286-292), on both
+    the host and the device entry points."""
+    import torch
+    from semantica_gpu import SemanticaError, _lib
+    rng = np.random.default_rng(11)
+    for n, hi in ((10, 2048), (13, 2048), (60, 1100), (200, 300)):
+        lens = rng.integers(1, hi + 1, size=n)
+        off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        T = int(off[-1])
+        toks = rng.integers(0, 4096, size=T).astype(np.int32)
+        say(f"sequence groups: {n} sequences, {T} tokens")
+        y = tiny_gpu.forward_packed(toks, off, 768)
+        tiny_gpu.profile_enable(True)
+        try:
+            y1 = tiny_gpu.forward_packed(toks, off, 768)
+        finally:
+            tiny_gpu.profile_enable(False)
+        assert np.array_equal(y.view(np.uint32), y1.view(np.uint32))
+        if T < 16384:
+            continue
+        bad = toks.copy()
+        i1, i2 = int(n * 0.6), int(n * 0.9)
+        bad[off[i2]] = 5000
+        bad[off[i1 + 1] - 1] = 4096 + i1
+        with pytest.raises(SemanticaError) as eh:
+            tiny_gpu.forward_packed(bad, off, 768)
+        d_tok = torch.from_numpy(bad).cuda()
+        out = torch.empty((n, 768), dtype=torch.float32, device="cuda")
+        with pytest.raises(SemanticaError) as ed:
+            tiny_gpu.forward_device(d_tok.data_ptr(), off, 768, out.data_ptr())
+        say(f"  errors at sequences {i1} and {i2}: host '{eh.value.message}' device '{ed.value.message}'")
+        expect = (_lib.SG_ERR_TOKEN, f"token ID out of range: {4096 + i1}")
+        assert (eh.value.code, eh.value.message) == (ed.value.code, ed.value.message) == expect
+
+
 def _teacher_forced(gpu, om, toks, off, dim, n_layers, tag, seam_layers=(), threads=16):
     """Teacher-forced parity at every layer.  The GPU's per-layer trace
     (sg_forward_trace) gives each layer's Q|K|V GEMM output, attention output
