@@ -153,20 +153,41 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
           stg[u];
   };
 
-  // S^T subtile st (keys 16st..16st+15 of the tile x 16 queries), scaled by
-  // 64: lane holds query ln and keys 16st + 4g4 + r in register r.
-  auto scores = [&](int st, const _Float16* kb) {
-    f32x4_t acc = {0, 0, 0, 0};
+  // S^T subtiles 0 and 1 of a tile (keys 0..15 and 16..31 x 16 queries),
+  // scaled by 64: lane holds query ln and keys 16st + 4g4 + r in register r.
+  // Each subtile's accumulator takes ah.bh, ah.bl, al.bh of k-step ks in that
+  // order.  Reads run half a step ahead: subtile 1's K fragments of ks are
+  // read before subtile 0's MFMAs of ks, subtile 0's of ks + 1 before
+  // subtile 1's MFMAs (the scheduling groups pin that order), so each read's
+  // latency hides behind three MFMAs with two fragment pairs live.
+  auto scores2 = [&](const _Float16* kb, f32x4_t& a0, f32x4_t& a1) {
+    const _Float16* p0 = kb + ln * kKStride + 8 * g4;
+    auto rd = [&](int st, int ks, half8_t& h, half8_t& l) {
+      h = *reinterpret_cast<const half8_t*>(p0 + 16 * st * kKStride + 32 * ks);
+      l = *reinterpret_cast<const half8_t*>(p0 + (kBK + 16 * st) * kKStride + 32 * ks);
+    };
+    a0 = f32x4_t{0, 0, 0, 0};
+    a1 = f32x4_t{0, 0, 0, 0};
+    half8_t h0, l0, h1, l1;
+    rd(0, 0, h0, l0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
 #pragma unroll
     for (int ks = 0; ks < kHD / 32; ks++) {
-      const half8_t ah = *reinterpret_cast<const half8_t*>(kb + (16 * st + ln) * kKStride + 32 * ks + 8 * g4);
-      const half8_t al =
-          *reinterpret_cast<const half8_t*>(kb + (kBK + 16 * st + ln) * kKStride + 32 * ks + 8 * g4);
-      acc = mfma16(ah, bqh[ks], acc);
-      acc = mfma16(ah, bql[ks], acc);
-      acc = mfma16(al, bqh[ks], acc);
+      rd(1, ks, h1, l1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      a0 = mfma16(h0, bqh[ks], a0);
+      a0 = mfma16(h0, bql[ks], a0);
+      a0 = mfma16(l0, bqh[ks], a0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+      if (ks + 1 < kHD / 32) {
+        rd(0, ks + 1, h0, l0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      a1 = mfma16(h1, bqh[ks], a1);
+      a1 = mfma16(h1, bql[ks], a1);
+      a1 = mfma16(l1, bqh[ks], a1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
     }
-    return acc;
   };
   auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
   // Pass-1 max over one tile's scores (keys past S only in a sequence's last tile).
@@ -200,15 +221,29 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
       }
     }
   };
-  // O^T += V^T P^T for one tile.
+  // O^T += V^T P^T for one tile, the V^T fragments of dim tile mt + 2 read
+  // from LDS while the MFMAs of mt run.
   auto pv = [&](f32x4_t* o, const _Float16* vb, const half8_t& ph, const half8_t& pl) {
+    const _Float16* p0 = vb + ln * kVStride + 8 * g4;
+    half8_t fr[3][2];  // [buffer][hi, lo]
+    auto rd = [&](int mt, half8_t(&f)[2]) {
+      f[0] = *reinterpret_cast<const half8_t*>(p0 + 16 * mt * kVStride);
+      f[1] = *reinterpret_cast<const half8_t*>(p0 + (kHD + 16 * mt) * kVStride);
+    };
+    rd(0, fr[0]);
+    rd(1, fr[1]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
     for (int mt = 0; mt < kHD / 16; mt++) {
-      const half8_t ah = *reinterpret_cast<const half8_t*>(vb + (16 * mt + ln) * kVStride + 8 * g4);
-      const half8_t al = *reinterpret_cast<const half8_t*>(vb + (kHD + 16 * mt + ln) * kVStride + 8 * g4);
-      o[mt] = mfma16(ah, ph, o[mt]);
-      o[mt] = mfma16(ah, pl, o[mt]);
-      o[mt] = mfma16(al, ph, o[mt]);
+      if (mt + 2 < kHD / 16) {
+        rd(mt + 2, fr[(mt + 2) % 3]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      const half8_t(&f)[2] = fr[mt % 3];
+      o[mt] = mfma16(f[0], ph, o[mt]);
+      o[mt] = mfma16(f[0], pl, o[mt]);
+      o[mt] = mfma16(f[1], ph, o[mt]);
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
     }
   };
 
@@ -328,8 +363,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
         else
           load_v(0);  // pass 2's first tile
         if (active) {
-          sr[t][0] = scores(0, kbuf(t & 1));
-          sr[t][1] = scores(1, kbuf(t & 1));
+          scores2(kbuf(t & 1), sr[t][0], sr[t][1]);
           m = tile_max(m, kt, sr[t][0], sr[t][1]);
         }
       }
@@ -355,7 +389,11 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
       store_k(kbuf(0));
       __syncthreads();
       if (kt + kBK < S) load_k(kt + kBK);  // in flight during the MFMAs
-      if (active) m = tile_max(m, kt, scores(0, kbuf(0)), scores(1, kbuf(0)));
+      if (active) {
+        f32x4_t a0, a1;
+        scores2(kbuf(0), a0, a1);
+        m = tile_max(m, kt, a0, a1);
+      }
     }
     m = fmaxf(m, __shfl_xor(m, 16));
     m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
@@ -368,7 +406,11 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
     for (int kt = 0; kt < S; kt += kBK) {
       load_v(kt);  // in flight during the score MFMAs
       half8_t ph, pl;
-      if (active) weights(kt, scores(0, kbuf(0)), scores(1, kbuf(0)), m, lsum, ph, pl);
+      if (active) {
+        f32x4_t a0, a1;
+        scores2(kbuf(0), a0, a1);
+        weights(kt, a0, a1, m, lsum, ph, pl);
+      }
       store_v(vbuf(0));
       __syncthreads();  // V^T tile staged; K tile free
       const bool more = kt + kBK < S;
