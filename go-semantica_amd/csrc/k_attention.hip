@@ -68,34 +68,129 @@ __device__ __forceinline__ f32x4_t mfma16(half8_t a, half8_t b, f32x4_t c) {
 // the eight S^T registers a lane holds per 32-key tile the B operand of one
 // O^T += V^T P^T step.
 
-// QPRE: Q arrives as the QKV GEMM's fp32 output and each wave applies
-// attn_q_norm and RoPE to its 16 rows itself (the arithmetic of
-// k_qknorm_rope_split, so the operands are bit-identical), which saves writing
-// Q's hi/lo operands and reading them back.
-//
-// RS (every sequence of the launch at most kRegKeys keys): pass 1 keeps each
-// lane's raw scores in registers (8 per 32-key tile, 128 VGPRs at 512 keys)
-// and pass 2 reads them back instead of recomputing S^T, so K is streamed
-// once and a third of the MFMAs and LDS reads go away; pass 1 streams only K
-// and pass 2 only V^T, each through two LDS buffers (one barrier per tile).
-// The values are the ones pass 2 would recompute, so the output is identical.
 constexpr int kRegTiles = sgk::kAttnRegKeys / kBK;
 constexpr int kKBuf = 2 * kBK * kKStride;  // halves of one K tile buffer [hi/lo][key][dim]
 constexpr int kVBuf = 2 * kHD * kVStride;  // halves of one V^T tile buffer [hi/lo][dim][key]
 
-template <bool QPRE, bool RS>
+// Q^T as the B operand of one wave's 16 (head, query) rows: lane (query ln,
+// group g4), k-step ks holds dims 32ks + 8g4 .. + 7 of row qr, scaled by 8
+// and split hi/lo.  QPRE: Q arrives as the QKV GEMM's fp32 output and the wave
+// applies attn_q_norm and RoPE to its 16 rows itself (the arithmetic of
+// k_qknorm_rope_split, so the operands are bit-identical), which saves writing
+// Q's hi/lo operands and reading them back; tile: the wave's 16 x 40 floats
+// of LDS for the norm.  Otherwise Q arrives split (qh, ql).
+template <bool QPRE>
+__device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bql)[kHD / 32],
+                                          const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq,
+                                          const sg_attn_qpre& qp, int qr, int head, int ln, int g4, int lane,
+                                          float* tile) {
+  if constexpr (QPRE) {
+    // Every global load (the row's position, Q, the norm weights, the RoPE
+    // table rows) is issued up front, so the prologue pays one memory latency
+    // instead of one per phase; the registers are free this early.
+    // Lane (ln, g4) holds elements e = 32ks + 8g4 + t of row ln.
+    const int pos = qp.row_pos[qr];
+    float x[kHD / 32][8], wq[kHD / 32][8];
+    const float* src = qp.q + (int64_t)qr * qp.ldq + head * kHD + 8 * g4;
+#pragma unroll
+    for (int ks = 0; ks < kHD / 32; ks++) {
+      *reinterpret_cast<f32x4_t*>(&x[ks][0]) = *reinterpret_cast<const f32x4_t*>(src + 32 * ks);
+      *reinterpret_cast<f32x4_t*>(&x[ks][4]) = *reinterpret_cast<const f32x4_t*>(src + 32 * ks + 4);
+    }
+    if (qp.w) {
+#pragma unroll
+      for (int ks = 0; ks < kHD / 32; ks++) {
+        *reinterpret_cast<f32x4_t*>(&wq[ks][0]) = *reinterpret_cast<const f32x4_t*>(qp.w + 32 * ks + 8 * g4);
+        *reinterpret_cast<f32x4_t*>(&wq[ks][4]) = *reinterpret_cast<const f32x4_t*>(qp.w + 32 * ks + 8 * g4 + 4);
+      }
+    }
+    float cv[kHD / 64][8], sv[kHD / 64][8];
+    const float* cr = qp.cos_t + (int64_t)pos * (kHD / 2) + 8 * g4;
+    const float* sr = qp.sin_t + (int64_t)pos * (kHD / 2) + 8 * g4;
+#pragma unroll
+    for (int ks = 0; ks < kHD / 64; ks++) {
+      *reinterpret_cast<f32x4_t*>(&cv[ks][0]) = *reinterpret_cast<const f32x4_t*>(cr + 32 * ks);
+      *reinterpret_cast<f32x4_t*>(&cv[ks][4]) = *reinterpret_cast<const f32x4_t*>(cr + 32 * ks + 4);
+      *reinterpret_cast<f32x4_t*>(&sv[ks][0]) = *reinterpret_cast<const f32x4_t*>(sr + 32 * ks);
+      *reinterpret_cast<f32x4_t*>(&sv[ks][4]) = *reinterpret_cast<const f32x4_t*>(sr + 32 * ks + 4);
+    }
+    if (qp.w) {
+      // RMSNorm's sum of squares in the AVX2 lane order (sg_rmsnorm8): lane v
+      // of a row chains element 8i + v over i.  Element e sits at i = 4ks + g4,
+      // v = t here, so each 32-element chunk goes through the wave's 16 x
+      // 40-float LDS tile; lane (row rA or rA + 8, v) then reads the chunk's
+      // elements 8k + v, k = 0..3, in order.
+      const int v = lane & 7, rA = lane >> 3;
+      float accA = 0.0f, accB = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < kHD / 32; ks++) {
+        asm volatile("" ::: "memory");
+        *reinterpret_cast<f32x4_t*>(tile + ln * 40 + 8 * g4) = f32x4_t{x[ks][0], x[ks][1], x[ks][2], x[ks][3]};
+        *reinterpret_cast<f32x4_t*>(tile + ln * 40 + 8 * g4 + 4) = f32x4_t{x[ks][4], x[ks][5], x[ks][6], x[ks][7]};
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const float a = tile[rA * 40 + 8 * k + v];
+          accA = __builtin_fmaf(a, a, accA);
+          const float b = tile[(rA + 8) * 40 + 8 * k + v];
+          accB = __builtin_fmaf(b, b, accB);
+        }
+      }
+      asm volatile("" ::: "memory");
+      const float invA = 1.0f / sg_sqrt(sg_hsum8(accA) / (float)kHD + qp.eps);
+      const float invB = 1.0f / sg_sqrt(sg_hsum8(accB) / (float)kHD + qp.eps);
+      const float iA = __shfl(invA, 8 * (ln & 7)), iB = __shfl(invB, 8 * (ln & 7));
+      const float inv = ln < 8 ? iA : iB;
+#pragma unroll
+      for (int ks = 0; ks < kHD / 32; ks++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          const float u = x[ks][t] * inv;
+          x[ks][t] = u * wq[ks][t];
+        }
+    }
+    // RoPE (rope_cache.go:85-104): pairs (e, e + 128) are chunks ks and ks + 4
+    // of the same lane and slot.
+#pragma unroll
+    for (int ks = 0; ks < kHD / 64; ks++) {
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const float v0 = x[ks][t], v1 = x[ks + kHD / 64][t];
+        const float a = v0 * cv[ks][t], b = v1 * sv[ks][t], cc = v0 * sv[ks][t], dd = v1 * cv[ks][t];
+        x[ks][t] = a - b;
+        x[ks + kHD / 64][t] = cc + dd;
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < kHD / 32; ks++)
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const hl16 sp = split_f16(x[ks][t] * kQKScale);
+        bqh[ks][t] = sp.hi;
+        bql[ks][t] = sp.lo;
+      }
+  } else {
+    const int64_t qo = (int64_t)qr * ldq + head * kHD + 8 * g4;
+#pragma unroll
+    for (int ks = 0; ks < kHD / 32; ks++) {
+      bqh[ks] = *reinterpret_cast<const half8_t*>(qh + qo + 32 * ks);
+      bql[ks] = *reinterpret_cast<const half8_t*>(ql + qo + 32 * ks);
+    }
+  }
+}
+
+// Sequences longer than kRegTiles tiles: pass 2 recomputes S^T.  One K and
+// one V^T buffer, tiles staged through registers.
+template <bool QPRE>
 __global__ __launch_bounds__(kNT, 2) void k_attn(
     const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
     const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vt, int ldvt, float* __restrict__ out, int ldo, const int32_t* __restrict__ seq_off,
     const int32_t* __restrict__ voff, const sg_item* __restrict__ items, int G, float sscale,
     float* __restrict__ amax, sg_attn_qpre qp) {
-  // Two-pass: one K and one V^T buffer.  RS: two K buffers in pass 1, two V^T
-  // buffers in pass 2, over the same memory.
-  constexpr int kLdsHalves = RS ? (kKBuf > kVBuf ? 2 * kKBuf : 2 * kVBuf) : kKBuf + kVBuf;
-  __shared__ __attribute__((aligned(16))) _Float16 lds[kLdsHalves];
+  __shared__ __attribute__((aligned(16))) _Float16 lds[kKBuf + kVBuf];
   __shared__ float red[kWaves];
-  auto kbuf = [&](int b) { return lds + b * kKBuf; };
-  auto vbuf = [&](int b) { return RS ? lds + b * kVBuf : lds + kKBuf; };
+  auto kbuf = [&](int) { return lds; };
+  auto vbuf = [&](int) { return lds + kKBuf; };
 
   const sg_item it = items[blockIdx.x];
   const int kvh = blockIdx.y;
@@ -252,138 +347,12 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
   // with max exactly.  Keys past S only occur in a sequence's last tile.
   float m = -INFINITY;
   load_k(0);  // in flight while Q is prepared
-  if constexpr (QPRE) {
-    // Lane (ln, g4) holds elements e = 32ks + 8g4 + t of row ln.
-    float x[kHD / 32][8];
-    const float* src = qp.q + (int64_t)qr * qp.ldq + head * kHD + 8 * g4;
-#pragma unroll
-    for (int ks = 0; ks < kHD / 32; ks++) {
-      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src + 32 * ks);
-      const f32x4_t b = *reinterpret_cast<const f32x4_t*>(src + 32 * ks + 4);
-#pragma unroll
-      for (int t = 0; t < 4; t++) {
-        x[ks][t] = a[t];
-        x[ks][4 + t] = b[t];
-      }
-    }
-    if (qp.w) {
-      // RMSNorm's sum of squares in the AVX2 lane order (sg_rmsnorm8): lane v
-      // of a row chains element 8i + v over i.  Element e sits at i = 4ks + g4,
-      // v = t here, so each 32-element chunk goes through a 16 x 40-float LDS
-      // tile of this wave (inside K buffer 0, which nothing uses before the
-      // first barrier below); lane (row rA or rA + 8, v) then reads the chunk's
-      // elements 8k + v, k = 0..3, in order.
-      float* tile = reinterpret_cast<float*>(lds) + w * (16 * 40);
-      const int v = lane & 7, rA = lane >> 3;
-      float accA = 0.0f, accB = 0.0f;
-#pragma unroll
-      for (int ks = 0; ks < kHD / 32; ks++) {
-        asm volatile("" ::: "memory");
-        *reinterpret_cast<f32x4_t*>(tile + ln * 40 + 8 * g4) = f32x4_t{x[ks][0], x[ks][1], x[ks][2], x[ks][3]};
-        *reinterpret_cast<f32x4_t*>(tile + ln * 40 + 8 * g4 + 4) = f32x4_t{x[ks][4], x[ks][5], x[ks][6], x[ks][7]};
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const float a = tile[rA * 40 + 8 * k + v];
-          accA = __builtin_fmaf(a, a, accA);
-          const float b = tile[(rA + 8) * 40 + 8 * k + v];
-          accB = __builtin_fmaf(b, b, accB);
-        }
-      }
-      asm volatile("" ::: "memory");
-      const float invA = 1.0f / sg_sqrt(sg_hsum8(accA) / (float)kHD + qp.eps);
-      const float invB = 1.0f / sg_sqrt(sg_hsum8(accB) / (float)kHD + qp.eps);
-      const float iA = __shfl(invA, 8 * (ln & 7)), iB = __shfl(invB, 8 * (ln & 7));
-      const float inv = ln < 8 ? iA : iB;
-#pragma unroll
-      for (int ks = 0; ks < kHD / 32; ks++) {
-        const f32x4_t wa = *reinterpret_cast<const f32x4_t*>(qp.w + 32 * ks + 8 * g4);
-        const f32x4_t wb = *reinterpret_cast<const f32x4_t*>(qp.w + 32 * ks + 8 * g4 + 4);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-          const float u = x[ks][t] * inv;
-          x[ks][t] = u * wa[t];
-          const float u2 = x[ks][4 + t] * inv;
-          x[ks][4 + t] = u2 * wb[t];
-        }
-      }
-    }
-    // RoPE (rope_cache.go:85-104): pairs (e, e + 128) are chunks ks and ks + 4
-    // of the same lane and slot.
-    const int pos = qp.row_pos[qr];
-    const float* cr = qp.cos_t + (int64_t)pos * (kHD / 2) + 8 * g4;
-    const float* sr = qp.sin_t + (int64_t)pos * (kHD / 2) + 8 * g4;
-#pragma unroll
-    for (int ks = 0; ks < kHD / 64; ks++) {
-      float cv[8], sv[8];
-      *reinterpret_cast<f32x4_t*>(cv) = *reinterpret_cast<const f32x4_t*>(cr + 32 * ks);
-      *reinterpret_cast<f32x4_t*>(cv + 4) = *reinterpret_cast<const f32x4_t*>(cr + 32 * ks + 4);
-      *reinterpret_cast<f32x4_t*>(sv) = *reinterpret_cast<const f32x4_t*>(sr + 32 * ks);
-      *reinterpret_cast<f32x4_t*>(sv + 4) = *reinterpret_cast<const f32x4_t*>(sr + 32 * ks + 4);
-#pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const float v0 = x[ks][t], v1 = x[ks + kHD / 64][t];
-        const float a = v0 * cv[t], b = v1 * sv[t], cc = v0 * sv[t], dd = v1 * cv[t];
-        x[ks][t] = a - b;
-        x[ks + kHD / 64][t] = cc + dd;
-      }
-    }
-#pragma unroll
-    for (int ks = 0; ks < kHD / 32; ks++)
-#pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const hl16 sp = split_f16(x[ks][t] * kQKScale);
-        bqh[ks][t] = sp.hi;
-        bql[ks][t] = sp.lo;
-      }
-  } else {
-    const int64_t qo = (int64_t)qr * ldq + head * kHD + 8 * g4;
-#pragma unroll
-    for (int ks = 0; ks < kHD / 32; ks++) {
-      bqh[ks] = *reinterpret_cast<const half8_t*>(qh + qo + 32 * ks);
-      bql[ks] = *reinterpret_cast<const half8_t*>(ql + qo + 32 * ks);
-    }
-  }
+  q_operand<QPRE>(bqh, bql, qh, ql, ldq, qp, qr, head, ln, g4, lane, reinterpret_cast<float*>(lds) + w * (16 * 40));
   f32x4_t o[kHD / 16];
 #pragma unroll
   for (int mt = 0; mt < kHD / 16; mt++) o[mt] = f32x4_t{0, 0, 0, 0};
   float lsum = 0.0f;
-  if constexpr (RS) {
-    f32x4_t sr[kRegTiles][2];  // raw scores of tile t, subtiles 0 and 1
-    __syncthreads();            // the Q prologue's LDS tiles are free
-#pragma unroll
-    for (int t = 0; t < kRegTiles; t++) {
-      const int kt = t * kBK;
-      if (kt < S) {
-        // Buffer t & 1 was last read in tile t - 2, before the previous barrier.
-        store_k(kbuf(t & 1));
-        __syncthreads();
-        if (kt + kBK < S)
-          load_k(kt + kBK);  // in flight during the MFMAs
-        else
-          load_v(0);  // pass 2's first tile
-        if (active) {
-          scores2(kbuf(t & 1), sr[t][0], sr[t][1]);
-          m = tile_max(m, kt, sr[t][0], sr[t][1]);
-        }
-      }
-    }
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
-    __syncthreads();  // the K buffers are free (the V^T buffers overlay them)
-#pragma unroll
-    for (int t = 0; t < kRegTiles; t++) {
-      const int kt = t * kBK;
-      if (kt < S) {
-        half8_t ph, pl;  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
-        if (active) weights(kt, sr[t][0], sr[t][1], m, lsum, ph, pl);
-        store_v(vbuf(t & 1));
-        __syncthreads();
-        if (kt + kBK < S) load_v(kt + kBK);  // in flight during the P.V MFMAs
-        if (active) pv(o, vbuf(t & 1), ph, pl);
-      }
-    }
-  } else {
+  {
     for (int kt = 0; kt < S; kt += kBK) {
       __syncthreads();  // every wave is done with the previous tile
       store_k(kbuf(0));
@@ -420,6 +389,292 @@ __global__ __launch_bounds__(kNT, 2) void k_attn(
       __syncthreads();             // K tile staged; V^T tile free
     }
   }
+  lsum = lsum + __shfl_xor(lsum, 16);
+  lsum = lsum + __shfl_xor(lsum, 32);
+  const float f = (1.0f / lsum) * kPUnscale;
+
+  // O^T tile mt: lane holds query ln, dims 16mt + 4g4 + r.
+  float mx = 0.0f;
+  if (qvalid) {
+    float* op = out + (int64_t)(r0 + qrow) * ldo + head * kHD + 4 * g4;
+#pragma unroll
+    for (int mt = 0; mt < kHD / 16; mt++) {
+      f32x4_t y;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        y[j] = o[mt][j] * f;
+        mx = fmaxf(mx, fabsf(y[j]));
+      }
+      *reinterpret_cast<f32x4_t*>(op + 16 * mt) = y;
+    }
+  }
+  if (amax) {  // all chunks of a workgroup belong to one sequence
+    mx = sg_wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    if (tid == 0) {
+      float mm = red[0];
+#pragma unroll
+      for (int i = 1; i < kWaves; i++) mm = fmaxf(mm, red[i]);
+      sg_atomic_max_nonneg(amax + it.seq, mm);
+    }
+  }
+}
+
+// wait_vmcnt<N>: this wave's vector memory operations older than the last N
+// have completed, and its LDS reads too (s_waitcnt vmcnt(N) lgkmcnt(0)).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+}
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// One 64-lane buffer_load_dwordx4 ... lds (1 KB to LDS at lds_addr + 16 *
+// lane, lane l reading rsrc.base + voff_l + soff), issued from inline
+// assembly.  The compiler then sees no LDS write, so it inserts no wait in
+// front of the fragment reads of the other ring stages (it cannot tell them
+// apart from the copies once several are in flight); the kernel orders copies
+// and reads itself with s_waitcnt vmcnt + s_barrier.  M0 (the copy's LDS base)
+// is saved and restored around it.
+__device__ __forceinline__ void lds_copy16(uint32_t lds_addr, uint32_t voff, i32x4_t rsrc, uint32_t soff) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+      : "memory");
+}
+
+// Raw buffer descriptor over [base, base + 2 GB): stride 0, the rest as
+// __builtin_amdgcn_make_buffer_rsrc builds it.
+__device__ __forceinline__ i32x4_t raw_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4_t{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), 0x7fffffff, 0x00020000};  // word 3: gfx9 raw buffer
+}
+
+constexpr int kTileBytes = 32 * 1024;  // one K or V^T tile, hi and lo halves
+constexpr int kRing = 3;               // tile stages in LDS
+
+// Sequences of at most kRegTiles tiles (every sequence of the launch at most
+// kRegKeys keys): pass 1 keeps each lane's raw scores in registers (8 per
+// 32-key tile, 128 VGPRs at 512 keys) and pass 2 reads them back instead of
+// recomputing S^T, so K is streamed once and a third of the MFMAs and LDS
+// reads go away.  The tiles reach LDS by buffer_load ... lds (no staging
+// registers): one stream of 2 nt items, the nt K tiles then the nt V^T tiles,
+// item i in ring stage i % 3, issued two items ahead; each wave issues four
+// 1-KB copies per item (past the last item it re-copies that one into the free
+// stage), so one constant vmcnt per step says "item i has landed" and the
+// barrier after it publishes every wave's copies and retires the stage the
+// next copies overwrite.
+//
+// LDS layouts, XOR-swizzled in 16-byte chunks so that the 16x16x32 fragment
+// reads (16 rows x 4 lane groups) hit distinct banks with unpadded rows:
+//   K stage:   row R = 32 hl + key (hl 0 hi, 1 lo), 512 B per row; chunk c
+//              (dims 8c .. 8c + 7) at position c ^ (R & 15).
+//   V^T stage: row d = dim, 128 B per row (hi keys then lo keys, the global
+//              layout); chunk c at position c ^ ((d >> 1) & 7).
+// A copy lane picks the global chunk its LDS position holds, so the swizzle
+// costs nothing at copy time; fragment addresses are one XOR per k-step.
+template <bool QPRE>
+__global__ __launch_bounds__(kNT, 2) void k_attn_rs(
+    const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
+    const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vt, int ldvt, float* __restrict__ out,
+    int ldo, const int32_t* __restrict__ seq_off, const int32_t* __restrict__ voff, const sg_item* __restrict__ items,
+    int G, float sscale, float* __restrict__ amax, sg_attn_qpre qp) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kRing * kTileBytes];
+  __shared__ float red[kWaves];
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+
+  const sg_item it = items[blockIdx.x];
+  const int kvh = blockIdx.y;
+  const int r0 = seq_off[it.seq];
+  const int S = seq_off[it.seq + 1] - r0;
+  const int vo = voff[it.seq];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6) & (kWaves - 1);
+  const int ln = lane & 15, g4 = lane >> 4;
+  const int nqb = (S + kQW - 1) / kQW;
+  const int nt = (S + kBK - 1) / kBK;  // <= kRegTiles (the host checks the longest sequence)
+  const int c = it.c0 + w;
+  const bool active = c < G * nqb;  // wave-uniform
+  const int hg = active ? c / nqb : 0;
+  const int q0 = active ? (c % nqb) * kQW : 0;
+  const int head = kvh * G + hg;
+  const int qrow = q0 + ln;
+  const bool qvalid = active && qrow < S;
+  const int qr = r0 + min(qrow, S - 1);
+
+  // ---- copies ----
+  // Wave w's four copies of an item land at w * 4 KB + i * 1 KB of the stage.
+  // K item: copy i moves rows R = 8w + 2i and 8w + 2i + 1 (hi for waves 0-3,
+  // lo for waves 4-7); lane L takes row R = 8w + 2i + L / 32 and LDS position
+  // L % 32, i.e. global chunk (L % 32) ^ (R & 15).  Keys past the sequence's
+  // end are clamped to its last key (masked below), as in k_attn.
+  // V^T item: copy i moves dims 32w + 8i .. + 7; lane L takes dim
+  // d = 32w + 8i + L / 8, position L % 8, global chunk (L % 8) ^ ((d >> 1) & 7);
+  // every tile of a sequence lies inside its padded V^T columns.
+  const i32x4_t rk = raw_rsrc((w < 4 ? kh : kl) + (int64_t)r0 * ldk + kvh * kHD);
+  const i32x4_t rv = raw_rsrc(vt + (int64_t)kvh * kHD * ldvt + 2 * vo);
+  int kkey[4];
+  uint32_t kchunk[4], voffs[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int R = 8 * w + 2 * i + (lane >> 5);
+    kkey[i] = R & 31;
+    kchunk[i] = 16u * (uint32_t)((lane & 31) ^ (R & 15));
+    const int d = 32 * (w & 7) + 8 * i + (lane >> 3), cv = (lane & 7) ^ ((d >> 1) & 7);
+    voffs[i] = (uint32_t)d * (uint32_t)ldvt * 2u + 16u * (uint32_t)cv;
+  }
+  auto issue = [&](int item) {
+    const int last = 2 * nt - 1;
+    const int src = item < last ? item : last;
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_ptr)(lds + ((unsigned)item % kRing) * kTileBytes + w * 4096);
+    const bool isk = src < nt;
+    const int kt = src * kBK;
+    const uint32_t soff = isk ? 0u : (uint32_t)(src - nt) * kBK * 4u;  // V^T: the tile's columns, 64 halves per 32 keys
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t ko = (uint32_t)min(kt + kkey[i], S - 1) * (uint32_t)ldk * 2u + kchunk[i];
+      lds_copy16(dst + 1024u * i, isk ? ko : voffs[i], isk ? rk : rv, soff);
+    }
+  };
+  issue(0);
+  issue(1);
+  half8_t bqh[kHD / 32], bql[kHD / 32];
+  // The Q prologue's LDS tiles sit in stage 2, which no copy touches before
+  // the first barrier.
+  q_operand<QPRE>(bqh, bql, qh, ql, ldq, qp, qr, head, ln, g4, lane,
+                  reinterpret_cast<float*>(lds + 2 * kTileBytes) + w * (16 * 40));
+
+  auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
+  // ---- pass 1: S^T = K Q^T per tile, kept in registers; row max ----
+  // K fragment (row R = 32 hl + 16 st + ln, chunk 4 ks + g4) at
+  // R * 512 + 16 * ((4 ks + g4) ^ ln) = (xk ^ 64 ks) + 8192 st + 16384 hl.
+  const uint32_t xk = (uint32_t)ln * 512u + 16u * (uint32_t)(g4 ^ (ln & 3)) + 64u * (uint32_t)(ln >> 2);
+  auto scores2 = [&](const unsigned char* kb, f32x4_t& a0, f32x4_t& a1) {
+    auto rd = [&](int st, int ks, half8_t& h, half8_t& l) {
+      const unsigned char* p = kb + (xk ^ (64u * ks)) + 8192 * st;
+      h = *reinterpret_cast<const half8_t*>(p);
+      l = *reinterpret_cast<const half8_t*>(p + 16384);
+    };
+    a0 = f32x4_t{0, 0, 0, 0};
+    a1 = f32x4_t{0, 0, 0, 0};
+    half8_t h0, l0, h1, l1;
+    rd(0, 0, h0, l0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int ks = 0; ks < kHD / 32; ks++) {
+      rd(1, ks, h1, l1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      a0 = mfma16(h0, bqh[ks], a0);
+      a0 = mfma16(h0, bql[ks], a0);
+      a0 = mfma16(l0, bqh[ks], a0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+      if (ks + 1 < kHD / 32) {
+        rd(0, ks + 1, h0, l0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      a1 = mfma16(h1, bqh[ks], a1);
+      a1 = mfma16(h1, bql[ks], a1);
+      a1 = mfma16(l1, bqh[ks], a1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    }
+  };
+  float m = -INFINITY;
+  f32x4_t sr[kRegTiles][2];
+#pragma unroll
+  for (int t = 0; t < kRegTiles; t++) {
+    if (t < nt) {
+      wait_vmcnt<4>();  // item t landed (item t + 1 may still be in flight)
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      issue(t + 2);
+      // Every wave computes (an inactive wave's results are never stored).
+      scores2(lds + (t % kRing) * kTileBytes, sr[t][0], sr[t][1]);
+      const int kt = t * kBK;
+      if (kt + kBK <= S) {  // keys past S only in a sequence's last tile
+#pragma unroll
+        for (int r = 0; r < 4; r++) m = fmaxf(m, fmaxf(sr[t][0][r], sr[t][1][r]));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          m = key_of(kt, 0, r) < S ? fmaxf(m, sr[t][0][r]) : m;
+          m = key_of(kt, 1, r) < S ? fmaxf(m, sr[t][1][r]) : m;
+        }
+      }
+    }
+  }
+  // Max of the raw (x64) scores; scaling by the power of two sscale commutes
+  // with max exactly.
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
+
+  // ---- pass 2: e = fastExp(s - m), row sums, O^T += V^T P^T ----
+  // V^T fragment (dim 16 mt + ln, chunk g4 hi / 4 + g4 lo) at
+  // (16 mt + ln) * 128 + 16 * (chunk ^ ((ln >> 1) & 7)): xv (+ 64 for lo)
+  // + 2048 mt.
+  const uint32_t xv = (uint32_t)ln * 128u + 16u * (uint32_t)(g4 ^ ((ln >> 1) & 7));
+  f32x4_t o[kHD / 16];
+#pragma unroll
+  for (int mt = 0; mt < kHD / 16; mt++) o[mt] = f32x4_t{0, 0, 0, 0};
+  float lsum = 0.0f;
+  auto pv = [&](const unsigned char* vb, const half8_t& ph, const half8_t& pl) {
+    const unsigned char* p0 = vb + xv;
+    half8_t fr[3][2];  // [buffer][hi, lo]
+    auto rd = [&](int mt, half8_t(&f)[2]) {
+      f[0] = *reinterpret_cast<const half8_t*>(p0 + 2048 * mt);
+      f[1] = *reinterpret_cast<const half8_t*>(vb + ((xv ^ 64u) + 2048u * mt));
+    };
+    rd(0, fr[0]);
+    rd(1, fr[1]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int mt = 0; mt < kHD / 16; mt++) {
+      if (mt + 2 < kHD / 16) {
+        rd(mt + 2, fr[(mt + 2) % 3]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      const half8_t(&f)[2] = fr[mt % 3];
+      o[mt] = mfma16(f[0], ph, o[mt]);
+      o[mt] = mfma16(f[0], pl, o[mt]);
+      o[mt] = mfma16(f[1], ph, o[mt]);
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    }
+  };
+#pragma unroll
+  for (int t = 0; t < kRegTiles; t++) {
+    if (t < nt) {
+      const int item = nt + t;
+      half8_t ph, pl;  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
+      const int kt = t * kBK;
+      const bool full = kt + kBK <= S;
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          float e = sg_fast_exp_nonpos(sr[t][st][r] * sscale - m);
+          if (!full) e = key_of(kt, st, r) < S ? e : 0.0f;
+          lsum = lsum + e;
+          const hl16 q = split_f16(e * kPScale);
+          ph[4 * st + r] = q.hi;
+          pl[4 * st + r] = q.lo;
+        }
+      }
+      wait_vmcnt<4>();
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      issue(item + 2);
+      pv(lds + ((unsigned)item % kRing) * kTileBytes, ph, pl);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-copies past the last item have landed
   lsum = lsum + __shfl_xor(lsum, 16);
   lsum = lsum + __shfl_xor(lsum, 32);
   const float f = (1.0f / lsum) * kPUnscale;
@@ -546,8 +801,12 @@ void launch_attn(dim3 grid, hipStream_t s, const _Float16* qh, const _Float16* q
                  const _Float16* kl, int ldk, const _Float16* vt, int ldvt, float* out, int ldo,
                  const int32_t* seq_off, const int32_t* voff, const sg_item* items, int G, float sscale, float* amax,
                  const sg_attn_qpre& qp) {
-  hipLaunchKernelGGL((k_attn<QPRE, RS>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
-                     seq_off, voff, items, G, sscale, amax, qp);
+  if constexpr (RS)
+    hipLaunchKernelGGL((k_attn_rs<QPRE>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
+                       seq_off, voff, items, G, sscale, amax, qp);
+  else
+    hipLaunchKernelGGL((k_attn<QPRE>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
+                       seq_off, voff, items, G, sscale, amax, qp);
 }
 }  // namespace
 
