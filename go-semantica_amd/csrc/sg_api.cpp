@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdint>
@@ -201,9 +202,11 @@ struct sg_ctx {
   hipStream_t stream = nullptr;
   std::mutex mu;  // guards the scratch below for the kernel seam
   HostBuf meta_h;
-  DevBuf meta_d, f16, amax, tab, split;
-  // Last use of f16 / split by an asynchronous GEMM call (sg_matmul_q8_0_int8,
-  // sg_ffn_gate_up): the next such call waits for it on its own stream.
+  DevBuf meta_d, f16, amax, tab;
+  DevBuf split;  // sg_attention's split operands
+  // Last use of f16 (and of a gate weight's gate/up interleave) by an
+  // asynchronous GEMM call (sg_matmul_q8_0_int8, sg_ffn_gate_up): the next
+  // such call waits for it on its own stream.
   hipEvent_t gemm_done = nullptr;
   bool gemm_pending = false;
 };
@@ -921,8 +924,10 @@ int sg_q8_weight_create(sg_ctx* ctx, const void* q8, int32_t out_dim, int32_t in
   *out = nullptr;
   if (out_dim <= 0 || in_dim <= 0 || in_dim % 32) return fail(SG_ERR_INVALID, "in_dim must be a positive multiple of 32");
   SG_TRY(set_device(ctx));
+  static std::atomic<uint64_t> next_id{1};
   sg_q8_weight* w = new sg_q8_weight;
   w->ctx = ctx;
+  w->id = next_id.fetch_add(1);
   w->N = out_dim;
   w->K = in_dim;
   DevBuf stage;
@@ -946,6 +951,7 @@ void sg_q8_weight_free(sg_q8_weight* w) {
   if (w->w) (void)hipFree(w->w);
   if (w->w8) (void)hipFree(w->w8);
   if (w->st) (void)hipFree(w->st);
+  w->pair.release();
   delete w;
 }
 
@@ -1070,21 +1076,32 @@ int sg_ffn_gate_up(sg_ctx* ctx, float* dst, const sg_q8_weight* w_gate, const sg
   // Block-major [K/32][N][32]: each 32-row group of one block is one 2-KB
   // chunk (128 B of scales), and chunks of gate and up alternate.
   // From kI8MinRows rows the int8 copies are interleaved (1-KB chunks) and the
-  // int8-operand GEMM runs, as in the forward.
+  // int8-operand GEMM runs, as in the forward.  The interleave is kept on the
+  // gate weight for its last (up weight, route) pair and rebuilt only when
+  // either changes; it is written on `s` after gemm_scratch_begin, so every
+  // later call (ordered after this one) sees it complete.
   const bool i8 = batch >= sgk::kI8MinRows;
   const size_t wch = (size_t)sgk::kGeluGroup * 32 * (i8 ? 1 : sizeof(_Float16)), sch = sgk::kGeluGroup * sizeof(float);
   const size_t nch = (size_t)(K / 32) * (N / sgk::kGeluGroup);
-  SG_TRY(ctx->split.ensure(2 * nch * (wch + sch)));
   SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)ar * K));
-  uint8_t* wi = ctx->split.as<uint8_t>();
-  uint8_t* si = wi + 2 * nch * wch;
-  const void* wg = i8 ? (const void*)w_gate->w8 : (const void*)w_gate->w;
-  const void* wu = i8 ? (const void*)w_up->w8 : (const void*)w_up->w;
   SG_TRY(gemm_scratch_begin(ctx, s));
-  SG_HIP(hipMemcpy2DAsync(wi, 2 * wch, wg, wch, wch, nch, hipMemcpyDeviceToDevice, s));
-  SG_HIP(hipMemcpy2DAsync(wi + wch, 2 * wch, wu, wch, wch, nch, hipMemcpyDeviceToDevice, s));
-  SG_HIP(hipMemcpy2DAsync(si, 2 * sch, w_gate->st, sch, sch, nch, hipMemcpyDeviceToDevice, s));
-  SG_HIP(hipMemcpy2DAsync(si + sch, 2 * sch, w_up->st, sch, sch, nch, hipMemcpyDeviceToDevice, s));
+  const bool rebuild = w_gate->pair_up != w_up->id || w_gate->pair_i8 != (int)i8;
+  if (rebuild) {
+    w_gate->pair_up = 0;  // invalid until the copies below are enqueued
+    SG_TRY(w_gate->pair.ensure(2 * nch * (wch + sch)));
+  }
+  uint8_t* wi = w_gate->pair.as<uint8_t>();
+  uint8_t* si = wi + 2 * nch * wch;
+  if (rebuild) {
+    const void* wg = i8 ? (const void*)w_gate->w8 : (const void*)w_gate->w;
+    const void* wu = i8 ? (const void*)w_up->w8 : (const void*)w_up->w;
+    SG_HIP(hipMemcpy2DAsync(wi, 2 * wch, wg, wch, wch, nch, hipMemcpyDeviceToDevice, s));
+    SG_HIP(hipMemcpy2DAsync(wi + wch, 2 * wch, wu, wch, wch, nch, hipMemcpyDeviceToDevice, s));
+    SG_HIP(hipMemcpy2DAsync(si, 2 * sch, w_gate->st, sch, sch, nch, hipMemcpyDeviceToDevice, s));
+    SG_HIP(hipMemcpy2DAsync(si + sch, 2 * sch, w_up->st, sch, sch, nch, hipMemcpyDeviceToDevice, s));
+    w_gate->pair_up = w_up->id;
+    w_gate->pair_i8 = (int)i8;
+  }
   if (i8) {
     int8_t* a8 = ctx->f16.as<int8_t>();
     SG_HIP(sgk::i8_blocked(x, batch, K, a8, ar, s));
@@ -1150,7 +1167,7 @@ int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const flo
   // Split operands as the forward's producers write them.
   const size_t T = (size_t)meta.T, qd = (size_t)n_heads * head_dim, kvd = (size_t)n_kv_heads * head_dim;
   SG_TRY(ctx->split.ensure(2 * sizeof(_Float16) * (T * qd + T * kvd + kvd * (size_t)meta.Tp)));
-  SG_TRY(gemm_scratch_begin(ctx, s));  // split is shared with sg_ffn_gate_up
+  SG_TRY(gemm_scratch_begin(ctx, s));  // after the asynchronous GEMM calls of this context
   _Float16* qs_h = ctx->split.as<_Float16>();
   _Float16* qs_l = qs_h + T * qd;
   _Float16* ks_h = qs_l + T * qd;

@@ -75,6 +75,35 @@ def test_gemm_fp32_config1(gpu_ctx, oracle, N, K):
     assert rel_err(got, avx2) <= 1e-5
 
 
+def test_ffn_gate_up_interleave_cache(gpu_ctx):
+    """sg_ffn_gate_up keeps the gate/up interleave on the gate weight and
+    rebuilds it only when the up weight or the operand route changes: one gate
+    with two up weights, alternating, on both routes (M = 40 and 4200) and back,
+    every call equal to the unfused GEMMs + GELU * up bit for bit."""
+    import torch
+    from semantica_gpu import kernels, synth
+    N, K = 256, 768
+    rng = np.random.default_rng(17)
+    wg = kernels.Q8Weight(gpu_ctx, synth.q8_0_random(rng, N, K), N, K)
+    ups = [kernels.Q8Weight(gpu_ctx, synth.q8_0_random(rng, N, K), N, K) for _ in range(2)]
+    say("ffn gate/up interleave cache")
+    try:
+        for M, u in [(40, 0), (40, 0), (40, 1), (4200, 1), (4200, 0), (40, 0), (4200, 0)]:
+            xq = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+            rs = rng.uniform(1e-3, 2e-2, M).astype(np.float32)
+            gate = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            up, ref, got = torch.empty_like(gate), torch.empty_like(gate), torch.empty_like(gate)
+            kernels.matmul_q8_0(gpu_ctx, gate, wg, dev(xq), dev(rs))
+            kernels.matmul_q8_0(gpu_ctx, up, ups[u], dev(xq), dev(rs))
+            kernels.gelu_quick_mul(gpu_ctx, ref, gate, up)
+            kernels.ffn_gate_up(gpu_ctx, got, wg, ups[u], dev(xq), dev(rs))
+            assert np.array_equal(host(got).view(np.uint32), host(ref).view(np.uint32)), (M, u)
+    finally:
+        wg.close()
+        for w in ups:
+            w.close()
+
+
 @pytest.mark.parametrize("M,K", [(1, 768), (33, 768), (2048, 768), (4500, 768), (8200, 768), (4500, 800)])
 def test_ffn_gate_up_fused_bit_exact(gpu_ctx, oracle, M, K):
     """The fused gate/up GEMM with GELUQuick * up in its epilogue equals the
