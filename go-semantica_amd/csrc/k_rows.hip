@@ -23,9 +23,8 @@ __device__ __forceinline__ uint16_t rd_u16(const uint8_t* p) { return (uint16_t)
 
 // One thread per Q8_0 block: 2-byte fp16 scale + 32 int8 values
 // (GGUF Q8_0 layout; extractQ8_0Scales model_int8.go:543-569 reads the same bytes).
-__global__ void k_repack_q8_0(const uint8_t* __restrict__ raw, int rows, int cols, _Float16* __restrict__ w16,
-                              int8_t* __restrict__ w8, float* __restrict__ st, int ld, int row_off, int grp,
-                              int gstride) {
+__global__ void k_repack_q8_0(const uint8_t* __restrict__ raw, int rows, int cols, int8_t* __restrict__ w8,
+                              float* __restrict__ st, int ld, int row_off, int grp, int gstride) {
   const int nb = cols / 32;
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= (int64_t)rows * nb) return;
@@ -33,19 +32,9 @@ __global__ void k_repack_q8_0(const uint8_t* __restrict__ raw, int rows, int col
   const int dr = row_off + (r / grp) * gstride + r % grp;
   const uint8_t* blk = raw + id * 34;
   st[(int64_t)b * ld + dr] = sg_f16_ieee(rd_u16(blk));
-  _Float16* dst = w16 + ((int64_t)b * ld + dr) * 32;
+  int8_t* d8 = w8 + ((int64_t)b * ld + dr) * 32;
 #pragma unroll
-  for (int i = 0; i < 32; i += 8) {
-    half8_t v;
-#pragma unroll
-    for (int t = 0; t < 8; t++) v[t] = (_Float16)(float)(int8_t)blk[2 + i + t];
-    *reinterpret_cast<half8_t*>(dst + i) = v;
-  }
-  if (w8) {  // the same values as int8, same layout
-    int8_t* d8 = w8 + ((int64_t)b * ld + dr) * 32;
-#pragma unroll
-    for (int i = 0; i < 32; i++) d8[i] = (int8_t)blk[2 + i];
-  }
+  for (int i = 0; i < 32; i++) d8[i] = (int8_t)blk[2 + i];
 }
 
 // int8 x[M][K] -> block-major int8 y[K/32][a_rows][32]: one thread moves a
@@ -78,35 +67,6 @@ __global__ void k_repack_embd(const uint8_t* __restrict__ raw, int vocab, int d,
   int8_t* dst = q + id * 32;
 #pragma unroll
   for (int i = 0; i < 32; i++) dst[i] = (int8_t)blk[2 + i];
-}
-
-__global__ void k_i8_to_f16_blocked(const int8_t* __restrict__ x, int M, int K, _Float16* __restrict__ y,
-                                    int a_rows) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)M * K) return;
-  const int m = (int)(i / K), k = (int)(i % K);
-  y[((int64_t)(k >> 5) * a_rows + m) * 32 + (k & 31)] = (_Float16)(float)x[i];
-}
-
-// 16 consecutive k of one row per thread: one 16-byte load, two 16-byte
-// stores into the row's 64-byte piece of K-block k/32.
-__global__ void k_i8_to_f16_blocked16(const int8_t* __restrict__ x, int M, int K, _Float16* __restrict__ y,
-                                      int a_rows) {
-  const int kc16 = K >> 4;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)M * kc16) return;
-  const int m = (int)(i / kc16), kc = (int)(i % kc16) << 4;
-  typedef int8_t i8x16_t __attribute__((ext_vector_type(16)));
-  const i8x16_t v = *reinterpret_cast<const i8x16_t*>(x + (int64_t)m * K + kc);
-  half8_t lo, hi;
-#pragma unroll
-  for (int t = 0; t < 8; t++) {
-    lo[t] = (_Float16)(float)v[t];
-    hi[t] = (_Float16)(float)v[8 + t];
-  }
-  _Float16* d = y + ((int64_t)(kc >> 5) * a_rows + m) * 32 + (kc & 31);
-  *reinterpret_cast<half8_t*>(d) = lo;
-  *reinterpret_cast<half8_t*>(d + 8) = hi;
 }
 
 __global__ void k_fill(float* __restrict__ p, float v, int64_t n) {
@@ -203,17 +163,26 @@ __global__ __launch_bounds__(kThreads) void k_embed_only(const int32_t* __restri
 
 // -------------------------------------------------------------- quantize --
 
+// Four codes as int8 (one 4-byte store).
+__device__ __forceinline__ void store_codes4(int8_t* p, const float (&c)[4]) {
+  uint32_t u = 0;
+#pragma unroll
+  for (int t = 0; t < 4; t++) u |= (uint32_t)(uint8_t)(int8_t)(int)c[t] << (8 * t);
+  *reinterpret_cast<uint32_t*>(p) = u;
+}
+
 // quantize.go:29-103 with the tensor max replaced by the per-sequence max
 // gathered into amax (one reference call quantizes one sequence):
 // scale = m/127 (fp32), inv = 1/scale (fp32),
 // q = clamp(round_half_away(float64(x)*float64(inv)), +-127) (sg_quant_code);
 // m == 0 -> scale 1, q 0.
 // One row per wave (4 rows per workgroup): the row's scale and reciprocal are
-// computed once, then the wave walks the row in coalesced float4 slots.
-template <bool F16>
+// computed once, then the wave walks the row in coalesced float4 slots.  The
+// codes go to the block-major GEMM operand qb [cols/32][a_rows][32] (qb !=
+// null) or row-major to qi [rows][cols].
 __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__ x, int ldx, int rows, int cols,
                                                        const int32_t* __restrict__ row_seq,
-                                                       const float* __restrict__ amax, _Float16* __restrict__ qf,
+                                                       const float* __restrict__ amax, int8_t* __restrict__ qb,
                                                        int a_rows, int8_t* __restrict__ qi,
                                                        float* __restrict__ row_scale) {
   const int row = blockIdx.x * (kThreads / SG_WAVE) + (threadIdx.x >> 6);
@@ -232,35 +201,8 @@ __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__
     float qv[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) qv[t] = sg_quant_code(v[t], inv);  // m == 0: inv == 0 gives 0
-    if (F16) {  // block-major GEMM operand: [k/32][a_rows][32]
-      half4_t h;
-#pragma unroll
-      for (int t = 0; t < 4; t++) h[t] = (_Float16)qv[t];
-      const int k = 4 * c4;
-      *reinterpret_cast<half4_t*>(qf + ((int64_t)(k >> 5) * a_rows + row) * 32 + (k & 31)) = h;
-    } else {
-      char4 c;
-      c.x = (signed char)(int)qv[0]; c.y = (signed char)(int)qv[1]; c.z = (signed char)(int)qv[2];
-      c.w = (signed char)(int)qv[3];
-      *reinterpret_cast<char4*>(qi + (int64_t)row * cols + 4 * c4) = c;
-    }
-  }
-}
-
-// Four codes of one K-block piece of the GEMM operand: fp16-encoded integers
-// (8 bytes) or int8 (4 bytes).
-template <typename OutT>
-__device__ __forceinline__ void store_codes4(OutT* p, const float (&c)[4]) {
-  if constexpr (std::is_same<OutT, int8_t>::value) {
-    uint32_t u = 0;
-#pragma unroll
-    for (int t = 0; t < 4; t++) u |= (uint32_t)(uint8_t)(int8_t)(int)c[t] << (8 * t);
-    *reinterpret_cast<uint32_t*>(p) = u;
-  } else {
-    half4_t hv;
-#pragma unroll
-    for (int t = 0; t < 4; t++) hv[t] = (_Float16)c[t];
-    *reinterpret_cast<half4_t*>(p) = hv;
+    const int k = 4 * c4;
+    store_codes4(qb ? qb + ((int64_t)(k >> 5) * a_rows + row) * 32 + (k & 31) : qi + (int64_t)row * cols + k, qv);
   }
 }
 
@@ -270,11 +212,11 @@ __device__ __forceinline__ void store_codes4(OutT* p, const float (&c)[4]) {
 // one the unfused path quantizes), then quantized as k_quantize does
 // (model_int8.go:194-199 / :216-221: RMSNorm, then QuantizeSymmetricINT8 of
 // the normed sequence).  Saves writing xn and reading it back.
-template <int NC, typename OutT>
+template <int NC>
 __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restrict__ h, const float* __restrict__ w,
                                                             float eps, int T, const int32_t* __restrict__ row_seq,
                                                             const float* __restrict__ amax,
-                                                            OutT* __restrict__ qf, int a_rows,
+                                                            int8_t* __restrict__ qf, int a_rows,
                                                             float* __restrict__ row_scale) {
   constexpr int D = NC * 32;
   __shared__ __attribute__((aligned(16))) float tiles[kThreads / SG_WAVE][8 * 40];
@@ -294,7 +236,7 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
   }
   if (j == 0) row_scale[row] = scale;
   // chunk c is K-block c; lane j holds its elements 4j..4j+3
-  OutT* qr = qf + (int64_t)row * 32 + 4 * j;
+  int8_t* qr = qf + (int64_t)row * 32 + 4 * j;
 #pragma unroll
   for (int c = 0; c < NC; c++) {
     float cv[4];
@@ -308,11 +250,11 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
 // group per row, lane j handling elements 32c + 4j .. + 3 of every chunk c
 // (chunk c is K-block c), so a wave's stores cover 8 consecutive rows' 64-byte
 // block pieces: 512 contiguous bytes per instruction.
-template <int NC, typename OutT>
+template <int NC>
 __global__ __launch_bounds__(kThreads) void k_quantize_blocked(const float* __restrict__ x, int ldx, int rows,
                                                                const int32_t* __restrict__ row_seq,
                                                                const float* __restrict__ amax,
-                                                               OutT* __restrict__ qf, int a_rows,
+                                                               int8_t* __restrict__ qf, int a_rows,
                                                                float* __restrict__ row_scale) {
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7;
@@ -328,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void k_quantize_blocked(const float* __re
   f32x4_t v[NC];  // every load in flight before the first store
 #pragma unroll
   for (int c = 0; c < NC; c++) v[c] = xr[8 * c];
-  OutT* qr = qf + (int64_t)row * 32 + 4 * j;
+  int8_t* qr = qf + (int64_t)row * 32 + 4 * j;
 #pragma unroll
   for (int c = 0; c < NC; c++) {
     float cv[4];
@@ -611,30 +553,18 @@ inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1)
 
 namespace sgk {
 
-hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, int8_t* w8, float* st, int ld,
-                       int row_off, int grp, int gstride, hipStream_t s) {
+hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, int8_t* w8, float* st, int ld, int row_off, int grp,
+                       int gstride, hipStream_t s) {
   const int64_t n = (int64_t)rows * (cols / 32);
   if (grp <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(n, 256)), dim3(256), 0, s, raw, rows, cols, w16, w8, st, ld,
-                     row_off, grp, gstride);
+  hipLaunchKernelGGL(k_repack_q8_0, dim3(blocks_for(n, 256)), dim3(256), 0, s, raw, rows, cols, w8, st, ld, row_off,
+                     grp, gstride);
   return hipGetLastError();
 }
 
 hipError_t repack_embd(const uint8_t* raw, int vocab, int d, int8_t* q, float* sc, hipStream_t s) {
   const int64_t n = (int64_t)vocab * (d / 32);
   hipLaunchKernelGGL(k_repack_embd, dim3(blocks_for(n, 256)), dim3(256), 0, s, raw, vocab, d, q, sc);
-  return hipGetLastError();
-}
-
-hipError_t i8_to_f16_blocked(const int8_t* x, int M, int K, _Float16* y, int a_rows, hipStream_t s) {
-  const int64_t n = (int64_t)M * K;
-  if (n <= 0) return hipSuccess;
-  if (K % 32 || a_rows < M) return hipErrorInvalidValue;
-  if (K % 32 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
-    hipLaunchKernelGGL(k_i8_to_f16_blocked16, dim3(blocks_for(n / 16, 256)), dim3(256), 0, s, x, M, K, y, a_rows);
-    return hipGetLastError();
-  }
-  hipLaunchKernelGGL(k_i8_to_f16_blocked, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, M, K, y, a_rows);
   return hipGetLastError();
 }
 
@@ -695,71 +625,37 @@ hipError_t embed_only(const int32_t* tokens, int T, const int8_t* eq, const floa
 }
 
 hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
-                    _Float16* f16, int a_rows, int8_t* i8, float* row_scale, hipStream_t s) {
+                    int8_t* q8, int a_rows, int8_t* i8, float* row_scale, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  if (cols % 4 || ldx % 4) return hipErrorInvalidValue;
-  if (f16 && (cols % 32 || a_rows < rows)) return hipErrorInvalidValue;
-  const unsigned nblk = blocks_for(rows, kThreads / SG_WAVE);
-  if (f16 && (ldx & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
-    switch (cols) {  // the widths the forward quantizes: hidden, attention output, FFN
-      case 768:
-        hipLaunchKernelGGL((k_quantize_blocked<24, _Float16>), dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0, s, x,
-                           ldx, rows, row_seq, amax, f16, a_rows, row_scale);
-        return hipGetLastError();
-      case 1152:
-        hipLaunchKernelGGL((k_quantize_blocked<36, _Float16>), dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0, s, x,
-                           ldx, rows, row_seq, amax, f16, a_rows, row_scale);
-        return hipGetLastError();
+  if (cols % 4 || ldx % 4 || (!q8 && !i8)) return hipErrorInvalidValue;
+  if (q8 && (cols % 32 || a_rows < rows)) return hipErrorInvalidValue;
+  if (q8 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    const unsigned nb = blocks_for(rows, kRowsPerBlock);
+    switch (cols) {  // the widths the forward quantizes: attention output, hidden, FFN
+#define SG_QB(C)                                                                                                   \
+  case C:                                                                                                          \
+    hipLaunchKernelGGL((k_quantize_blocked<C / 32>), dim3(nb), dim3(kThreads), 0, s, x, ldx, rows, row_seq, amax, \
+                       q8, a_rows, row_scale);                                                                     \
+    return hipGetLastError();
+      SG_QB(256) SG_QB(512) SG_QB(768) SG_QB(1024) SG_QB(1152)
+#undef SG_QB
       default:
         break;
     }
   }
-  if (f16)
-    hipLaunchKernelGGL(k_quantize<true>, dim3(nblk), dim3(kThreads), 0, s, x, ldx, rows, cols, row_seq, amax, f16,
-                       a_rows, nullptr, row_scale);
-  else
-    hipLaunchKernelGGL(k_quantize<false>, dim3(nblk), dim3(kThreads), 0, s, x, ldx, rows, cols, row_seq, amax,
-                       nullptr, 0, i8, row_scale);
+  hipLaunchKernelGGL(k_quantize, dim3(blocks_for(rows, kThreads / SG_WAVE)), dim3(kThreads), 0, s, x, ldx, rows, cols,
+                     row_seq, amax, q8, a_rows, q8 ? nullptr : i8, row_scale);
   return hipGetLastError();
 }
 
 hipError_t norm_quantize(const float* h, const float* w, float eps, int T, int d, const int32_t* row_seq,
-                         const float* amax, _Float16* f16, int a_rows, float* row_scale, hipStream_t s) {
+                         const float* amax, int8_t* q8, int a_rows, float* row_scale, hipStream_t s) {
   if (T <= 0) return hipSuccess;
   if (a_rows < T) return hipErrorInvalidValue;
   SG_DISPATCH_NPL(d, NPL,
-                  hipLaunchKernelGGL((k_norm_quantize<NPL / 4, _Float16>), dim3(blocks_for(T, kRowsPerBlock)),
-                                     dim3(kThreads), 0, s, h, w, eps, T, row_seq, amax, f16, a_rows, row_scale));
+                  hipLaunchKernelGGL((k_norm_quantize<NPL / 4>), dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads),
+                                     0, s, h, w, eps, T, row_seq, amax, q8, a_rows, row_scale));
   return hipGetLastError();
-}
-
-hipError_t norm_quantize_i8(const float* h, const float* w, float eps, int T, int d, const int32_t* row_seq,
-                            const float* amax, int8_t* q8, int a_rows, float* row_scale, hipStream_t s) {
-  if (T <= 0) return hipSuccess;
-  if (a_rows < T) return hipErrorInvalidValue;
-  SG_DISPATCH_NPL(d, NPL,
-                  hipLaunchKernelGGL((k_norm_quantize<NPL / 4, int8_t>), dim3(blocks_for(T, kRowsPerBlock)),
-                                     dim3(kThreads), 0, s, h, w, eps, T, row_seq, amax, q8, a_rows, row_scale));
-  return hipGetLastError();
-}
-
-hipError_t quantize_i8(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
-                       int8_t* q8, int a_rows, float* row_scale, hipStream_t s) {
-  if (rows <= 0) return hipSuccess;
-  if ((ldx & 3) || (reinterpret_cast<uintptr_t>(x) & 15) || a_rows < rows || !quantize_i8_width(cols))
-    return hipErrorInvalidValue;
-  switch (cols) {  // the widths the forward quantizes: attention output, FFN
-    case 768:
-      hipLaunchKernelGGL((k_quantize_blocked<24, int8_t>), dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0,
-                         s, x, ldx, rows, row_seq, amax, q8, a_rows, row_scale);
-      return hipGetLastError();
-    case 1152:
-      hipLaunchKernelGGL((k_quantize_blocked<36, int8_t>), dim3(blocks_for(rows, kRowsPerBlock)), dim3(kThreads), 0,
-                         s, x, ldx, rows, row_seq, amax, q8, a_rows, row_scale);
-      return hipGetLastError();
-    default:
-      return hipErrorInvalidValue;
-  }
 }
 
 hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s) {

@@ -202,9 +202,9 @@ struct sg_ctx {
   hipStream_t stream = nullptr;
   std::mutex mu;  // guards the scratch below for the kernel seam
   HostBuf meta_h;
-  DevBuf meta_d, f16, amax, tab;
+  DevBuf meta_d, a8, amax, tab;
   DevBuf split;  // sg_attention's split operands
-  // Last use of f16 (and of a gate weight's gate/up interleave) by an
+  // Last use of a8 (and of a gate weight's gate/up interleave) by an
   // asynchronous GEMM call (sg_matmul_q8_0_int8, sg_ffn_gate_up): the next
   // such call waits for it on its own stream.
   hipEvent_t gemm_done = nullptr;
@@ -221,8 +221,7 @@ hipStream_t ctx_stream(const sg_ctx* c, void* stream) {
 namespace {
 
 struct LayerDev {
-  _Float16 *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wd = nullptr;
-  int8_t *wqkv8 = nullptr, *wo8 = nullptr, *wgu8 = nullptr, *wd8 = nullptr;  // the same values as int8
+  int8_t *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wd = nullptr;  // block-major int8 [K/32][N][32]
   float *sqkv = nullptr, *so = nullptr, *sgu = nullptr, *sd = nullptr;
   float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
   float *post_attn = nullptr, *ffn_norm = nullptr, *post_ffw = nullptr;
@@ -295,7 +294,7 @@ struct Profiler {
 // stream of its own (created on first use, default flags and priority) with
 // the event that joins it back to the caller's stream.
 struct Lane {
-  DevBuf h, xn, qkv, att, o, g, a16, sx, amax, meta_d, err;
+  DevBuf h, xn, qkv, att, o, g, a8, sx, amax, meta_d, err;
   DevBuf ks, vt;  // attention operands, hi/lo fp16 (K row-major; V^T); Q is split inside the attention kernel
   HostBuf meta_h, io_h;
   hipStream_t stream = nullptr;
@@ -312,7 +311,7 @@ struct Lane {
     return SG_OK;
   }
   ~Lane() {
-    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a16, &sx, &amax, &meta_d, &err, &ks, &vt}) b->release();
+    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a8, &sx, &amax, &meta_d, &err, &ks, &vt}) b->release();
     meta_h.release();
     io_h.release();
     if (done) (void)hipEventDestroy(done);
@@ -377,15 +376,15 @@ int upload_f32(sg_model* m, float** dst, const float* src, int n) {
 }
 
 // Copies one raw Q8_0 matrix through `stage` and repacks it into rows
-// [row_off, row_off+rows) of w16 and w8 (the int8 copy) / columns of st.
+// [row_off, row_off+rows) of w8 / columns of st.
 // grp/gstride: row grouping of repack_q8_0 (0: rows stay contiguous).
-int upload_q8(const void* raw, int rows, int cols, DevBuf& stage, _Float16* w16, int8_t* w8, float* st, int ld_st,
-              int row_off, hipStream_t s, int grp = 0, int gstride = 0) {
+int upload_q8(const void* raw, int rows, int cols, DevBuf& stage, int8_t* w8, float* st, int ld_st, int row_off,
+              hipStream_t s, int grp = 0, int gstride = 0) {
   if (!raw) return fail(SG_ERR_INVALID, "missing Q8_0 tensor");
   const size_t bytes = (size_t)rows * (cols / 32) * 34;
   SG_TRY(stage.ensure(bytes));
   SG_HIP(hipMemcpyAsync(stage.p, raw, bytes, hipMemcpyHostToDevice, s));
-  SG_HIP(sgk::repack_q8_0(stage.as<uint8_t>(), rows, cols, w16, w8, st, ld_st, row_off, grp ? grp : rows, gstride, s));
+  SG_HIP(sgk::repack_q8_0(stage.as<uint8_t>(), rows, cols, w8, st, ld_st, row_off, grp ? grp : rows, gstride, s));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;
 }
@@ -446,7 +445,7 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
   float* att = w.att.as<float>();
   float* o = w.o.as<float>();
   float* g = w.g.as<float>();
-  _Float16* a16 = w.a16.as<_Float16>();
+  int8_t* a8 = w.a8.as<int8_t>();
   const int ar = sgk::gemm_pad_rows(T);
   _Float16* ks_h = w.ks.as<_Float16>();
   _Float16* ks_l = ks_h + (size_t)T * kvd;
@@ -462,26 +461,18 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
   const double attn_flops = 4.0 * c.num_heads * m->hd * meta.sum_sq;
   const double attn_bytes = t * (2.0 * qd + 2.0 * kvd) * 4.0;
   (void)attn_bytes;
-  // From kI8MinRows tokens the GEMM operands are int8 (the quantizers store the
-  // same codes as int8, the GEMMs read the int8 weight copies): half the
-  // operand bytes, one MFMA per block instead of two, the same output bits.
-  const bool i8 = T >= sgk::kI8MinRows && sgk::quantize_i8_width(qd) && sgk::quantize_i8_width(ff);
-  int8_t* a8 = reinterpret_cast<int8_t*>(a16);
   auto norm_q = [&](const float* w, float* am) {
-    return i8 ? sgk::norm_quantize_i8(h, w, eps, T, d, meta.row_seq, am, a8, ar, sx, s)
-              : sgk::norm_quantize(h, w, eps, T, d, meta.row_seq, am, a16, ar, sx, s);
+    return sgk::norm_quantize(h, w, eps, T, d, meta.row_seq, am, a8, ar, sx, s);
   };
   auto quant = [&](const float* x, int cols, float* am) {
-    return i8 ? sgk::quantize_i8(x, cols, T, cols, meta.row_seq, am, a8, ar, sx, s)
-              : sgk::quantize(x, cols, T, cols, meta.row_seq, am, a16, ar, nullptr, sx, s);
+    return sgk::quantize(x, cols, T, cols, meta.row_seq, am, a8, ar, nullptr, sx, s);
   };
   auto tap = [&](float* dst, const float* src, int l, int cols) {
     return hipMemcpyAsync(dst + (size_t)l * T * cols, src, sizeof(float) * (size_t)T * cols, hipMemcpyDeviceToDevice,
                           s);
   };
-  auto gemm = [&](const _Float16* w16, const int8_t* w8, const float* st, float* y, int N, int K) {
-    return i8 ? sgk::gemm_q8_i8(a8, ar, w8, st, sx, y, T, N, K, s)
-              : sgk::gemm_q8(a16, ar, w16, st, sx, y, nullptr, T, N, K, s);
+  auto gemm = [&](const int8_t* w8, const float* st, float* y, int N, int K) {
+    return sgk::gemm_q8(a8, ar, w8, st, sx, y, nullptr, T, N, K, s);
   };
 
   if (l0 == 0) {
@@ -496,7 +487,7 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
     const LayerDev& ly = m->layers[l];
     // The pre-norm's output xn is never stored: recomputed from h while quantizing.
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.attn_norm, site(l, 0)));
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), gemm(ly.wqkv, ly.wqkv8, ly.sqkv, qkv, nqkv, d));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), gemm(ly.wqkv, ly.sqkv, qkv, nqkv, d));
     if (tr && tr->qkv) SG_HIP(tap(tr->qkv, qkv, l, nqkv));
     // K's QK-norm + RoPE + split and V's V^T split in one launch; Q's norm and
     // RoPE run inside the attention kernel.
@@ -511,15 +502,14 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
                              site(l, 1), meta.max_len, s, &qpre));
     if (tr && tr->att) SG_HIP(tap(tr->att, att, l, qd));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), quant(att, qd, site(l, 1)));
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), gemm(ly.wo, ly.wo8, ly.so, o, d, qd));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), gemm(ly.wo, ly.so, o, d, qd));
     SG_LAUNCH(SG_K_NORM, t * d * 12.0,
               sgk::post_res_norm(o, h, ly.post_attn, ly.ffn_norm, eps, T, d, nullptr, meta.row_seq, site(l, 2), s));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.ffn_norm, site(l, 2)));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(2 * ff, d),
-              i8 ? sgk::gemm_q8_gelu_i8(a8, ar, ly.wgu8, ly.sgu, sx, g, T, ff, d, meta.row_seq, site(l, 3), s)
-                 : sgk::gemm_q8_gelu(a16, ar, ly.wgu, ly.sgu, sx, g, T, ff, d, meta.row_seq, site(l, 3), s));
+              sgk::gemm_q8_gelu(a8, ar, ly.wgu, ly.sgu, sx, g, T, ff, d, meta.row_seq, site(l, 3), s));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(ff), quant(g, ff, site(l, 3)));
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), gemm(ly.wd, ly.wd8, ly.sd, o, d, ff));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), gemm(ly.wd, ly.sd, o, d, ff));
     const bool last = l + 1 == L;
     SG_LAUNCH(SG_K_NORM, t * d * (last ? 16.0 : 12.0),
               sgk::post_res_norm(o, h, ly.post_ffw, last ? m->out_norm : m->layers[l + 1].attn_norm, eps, T, d,
@@ -593,7 +583,7 @@ int ensure_workspace(const sg_model* m, Lane& w, int T, int n_seq, int Tp) {
   SG_TRY(w.att.ensure(sizeof(float) * t * m->qd));
   SG_TRY(w.o.ensure(sizeof(float) * t * c.embed_dim));
   SG_TRY(w.g.ensure(sizeof(float) * t * c.interm_dim));
-  SG_TRY(w.a16.ensure(sizeof(_Float16) * (size_t)sgk::gemm_pad_rows(T) * a_cols));
+  SG_TRY(w.a8.ensure((size_t)sgk::gemm_pad_rows(T) * a_cols));
   SG_TRY(w.sx.ensure(sizeof(float) * t));
   SG_TRY(w.amax.ensure(sizeof(float) * 4 * (size_t)c.num_layers * n_seq));
   SG_TRY(w.ks.ensure(2 * sizeof(_Float16) * t * m->kvd));
@@ -741,7 +731,7 @@ void sg_shutdown(sg_ctx* c) {
   (void)hipStreamSynchronize(c->stream);
   c->meta_h.release();
   c->meta_d.release();
-  c->f16.release();
+  c->a8.release();
   c->amax.release();
   c->tab.release();
   c->split.release();
@@ -804,20 +794,18 @@ int sg_model_load(sg_ctx* ctx, const sg_model_desc* desc, sg_model** out) {
     if ((r = m->alloc(&ly.wqkv, (size_t)nqkv * d)) || (r = m->alloc(&ly.sqkv, (size_t)(d / 32) * nqkv)) ||
         (r = m->alloc(&ly.wo, (size_t)d * qd)) || (r = m->alloc(&ly.so, (size_t)(qd / 32) * d)) ||
         (r = m->alloc(&ly.wgu, (size_t)2 * ff * d)) || (r = m->alloc(&ly.sgu, (size_t)(d / 32) * 2 * ff)) ||
-        (r = m->alloc(&ly.wd, (size_t)d * ff)) || (r = m->alloc(&ly.sd, (size_t)(ff / 32) * d)) ||
-        (r = m->alloc(&ly.wqkv8, (size_t)nqkv * d)) || (r = m->alloc(&ly.wo8, (size_t)d * qd)) ||
-        (r = m->alloc(&ly.wgu8, (size_t)2 * ff * d)) || (r = m->alloc(&ly.wd8, (size_t)d * ff)))
+        (r = m->alloc(&ly.wd, (size_t)d * ff)) || (r = m->alloc(&ly.sd, (size_t)(ff / 32) * d)))
       return done(r);
-    if ((r = upload_q8(ld.attn_q, qd, d, stage, ly.wqkv, ly.wqkv8, ly.sqkv, nqkv, 0, s)) ||
-        (r = upload_q8(ld.attn_k, kvd, d, stage, ly.wqkv, ly.wqkv8, ly.sqkv, nqkv, qd, s)) ||
-        (r = upload_q8(ld.attn_v, kvd, d, stage, ly.wqkv, ly.wqkv8, ly.sqkv, nqkv, qd + kvd, s)) ||
-        (r = upload_q8(ld.attn_output, d, qd, stage, ly.wo, ly.wo8, ly.so, d, 0, s)) ||
+    if ((r = upload_q8(ld.attn_q, qd, d, stage, ly.wqkv, ly.sqkv, nqkv, 0, s)) ||
+        (r = upload_q8(ld.attn_k, kvd, d, stage, ly.wqkv, ly.sqkv, nqkv, qd, s)) ||
+        (r = upload_q8(ld.attn_v, kvd, d, stage, ly.wqkv, ly.sqkv, nqkv, qd + kvd, s)) ||
+        (r = upload_q8(ld.attn_output, d, qd, stage, ly.wo, ly.so, d, 0, s)) ||
         // gate and up interleaved in groups of 32 rows for the fused GELU GEMM
-        (r = upload_q8(ld.ffn_gate, ff, d, stage, ly.wgu, ly.wgu8, ly.sgu, 2 * ff, 0, s, sgk::kGeluGroup,
+        (r = upload_q8(ld.ffn_gate, ff, d, stage, ly.wgu, ly.sgu, 2 * ff, 0, s, sgk::kGeluGroup,
                        2 * sgk::kGeluGroup)) ||
-        (r = upload_q8(ld.ffn_up, ff, d, stage, ly.wgu, ly.wgu8, ly.sgu, 2 * ff, sgk::kGeluGroup, s, sgk::kGeluGroup,
+        (r = upload_q8(ld.ffn_up, ff, d, stage, ly.wgu, ly.sgu, 2 * ff, sgk::kGeluGroup, s, sgk::kGeluGroup,
                        2 * sgk::kGeluGroup)) ||
-        (r = upload_q8(ld.ffn_down, d, ff, stage, ly.wd, ly.wd8, ly.sd, d, 0, s)))
+        (r = upload_q8(ld.ffn_down, d, ff, stage, ly.wd, ly.sd, d, 0, s)))
       return done(r);
     if (!ld.attn_norm || !ld.ffn_norm) return done(fail(SG_ERR_INVALID, "layer %d: attn_norm/ffn_norm required", l));
     if ((r = upload_f32(m, &ly.attn_norm, ld.attn_norm, d)) || (r = upload_f32(m, &ly.q_norm, ld.attn_q_norm, m->hd)) ||
@@ -932,11 +920,10 @@ int sg_q8_weight_create(sg_ctx* ctx, const void* q8, int32_t out_dim, int32_t in
   w->K = in_dim;
   DevBuf stage;
   int r = SG_OK;
-  if (hipMalloc(&w->w, sizeof(_Float16) * (size_t)out_dim * in_dim) != hipSuccess ||
-      hipMalloc(&w->w8, (size_t)out_dim * in_dim) != hipSuccess ||
+  if (hipMalloc(&w->w8, (size_t)out_dim * in_dim) != hipSuccess ||
       hipMalloc(&w->st, sizeof(float) * (size_t)out_dim * (in_dim / 32)) != hipSuccess)
     r = fail(SG_ERR_NOMEM, "hipMalloc failed (weight)");
-  if (r == SG_OK) r = upload_q8(q8, out_dim, in_dim, stage, w->w, w->w8, w->st, out_dim, 0, ctx->stream);
+  if (r == SG_OK) r = upload_q8(q8, out_dim, in_dim, stage, w->w8, w->st, out_dim, 0, ctx->stream);
   stage.release();
   if (r != SG_OK) {
     sg_q8_weight_free(w);
@@ -948,7 +935,6 @@ int sg_q8_weight_create(sg_ctx* ctx, const void* q8, int32_t out_dim, int32_t in
 
 void sg_q8_weight_free(sg_q8_weight* w) {
   if (!w) return;
-  if (w->w) (void)hipFree(w->w);
   if (w->w8) (void)hipFree(w->w8);
   if (w->st) (void)hipFree(w->st);
   w->pair.release();
@@ -981,36 +967,29 @@ static int matmul_common(sg_ctx* ctx, float* dst, int32_t* sums, const sg_q8_wei
   if (!ctx || !w || !x || (!dst && !sums)) return fail(SG_ERR_INVALID, "NULL argument");
   if (batch < 0) return fail(SG_ERR_INVALID, "batch < 0");
   if (batch == 0) return SG_OK;
+  if (!sums && !row_scale) return fail(SG_ERR_INVALID, "row_scale is NULL");
   std::lock_guard<std::mutex> lk(ctx->mu);
   SG_TRY(set_device(ctx));
   hipStream_t s = pick(ctx, stream);
   const int ar = sgk::gemm_pad_rows(batch);
-  SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)ar * w->K));
+  SG_TRY(ctx->a8.ensure((size_t)ar * w->K));
   SG_TRY(gemm_scratch_begin(ctx, s));
+  int8_t* a8 = ctx->a8.as<int8_t>();
+  SG_HIP(sgk::i8_blocked(x, batch, w->K, a8, ar, s));
   if (sums) {  // parity dump: synchronous (a temporary output buffer)
-    SG_HIP(sgk::i8_to_f16_blocked(x, batch, w->K, ctx->f16.as<_Float16>(), ar, s));
     SG_TRY(ctx->amax.ensure(sizeof(float) * (size_t)batch));
     float* ones = ctx->amax.as<float>();
     SG_HIP(sgk::fill_f32(ones, 1.0f, batch, s));
     DevBuf y;
     SG_TRY(y.ensure(sizeof(float) * (size_t)batch * w->N));
-    hipError_t e = sgk::gemm_q8(ctx->f16.as<_Float16>(), ar, w->w, w->st, ones, y.as<float>(), sums, batch, w->N,
-                                w->K, s);
+    hipError_t e = sgk::gemm_q8(a8, ar, w->w8, w->st, ones, y.as<float>(), sums, batch, w->N, w->K, s);
     hipError_t e2 = hipStreamSynchronize(s);
     y.release();
     SG_HIP(e);
     SG_HIP(e2);
     return SG_OK;
   }
-  if (!row_scale) return fail(SG_ERR_INVALID, "row_scale is NULL");
-  if (batch >= sgk::kI8MinRows) {  // int8 operands, as the forward does at this size
-    int8_t* a8 = ctx->f16.as<int8_t>();
-    SG_HIP(sgk::i8_blocked(x, batch, w->K, a8, ar, s));
-    SG_HIP(sgk::gemm_q8_i8(a8, ar, w->w8, w->st, row_scale, dst, batch, w->N, w->K, s));
-  } else {
-    SG_HIP(sgk::i8_to_f16_blocked(x, batch, w->K, ctx->f16.as<_Float16>(), ar, s));
-    SG_HIP(sgk::gemm_q8(ctx->f16.as<_Float16>(), ar, w->w, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s));
-  }
+  SG_HIP(sgk::gemm_q8(a8, ar, w->w8, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s));
   return gemm_scratch_end(ctx, s);
 }
 
@@ -1027,17 +1006,11 @@ int sg_matmul_q8_0_int8_bench(sg_ctx* ctx, float* dst, const sg_q8_weight* w, co
   SG_TRY(set_device(ctx));
   hipStream_t s = pick(ctx, stream);
   const int ar = sgk::gemm_pad_rows(batch);
-  const bool i8 = batch >= sgk::kI8MinRows;
-  SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)ar * w->K));
+  SG_TRY(ctx->a8.ensure((size_t)ar * w->K));
   SG_TRY(gemm_scratch_begin(ctx, s));
-  if (i8)
-    SG_HIP(sgk::i8_blocked(x, batch, w->K, ctx->f16.as<int8_t>(), ar, s));
-  else
-    SG_HIP(sgk::i8_to_f16_blocked(x, batch, w->K, ctx->f16.as<_Float16>(), ar, s));
-  auto gemm = [&]() {
-    return i8 ? sgk::gemm_q8_i8(ctx->f16.as<int8_t>(), ar, w->w8, w->st, row_scale, dst, batch, w->N, w->K, s)
-              : sgk::gemm_q8(ctx->f16.as<_Float16>(), ar, w->w, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s);
-  };
+  int8_t* a8 = ctx->a8.as<int8_t>();
+  SG_HIP(sgk::i8_blocked(x, batch, w->K, a8, ar, s));
+  auto gemm = [&]() { return sgk::gemm_q8(a8, ar, w->w8, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s); };
   SG_HIP(gemm());  // warm
   hipEvent_t e0 = nullptr, e1 = nullptr;
   if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
@@ -1073,19 +1046,16 @@ int sg_ffn_gate_up(sg_ctx* ctx, float* dst, const sg_q8_weight* w_gate, const sg
   hipStream_t s = pick(ctx, stream);
   const int N = w_gate->N, K = w_gate->K, ar = sgk::gemm_pad_rows(batch);
   // Interleave gate and up rows in groups of 32 (the model does this at load).
-  // Block-major [K/32][N][32]: each 32-row group of one block is one 2-KB
-  // chunk (128 B of scales), and chunks of gate and up alternate.
-  // From kI8MinRows rows the int8 copies are interleaved (1-KB chunks) and the
-  // int8-operand GEMM runs, as in the forward.  The interleave is kept on the
-  // gate weight for its last (up weight, route) pair and rebuilt only when
-  // either changes; it is written on `s` after gemm_scratch_begin, so every
-  // later call (ordered after this one) sees it complete.
-  const bool i8 = batch >= sgk::kI8MinRows;
-  const size_t wch = (size_t)sgk::kGeluGroup * 32 * (i8 ? 1 : sizeof(_Float16)), sch = sgk::kGeluGroup * sizeof(float);
+  // Block-major [K/32][N][32]: each 32-row group of one block is one 1-KB
+  // chunk (128 B of scales), and chunks of gate and up alternate.  The
+  // interleave is kept on the gate weight for its last up weight and rebuilt
+  // only when that changes; it is written on `s` after gemm_scratch_begin, so
+  // every later call (ordered after this one) sees it complete.
+  const size_t wch = (size_t)sgk::kGeluGroup * 32, sch = sgk::kGeluGroup * sizeof(float);
   const size_t nch = (size_t)(K / 32) * (N / sgk::kGeluGroup);
-  SG_TRY(ctx->f16.ensure(sizeof(_Float16) * (size_t)ar * K));
+  SG_TRY(ctx->a8.ensure((size_t)ar * K));
   SG_TRY(gemm_scratch_begin(ctx, s));
-  const bool rebuild = w_gate->pair_up != w_up->id || w_gate->pair_i8 != (int)i8;
+  const bool rebuild = w_gate->pair_up != w_up->id;
   if (rebuild) {
     w_gate->pair_up = 0;  // invalid until the copies below are enqueued
     SG_TRY(w_gate->pair.ensure(2 * nch * (wch + sch)));
@@ -1093,25 +1063,16 @@ int sg_ffn_gate_up(sg_ctx* ctx, float* dst, const sg_q8_weight* w_gate, const sg
   uint8_t* wi = w_gate->pair.as<uint8_t>();
   uint8_t* si = wi + 2 * nch * wch;
   if (rebuild) {
-    const void* wg = i8 ? (const void*)w_gate->w8 : (const void*)w_gate->w;
-    const void* wu = i8 ? (const void*)w_up->w8 : (const void*)w_up->w;
-    SG_HIP(hipMemcpy2DAsync(wi, 2 * wch, wg, wch, wch, nch, hipMemcpyDeviceToDevice, s));
-    SG_HIP(hipMemcpy2DAsync(wi + wch, 2 * wch, wu, wch, wch, nch, hipMemcpyDeviceToDevice, s));
+    SG_HIP(hipMemcpy2DAsync(wi, 2 * wch, w_gate->w8, wch, wch, nch, hipMemcpyDeviceToDevice, s));
+    SG_HIP(hipMemcpy2DAsync(wi + wch, 2 * wch, w_up->w8, wch, wch, nch, hipMemcpyDeviceToDevice, s));
     SG_HIP(hipMemcpy2DAsync(si, 2 * sch, w_gate->st, sch, sch, nch, hipMemcpyDeviceToDevice, s));
     SG_HIP(hipMemcpy2DAsync(si + sch, 2 * sch, w_up->st, sch, sch, nch, hipMemcpyDeviceToDevice, s));
     w_gate->pair_up = w_up->id;
-    w_gate->pair_i8 = (int)i8;
   }
-  if (i8) {
-    int8_t* a8 = ctx->f16.as<int8_t>();
-    SG_HIP(sgk::i8_blocked(x, batch, K, a8, ar, s));
-    SG_HIP(sgk::gemm_q8_gelu_i8(a8, ar, reinterpret_cast<const int8_t*>(wi), reinterpret_cast<const float*>(si),
-                                row_scale, dst, batch, N, K, nullptr, nullptr, s));
-  } else {
-    SG_HIP(sgk::i8_to_f16_blocked(x, batch, K, ctx->f16.as<_Float16>(), ar, s));
-    SG_HIP(sgk::gemm_q8_gelu(ctx->f16.as<_Float16>(), ar, reinterpret_cast<const _Float16*>(wi),
-                             reinterpret_cast<const float*>(si), row_scale, dst, batch, N, K, nullptr, nullptr, s));
-  }
+  int8_t* a8 = ctx->a8.as<int8_t>();
+  SG_HIP(sgk::i8_blocked(x, batch, K, a8, ar, s));
+  SG_HIP(sgk::gemm_q8_gelu(a8, ar, reinterpret_cast<const int8_t*>(wi), reinterpret_cast<const float*>(si), row_scale,
+                           dst, batch, N, K, nullptr, nullptr, s));
   return gemm_scratch_end(ctx, s);
 }
 

@@ -115,16 +115,13 @@ struct HostBuf {
 struct sg_q8_weight {
   sg_ctx* ctx = nullptr;
   int N = 0, K = 0;
-  uint64_t id = 0;        // unique per created weight
-  _Float16* w = nullptr;  // block-major [K/32][N][32]
-  int8_t* w8 = nullptr;   // the same values as int8, same layout
-  float* st = nullptr;    // [K/32][N]
+  uint64_t id = 0;       // unique per created weight
+  int8_t* w8 = nullptr;  // block-major int8 [K/32][N][32]
+  float* st = nullptr;   // [K/32][N]
   // sg_ffn_gate_up with this weight as the gate: the gate/up interleave it
-  // last built (weights then scales), for the up weight with id pair_up on the
-  // int8 (pair_i8 = 1) or fp16 (0) operand route.
+  // last built (weights then scales), for the up weight with id pair_up.
   mutable sgi::DevBuf pair;
   mutable uint64_t pair_up = 0;
-  mutable int pair_i8 = -1;
 };
 
 #define SG_HIP(call)                                                                                     \

@@ -23,25 +23,22 @@ struct sg_attn_qpre {
 
 namespace sgk {
 
-// GEMM operands are block-major fp16 [K/32][rows][32]; activation buffers hold
+// GEMM operands are block-major int8 [K/32][rows][32]; activation buffers hold
 // gemm_pad_rows(M) rows per K-block so that every workgroup tile reads
 // allocated memory (rows past M are never stored).
 constexpr int kGemmRowPad = 256;
 inline int gemm_pad_rows(int M) { return (M + kGemmRowPad - 1) / kGemmRowPad * kGemmRowPad; }
 
 // ---- load-time repack (k_rows.hip) ----
-// Raw Q8_0 rows [rows][cols/32][34 B] -> block-major fp16 integer weights
-// w16[b][dst(r)][32] (ld rows per block), the same values as int8 in w8
-// (optional, same layout) and fp32 block scales (IEEE converter)
-// st[b][dst(r)] (ld per block), dst(r) = row_off + (r / grp) * gstride
-// + r % grp (grp = rows, gstride = 0: plain row_off + r).
-hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, _Float16* w16, int8_t* w8, float* st, int ld,
-                       int row_off, int grp, int gstride, hipStream_t s);
+// Raw Q8_0 rows [rows][cols/32][34 B] -> block-major int8 weights
+// w8[b][dst(r)][32] (ld rows per block) and fp32 block scales (IEEE
+// converter) st[b][dst(r)] (ld per block), dst(r) = row_off + (r / grp) *
+// gstride + r % grp (grp = rows, gstride = 0: plain row_off + r).
+hipError_t repack_q8_0(const uint8_t* raw, int rows, int cols, int8_t* w8, float* st, int ld, int row_off, int grp,
+                       int gstride, hipStream_t s);
 // token_embd: int8 values q[v][d] and per-block scales (gguf halving converter) sc[v][d/32].
 hipError_t repack_embd(const uint8_t* raw, int vocab, int d, int8_t* q, float* sc, hipStream_t s);
-// int8 x[M][K] -> block-major fp16 y[K/32][a_rows][32].
-hipError_t i8_to_f16_blocked(const int8_t* x, int M, int K, _Float16* y, int a_rows, hipStream_t s);
-// int8 x[M][K] -> block-major int8 y[K/32][a_rows][32] (gemm_q8_i8's operand).
+// int8 x[M][K] -> block-major int8 y[K/32][a_rows][32] (the GEMM operand).
 hipError_t i8_blocked(const int8_t* x, int M, int K, int8_t* y, int a_rows, hipStream_t s);
 hipError_t fill_f32(float* p, float v, int64_t n, hipStream_t s);
 hipError_t fill_i32(int32_t* p, int32_t v, int64_t n, hipStream_t s);
@@ -57,24 +54,15 @@ hipError_t embed_norm(const int32_t* tokens, int T, const int8_t* eq, const floa
                       float sqrt_d, const float* w, float eps, const int32_t* row_seq, float* h, float* xn,
                       float* amax, int32_t* err, hipStream_t s);
 // Per-sequence symmetric quantization of x[rows][cols] (stride ldx) using amax[row_seq[r]].
-// Writes fp16-encoded integers block-major f16[cols/32][a_rows][32] (f16 != null, the
-// GEMM operand) or int8 row-major i8[rows][cols] (i8 != null), and row_scale[rows].
+// Writes the int8 codes block-major q8[cols/32][a_rows][32] (q8 != null, the GEMM
+// operand) or row-major i8[rows][cols] (q8 == null), and row_scale[rows].
 hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
-                    _Float16* f16, int a_rows, int8_t* i8, float* row_scale, hipStream_t s);
+                    int8_t* q8, int a_rows, int8_t* i8, float* row_scale, hipStream_t s);
 // xn = RMSNorm(h; w) recomputed row by row exactly as post_res_norm / embed_norm
-// formed it, quantized with amax[row_seq[r]] into the block-major fp16 GEMM
-// operand f16[d/32][a_rows][32] and row_scale[T] (quantize's arithmetic).
+// formed it, quantized with amax[row_seq[r]] into the block-major int8 GEMM
+// operand q8[d/32][a_rows][32] and row_scale[T] (quantize's arithmetic).
 hipError_t norm_quantize(const float* h, const float* w, float eps, int T, int d, const int32_t* row_seq,
-                         const float* amax, _Float16* f16, int a_rows, float* row_scale, hipStream_t s);
-// int8-operand forms (gemm_q8_i8): the same codes stored as int8
-// q8[cols/32][a_rows][32].  quantize_i8 takes the forward's widths (768,
-// 1152) with 16-byte aligned rows.
-hipError_t norm_quantize_i8(const float* h, const float* w, float eps, int T, int d, const int32_t* row_seq,
-                            const float* amax, int8_t* q8, int a_rows, float* row_scale, hipStream_t s);
-hipError_t quantize_i8(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, const float* amax,
-                       int8_t* q8, int a_rows, float* row_scale, hipStream_t s);
-// Row widths quantize_i8 takes (other models keep the fp16-operand route).
-inline bool quantize_i8_width(int cols) { return cols == 768 || cols == 1152; }
+                         const float* amax, int8_t* q8, int a_rows, float* row_scale, hipStream_t s);
 hipError_t absmax_rows(const float* x, int ldx, int rows, int cols, const int32_t* row_seq, float* amax,
                        hipStream_t s);
 hipError_t seq_scales(const float* amax, int n_seq, float* out, hipStream_t s);
@@ -102,29 +90,21 @@ hipError_t embed_only(const int32_t* tokens, int T, const int8_t* eq, const floa
                       float sqrt_d, float* h, int32_t* err, hipStream_t s);
 
 // ---- GEMM (k_gemm.hip) ----
-// Y[M][N] = (sum_b float(P_b) * St[b][n]) * row_scale[m]; A fp16 [M][K], W fp16 [N][K].
-// sums != null additionally dumps the exact block sums int32 [M][N][K/32].
-// A block-major [K/32][a_rows][32] (a_rows >= gemm_pad_rows(M)), W block-major [K/32][N][32],
-// St [K/32][N].
-hipError_t gemm_q8(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* row_scale,
-                   float* Y, int32_t* sums, int M, int N, int K, hipStream_t s);
+// Y[M][N] = (sum_b float(P_b) * St[b][n]) * row_scale[m] with A int8 [M][K]
+// block-major [K/32][a_rows][32] (a_rows >= gemm_pad_rows(M)), W int8 [N][K]
+// block-major [K/32][N][32], St [K/32][N].  sums != null additionally dumps
+// the exact block sums int32 [M][N][K/32].
+hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
+                   int32_t* sums, int M, int N, int K, hipStream_t s);
 // FFN gate/up GEMM with GELUQuick(gate) * up in the epilogue: W holds 2*Nh rows,
-// gate and up interleaved in groups of 32 (see repack_q8_0's grouping);
+// gate and up interleaved in groups of kGeluGroup (see repack_q8_0's grouping);
 // G[M][Nh] is bit-identical to the unfused GEMMs + gelu_mul; amax (optional,
 // with row_seq) collects the sequences' max|g|.
-hipError_t gemm_q8_gelu(const _Float16* A, int a_rows, const _Float16* W, const float* St, const float* row_scale,
+hipError_t gemm_q8_gelu(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale,
                         float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s);
 // Gate/up interleaving used by gemm_q8_gelu: source row r of a matrix goes to
 // row row_off + (r / 32) * 64 + r % 32 (gate: row_off 0, up: row_off 32).
 constexpr int kGeluGroup = 32;
-// int8-operand forms of gemm_q8 / gemm_q8_gelu (same outputs, bit for bit):
-// A int8 [K/32][a_rows][32], W int8 [K/32][N][32].  The forward and the
-// kernel seam take them from kI8MinRows rows.
-constexpr int kI8MinRows = 4096;
-hipError_t gemm_q8_i8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
-                      int M, int N, int K, hipStream_t s);
-hipError_t gemm_q8_gelu_i8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale,
-                           float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s);
 
 // ---- attention (k_attention.hip) ----
 constexpr float kAttnQKScale = 8.0f;  // Q and K are split after scaling by 8 (exact)

@@ -61,22 +61,15 @@ extern "C" int sg_matmul_q8_0_int8_noalloc(sg_ctx* ctx, float* dst, const sg_q8_
     p = dev >= 0 && dev < kMaxDevices ? g_ptr[dev] : nullptr;
   }
   if (!p) return fail(SG_ERR_DEVICE, "scratch not set up for device %d (sg_init not called for it)", dev);
-  const bool i8 = batch >= sgk::kI8MinRows;
   const int ar = sgk::gemm_pad_rows(batch);
-  const size_t need = (size_t)ar * (size_t)w->K * (i8 ? 1 : sizeof(_Float16));
+  const size_t need = (size_t)ar * (size_t)w->K;
   if (need > SG_NOALLOC_SCRATCH_BYTES)
     return fail(SG_ERR_INVALID, "batch %d x in_dim %d needs %zu bytes of operand scratch; the limit is %u", batch,
                 w->K, need, (unsigned)SG_NOALLOC_SCRATCH_BYTES);
   SG_HIP(hipSetDevice(dev));
   const hipStream_t s = sgi::ctx_stream(ctx, stream);
-  if (i8) {  // int8 operands, as the forward does at this size
-    int8_t* a8 = static_cast<int8_t*>(p);
-    SG_HIP(sgk::i8_blocked(x, batch, w->K, a8, ar, s));
-    SG_HIP(sgk::gemm_q8_i8(a8, ar, w->w8, w->st, row_scale, dst, batch, w->N, w->K, s));
-  } else {
-    _Float16* a16 = static_cast<_Float16*>(p);
-    SG_HIP(sgk::i8_to_f16_blocked(x, batch, w->K, a16, ar, s));
-    SG_HIP(sgk::gemm_q8(a16, ar, w->w, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s));
-  }
+  int8_t* a8 = static_cast<int8_t*>(p);
+  SG_HIP(sgk::i8_blocked(x, batch, w->K, a8, ar, s));
+  SG_HIP(sgk::gemm_q8(a8, ar, w->w8, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s));
   return SG_OK;
 }

@@ -184,9 +184,9 @@ int sg_profile_read(sg_model *model, sg_profile *out);
  * return after their work on `stream` has completed. */
 
 /* Repacks one raw Q8_0 matrix [out_dim][in_dim/32][34 B] (host pointer) into
- * the device layouts used by the GEMM (fp16-encoded and int8 copies of the
- * values, 3 bytes per weight, plus the block scales).  in_dim must be a
- * multiple of 32.
+ * the device layout used by the GEMM (the int8 values block-major, one
+ * byte per weight, plus the fp32 block scales).  in_dim must be a multiple
+ * of 32.
  * (extractQ8_0Scales model_int8.go:543-569 + the weight bytes it views.) */
 int sg_q8_weight_create(sg_ctx *ctx, const void *q8, int32_t out_dim, int32_t in_dim,
                         sg_q8_weight **out);
@@ -213,9 +213,8 @@ int sg_matmul_q8_0_int8(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const in
  * array of SG_NOALLOC_SCRATCH_BYTES (resolved by sg_init, held until the
  * process ends) instead of a library-grown buffer.  No counterpart in the
  * reference: for callers that cannot allocate (HIP graph capture, serving
- * loops).  Limit: gemm_pad(batch) x in_dim bytes from 4096 rows (int8
- * operands), twice that below (fp16 operands), where gemm_pad rounds up to
- * 256 rows; larger inputs return SG_ERR_INVALID before any launch.  Calls
+ * loops).  Limit: gemm_pad(batch) x in_dim bytes, where gemm_pad rounds up
+ * to 256 rows; larger inputs return SG_ERR_INVALID before any launch.  Calls
  * that overlap on one device (e.g. on two streams) race on the array. */
 #define SG_NOALLOC_SCRATCH_BYTES (64u << 20)
 int sg_matmul_q8_0_int8_noalloc(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const int8_t *x,

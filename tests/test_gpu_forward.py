@@ -438,9 +438,9 @@ def test_config2_full_size_properties(full_gpu):
 
 def _batch_invariance(gpu, toks, off, out_dim, y, rows):
     """Each listed sequence embedded alone is bit-identical to its row of the packed batch.
-    A batch of 4096 tokens or more runs the int8-operand GEMMs and a sequence alone
-    (under 4096 tokens) the fp16-operand ones, so this also pins the two forms to
-    each other."""
+    The GEMM kernels are chosen by a sequence group's token count, so a sequence alone
+    and the packed batch often run different kernels: this also pins them to each
+    other."""
     for i in rows:
         a, b = int(off[i]), int(off[i + 1])
         alone = gpu.forward_packed(toks[a:b], np.array([0, b - a], np.int32), out_dim)[0]
@@ -476,22 +476,21 @@ def test_config4_full_size_properties(full_gpu):
     _batch_invariance(full_gpu, toks, off, 256, y, (0, 1, 100, 255))
 
 
-def test_operand_route_threshold(full_gpu):
-    """4096 packed tokens (the first size on the int8-operand GEMMs) against the
-    same sequences alone (fp16 operands) and 4095 tokens (fp16 operands): equal
-    bits for every shared sequence."""
+@pytest.mark.parametrize("lens,rows", [
+    ([1023, 1], (0, 1)),                          # T = 1024: gate/up leaves the register-direct kernel
+    ([2048, 1, 2047], (0, 1, 2)),                 # T = 4096: gate/up takes the 8-wave LDS kernel
+    ([2048] * 4 + [1] + [2048] * 4, (3, 4, 5, 8)),  # groups of 8192 and 8193 tokens: the other GEMMs switch
+])
+def test_gemm_kernel_thresholds(full_gpu, lens, rows):
+    """Packed batches whose sequence groups sit just past each GEMM kernel
+    threshold, against the same sequences alone (on the kernels below it):
+    equal bits for every listed sequence."""
     from semantica_gpu import synth
-    lens = [2048, 1, 2047]
     off = synth.offsets_from_lengths(lens)
     toks = synth.token_ids(int(off[-1]), 262144, seed=9)
-    say(f"operand route threshold lens={lens} (T={int(off[-1])})")
+    say(f"gemm kernel thresholds lens={lens} (T={int(off[-1])})")
     y = full_gpu.forward_packed(toks, off, 768)
-    _batch_invariance(full_gpu, toks, off, 768, y, range(3))
-    off2 = synth.offsets_from_lengths([2048, 2047])
-    toks2 = np.concatenate([toks[:2048], toks[2049:]])
-    y2 = full_gpu.forward_packed(toks2, off2, 768)
-    assert np.array_equal(y2[0].view(np.uint32), y[0].view(np.uint32))
-    assert np.array_equal(y2[1].view(np.uint32), y[2].view(np.uint32))
+    _batch_invariance(full_gpu, toks, off, 768, y, rows)
 
 
 def test_embed_texts_end_to_end(tiny_gpu, tiny_model):

@@ -77,9 +77,10 @@ def test_gemm_fp32_config1(gpu_ctx, oracle, N, K):
 
 def test_ffn_gate_up_interleave_cache(gpu_ctx):
     """sg_ffn_gate_up keeps the gate/up interleave on the gate weight and
-    rebuilds it only when the up weight or the operand route changes: one gate
-    with two up weights, alternating, on both routes (M = 40 and 4200) and back,
-    every call equal to the unfused GEMMs + GELU * up bit for bit."""
+    rebuilds it only when the up weight changes: one gate with two up weights,
+    alternating, on the register-direct (M = 40) and direct-to-LDS (M = 4200)
+    kernels and back, every call equal to the unfused GEMMs + GELU * up bit
+    for bit."""
     import torch
     from semantica_gpu import kernels, synth
     N, K = 256, 768
@@ -104,13 +105,15 @@ def test_ffn_gate_up_interleave_cache(gpu_ctx):
             w.close()
 
 
-@pytest.mark.parametrize("M,K", [(1, 768), (33, 768), (2048, 768), (4500, 768), (8200, 768), (4500, 800)])
+@pytest.mark.parametrize("M,K", [(1, 768), (33, 768), (1100, 800), (2048, 768), (4500, 768), (8200, 768),
+                                 (4500, 800)])
 def test_ffn_gate_up_fused_bit_exact(gpu_ctx, oracle, M, K):
     """The fused gate/up GEMM with GELUQuick * up in its epilogue equals the
     unfused GEMMs followed by the GELU kernel bit for bit, and the first rows
-    equal the oracle's block-serial GEMMs + geluquick * up.  From 4096 rows
-    both sides take the int8-operand kernels; K = 800 leaves a partial last
-    round of the ring-unrolled K loop."""
+    equal the oracle's block-serial GEMMs + geluquick * up.  The fused GEMM
+    runs register-direct below 1024 rows, then the 4-wave (6-stage ring) and
+    from 4096 rows the 8-wave direct-to-LDS kernel; K = 800 leaves a partial
+    last round of the ring-unrolled K loops."""
     import torch
     from semantica_gpu import kernels, synth
     N = 1152
@@ -145,8 +148,7 @@ def test_gemm_order_pins(gpu_ctx, M):
     column j hold pin i % 6's activations and pin j's weights, and the
     diagonal outputs must equal each pin's block-serial value exactly (which
     the VNNI, AVX2 and arm64 orders each miss on at least one pin).  M = 6
-    runs the register-direct kernel, 4104 and 8200 the two int8-operand
-    tilings."""
+    and 4104 run the register-direct kernel, 8200 the direct-to-LDS one."""
     import torch
     import gemm_pins
     from semantica_gpu import kernels, synth
@@ -216,11 +218,11 @@ def test_gemm_seam_async_across_streams(gpu_ctx, oracle):
         assert np.array_equal(got[::97].view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("M", [300, 4500])
+@pytest.mark.parametrize("M", [300, 8200])
 def test_gemm_unaligned_activations(gpu_ctx, M):
-    """int8 activations at an odd address take the byte-wise relayout (fp16
-    operands below 4096 rows, int8 operands from there): same bits as the
-    aligned call."""
+    """int8 activations at an odd address take the byte-wise relayout: same
+    bits as the aligned call (register-direct at 300 rows, direct-to-LDS at
+    8200)."""
     import torch
     from semantica_gpu import kernels, synth
     N, K = 768, 768
@@ -246,11 +248,11 @@ def test_gemm_unaligned_activations(gpu_ctx, M):
 @pytest.mark.parametrize("M", [4500, 8200])
 @pytest.mark.parametrize("N,K", [(1280, 768), (768, 1152), (768, 800)])
 def test_gemm_large_m(gpu_ctx, oracle, M, N, K):
-    """The direct-to-LDS kernels (8 waves x 128 columns at M = 8200 and at
-    4500 x 1280; 4 waves x 64 columns with a 6-stage ring at 4500 x 768;
-    ragged last tiles; K = 800 leaves 25 blocks, a partial last round of the
-    ring-unrolled K loop): first and last rows bit-exact to the block-serial
-    order, every row within 1e-5 of AVX2's."""
+    """Large M: 4500 rows on the register-direct kernel, 8200 on the 8-wave
+    direct-to-LDS kernel (256 x 128 tiles, 3-stage ring; ragged last tiles;
+    K = 800 leaves 25 blocks, a partial last round of the ring-unrolled K
+    loop): first and last rows bit-exact to the block-serial order, every row
+    within 1e-5 of AVX2's."""
     import torch
     from semantica_gpu import kernels, synth
     rng = np.random.default_rng(N + K)
