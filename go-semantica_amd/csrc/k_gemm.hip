@@ -413,20 +413,21 @@ hipError_t launch_lds(const int8_t* A, int a_rows, const int8_t* W, const float*
 namespace sgk {
 
 // Kernel choice by M (tile sweeps on MI355X at the model's shapes, M = 32 ..
-// 65536, with the forward's N and K): up to kRdMaxRows the register-direct
-// 64x64 tiles are fastest (no LDS, no barrier; the grid covers the chip);
-// above, the 8-wave direct-to-LDS kernel's 256x128 tiles.  The gate/up GEMM
-// (N = 2 x 1152, paired subtiles) takes register-direct 64x64 tiles below
-// 1024 rows, then 4-wave (128 x 64, 6-stage ring) and from 4096 rows 8-wave
-// direct-to-LDS tiles.
-constexpr int kRdMaxRows = 8192;
+// 65536, with the forward's N and K): below kRdRows the register-direct
+// 64x64 tiles are fastest (no LDS, no barrier; the grid covers the chip),
+// then the 4-wave direct-to-LDS kernel (128 x 64 tiles, 6-stage ring) and
+// from kLds8Rows the 8-wave one (256 x 128 tiles, 3-stage ring).  The
+// gate/up GEMM (N = 2 x 1152, paired subtiles) takes register-direct 64x64
+// tiles below 1024 rows, then 4-wave and from 4096 rows 8-wave tiles.
+constexpr int kRdRows = 6144, kLds8Rows = 12288;
 
 hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
                    int32_t* sums, int M, int N, int K, hipStream_t s) {
   if (M <= 0 || N <= 0) return hipSuccess;
   if (K <= 0 || K % 32) return hipErrorInvalidValue;
   if (sums) return launch_rd<1, 1, 1, 1, true>(A, a_rows, W, St, row_scale, Y, sums, M, N, K, s);
-  if (M <= kRdMaxRows) return launch_rd<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
+  if (M < kRdRows) return launch_rd<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
+  if (M < kLds8Rows) return launch_lds<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   return launch_lds<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
 }
 

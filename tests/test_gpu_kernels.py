@@ -142,13 +142,14 @@ def test_ffn_gate_up_fused_bit_exact(gpu_ctx, oracle, M, K):
     assert np.array_equal(g_host[:m].view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("M", [6, 4104, 8200])
+@pytest.mark.parametrize("M", [6, 8200, 12300])
 def test_gemm_order_pins(gpu_ctx, M):
     """The hand-derived order vectors of tests/gemm_pins.py: row i and
     column j hold pin i % 6's activations and pin j's weights, and the
     diagonal outputs must equal each pin's block-serial value exactly (which
     the VNNI, AVX2 and arm64 orders each miss on at least one pin).  M = 6
-    and 4104 run the register-direct kernel, 8200 the direct-to-LDS one."""
+    runs the register-direct kernel, 8200 the 4-wave and 12300 the 8-wave
+    direct-to-LDS kernel."""
     import torch
     import gemm_pins
     from semantica_gpu import kernels, synth
@@ -218,11 +219,11 @@ def test_gemm_seam_async_across_streams(gpu_ctx, oracle):
         assert np.array_equal(got[::97].view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("M", [300, 8200])
+@pytest.mark.parametrize("M", [300, 8200, 12300])
 def test_gemm_unaligned_activations(gpu_ctx, M):
     """int8 activations at an odd address take the byte-wise relayout: same
-    bits as the aligned call (register-direct at 300 rows, direct-to-LDS at
-    8200)."""
+    bits as the aligned call (register-direct at 300 rows, 4-wave
+    direct-to-LDS at 8200, 8-wave at 12300)."""
     import torch
     from semantica_gpu import kernels, synth
     N, K = 768, 768
@@ -245,14 +246,15 @@ def test_gemm_unaligned_activations(gpu_ctx, M):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("M", [4500, 8200])
+@pytest.mark.parametrize("M", [4500, 8200, 12300])
 @pytest.mark.parametrize("N,K", [(1280, 768), (768, 1152), (768, 800)])
 def test_gemm_large_m(gpu_ctx, oracle, M, N, K):
-    """Large M: 4500 rows on the register-direct kernel, 8200 on the 8-wave
-    direct-to-LDS kernel (256 x 128 tiles, 3-stage ring; ragged last tiles;
-    K = 800 leaves 25 blocks, a partial last round of the ring-unrolled K
-    loop): first and last rows bit-exact to the block-serial order, every row
-    within 1e-5 of AVX2's."""
+    """Large M: 4500 rows on the register-direct kernel, 8200 on the 4-wave
+    (128 x 64 tiles, 6-stage ring) and 12300 on the 8-wave (256 x 128 tiles,
+    3-stage ring) direct-to-LDS kernel; ragged last tiles; K = 800 leaves 25
+    blocks, a partial last round of the ring-unrolled K loops: first and last
+    rows bit-exact to the block-serial order, every row within 1e-5 of
+    AVX2's."""
     import torch
     from semantica_gpu import kernels, synth
     rng = np.random.default_rng(N + K)
