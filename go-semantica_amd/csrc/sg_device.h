@@ -299,17 +299,19 @@ __device__ __forceinline__ float sg_post_res_norm_row(const float* __restrict__ 
                                                       const float* __restrict__ w_post,
                                                       const float* __restrict__ w_next, float eps,
                                                       float* __restrict__ xrow, float* tile, int r, int j) {
-  f32x4_t x[NC];
+  // o and h are loaded together: one memory round trip before the first norm.
+  f32x4_t x[NC], hv[NC];
   const f32x4_t* op = reinterpret_cast<const f32x4_t*>(orow) + j;
-#pragma unroll
-  for (int c = 0; c < NC; c++) x[c] = op[8 * c];
-  if (w_post) sg_rmsnorm8_f4<NC>(x, w_post, tile, r, j, eps);
   f32x4_t* hp = reinterpret_cast<f32x4_t*>(hrow) + j;
 #pragma unroll
-  for (int c = 0; c < NC; c++) {
-    const f32x4_t hv = hp[8 * c];
+  for (int c = 0; c < NC; c++) x[c] = op[8 * c];
 #pragma unroll
-    for (int t = 0; t < 4; t++) x[c][t] = x[c][t] + hv[t];
+  for (int c = 0; c < NC; c++) hv[c] = hp[8 * c];
+  if (w_post) sg_rmsnorm8_f4<NC>(x, w_post, tile, r, j, eps);
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) x[c][t] = x[c][t] + hv[c][t];
     hp[8 * c] = x[c];
   }
   if (w_next) sg_rmsnorm8_f4<NC>(x, w_next, tile, r, j, eps);
