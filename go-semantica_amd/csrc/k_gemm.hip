@@ -150,14 +150,21 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
 
 // Register-direct kernel: every wave loads its own A and W fragments straight
 // from global memory (16 bytes per lane and operand per K-block, L1/L2
-// cached) into a register double buffer -- block b+1 is in flight while block
-// b computes -- with no LDS and no barrier in the K loop.  WM x WN waves per
-// workgroup, each owning TM x TN subtiles of 32x32 outputs.  A has a_rows
-// rows per K-block (>= the padded M the grid covers).  SUMS additionally
-// dumps the exact block sums int32 [M][N][K/32].  GELU (WN = 1, TN even): W
-// holds gate and up rows interleaved in groups of 32 (kGeluGroup), subtile
-// pairs (2p, 2p+1) of a wave are gate and up of the same features, and
-// gemm_epilogue writes g [M][N/2] with the sequences' max|g| in amax.
+// cached) into a ring of PF register stages -- blocks b+1 .. b+PF-1 are in
+// flight while block b computes -- with no LDS and no barrier in the K loop.
+// The prefetches are unconditional (past the last block they re-load block
+// nb-1, never computed): a load under a branch makes the compiler's wait
+// counting merge the two paths and wait for every load in flight, the
+// prefetch included.  The occupancy bound (two workgroups per CU) caps the
+// kernel at 256 VGPRs, which keeps the MFMA results in VGPRs; without it they
+// land in AGPRs and every one is copied back by a v_accvgpr_read before its
+// subtraction.  WM x WN waves per workgroup, each owning TM x TN subtiles of
+// 32x32 outputs.  A has a_rows rows per K-block (>= the padded M the grid
+// covers).  SUMS additionally dumps the exact block sums int32 [M][N][K/32].
+// GELU (WN = 1, TN even): W holds gate and up rows interleaved in groups of
+// 32 (kGeluGroup), subtile pairs (2p, 2p+1) of a wave are gate and up of the
+// same features, and gemm_epilogue writes g [M][N/2] with the sequences'
+// max|g| in amax.
 template <int TM, int TN>
 struct Stage {
   i32x4_t a[TM], w[TN];
@@ -204,8 +211,8 @@ __device__ __forceinline__ void compute(const Stage<TM, TN>& st, f32x16_t (&acc)
     }
 }
 
-template <int WM, int WN, int TM, int TN, bool SUMS, bool GELU>
-__global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8_rd(
+template <int WM, int WN, int TM, int TN, bool SUMS, bool GELU, int PF>
+__global__ __launch_bounds__(WM* WN* SG_WAVE, 2) void k_gemm_q8_rd(
     const int8_t* __restrict__ A, int a_rows, const int8_t* __restrict__ W, const float* __restrict__ St,
     const float* __restrict__ row_scale, float* __restrict__ Y, int32_t* __restrict__ sums, int M, int N, int K,
     const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
@@ -242,22 +249,35 @@ __global__ __launch_bounds__(WM* WN* SG_WAVE) void k_gemm_q8_rd(
       for (int r = 0; r < 16; r++) acc[tm][tn][r] = 0.0f;
   const i32x16_t bias = magic_bias();
 
-  Stage<TM, TN> s0, s1;
-  fetch<TM, TN>(s0, ap, wp, sp, 0, a_bstride, w_bstride, N);
+  // Ring of PF register stages: block b is in stage b % PF.  The prologue
+  // fetches blocks 0 .. PF-2; each step fetches block b + PF - 1 into the
+  // stage block b - 1 left, then computes block b.  The scheduling barrier
+  // keeps every prefetch ahead of the compute that follows it (the scheduler
+  // would otherwise sink the loads to their use and fold the stages into one
+  // register set).
+  Stage<TM, TN> st[PF];
+  static_for<0, PF - 1>([&](auto ic) {
+    constexpr int I = decltype(ic)::value;
+    fetch<TM, TN>(st[I], ap, wp, sp, min(I, nb - 1), a_bstride, w_bstride, N);
+  });
   int b = 0;
-  for (; b + 2 <= nb; b += 2) {
-    fetch<TM, TN>(s1, ap, wp, sp, b + 1, a_bstride, w_bstride, N);
-    compute<TM, TN, SUMS>(s0, acc, sums, M, N, nb, b, m_base, n_base, lr, lh, bias);
-    if (b + 2 < nb) fetch<TM, TN>(s0, ap, wp, sp, b + 2, a_bstride, w_bstride, N);
-    compute<TM, TN, SUMS>(s1, acc, sums, M, N, nb, b + 1, m_base, n_base, lr, lh, bias);
-  }
-  if (b < nb) compute<TM, TN, SUMS>(s0, acc, sums, M, N, nb, b, m_base, n_base, lr, lh, bias);
+  for (; b + PF <= nb; b += PF)
+    static_for<0, PF>([&](auto ic) {
+      constexpr int I = decltype(ic)::value;
+      fetch<TM, TN>(st[(I + PF - 1) % PF], ap, wp, sp, min(b + I + PF - 1, nb - 1), a_bstride, w_bstride, N);
+      __builtin_amdgcn_sched_barrier(0);
+      compute<TM, TN, SUMS>(st[I], acc, sums, M, N, nb, b + I, m_base, n_base, lr, lh, bias);
+    });
+  static_for<0, PF - 1>([&](auto ic) {  // the last nb % PF blocks, already in stages 0 ..
+    constexpr int I = decltype(ic)::value;
+    if (b + I < nb) compute<TM, TN, SUMS>(st[I], acc, sums, M, N, nb, b + I, m_base, n_base, lr, lh, bias);
+  });
 
   gemm_epilogue<WM, TM, TN, GELU>(acc, m_base, by, n_base, lr, lh, lane, wave, threadIdx.x, M, N, row_scale, Y,
                                   row_seq, amax);
 }
 
-template <int WM, int WN, int TM, int TN, bool SUMS, bool GELU = false>
+template <int WM, int WN, int TM, int TN, bool SUMS, bool GELU = false, int PF = 2>
 hipError_t launch_rd(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* rs, float* Y,
                      int32_t* sums, int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr,
                      float* amax = nullptr) {
@@ -265,7 +285,7 @@ hipError_t launch_rd(const int8_t* A, int a_rows, const int8_t* W, const float* 
   const int gm = (M + BM - 1) / BM;
   if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;  // A must cover the padded rows
   dim3 grid((N + BN - 1) / BN, gm);
-  hipLaunchKernelGGL((k_gemm_q8_rd<WM, WN, TM, TN, SUMS, GELU>), grid, dim3(WM * WN * SG_WAVE), 0, s, A, a_rows, W,
+  hipLaunchKernelGGL((k_gemm_q8_rd<WM, WN, TM, TN, SUMS, GELU, PF>), grid, dim3(WM * WN * SG_WAVE), 0, s, A, a_rows, W,
                      St, rs, Y, sums, M, N, K, row_seq, amax);
   return hipGetLastError();
 }
@@ -412,14 +432,21 @@ hipError_t launch_lds(const int8_t* A, int a_rows, const int8_t* W, const float*
 
 namespace sgk {
 
-// Kernel choice by M (tile sweeps on MI355X at the model's shapes, M = 32 ..
-// 65536, with the forward's N and K): below kRdRows the register-direct
-// 64x64 tiles are fastest (no LDS, no barrier; the grid covers the chip),
-// then the 4-wave direct-to-LDS kernel (128 x 64 tiles, 6-stage ring) and
-// from kLds8Rows the 8-wave one (256 x 128 tiles, 3-stage ring).  The
-// gate/up GEMM (N = 2 x 1152, paired subtiles) takes register-direct 64x64
-// tiles below 1024 rows, then 4-wave and from 4096 rows 8-wave tiles.
-constexpr int kRdRows = 6144, kLds8Rows = 12288;
+// Kernel choice by M, from tile sweeps on MI355X at the model's shapes
+// (M = 256 .. 32768, the forward's N and K) and, for the sizes where the
+// forward runs two sequence groups at once, from the two-group step time:
+// below kRdRows the register-direct 64x64 tiles (2x2 waves of 32x32), then
+// the 4-wave direct-to-LDS kernel (128 x 64 tiles, 6-stage ring) and from
+// kLds8Rows the 8-wave one (256 x 128 tiles, 3-stage ring).  Standalone the
+// register-direct 64x128 tiles beat both LDS kernels up to ~24k rows (QKV at
+// M = 16384: 43.3 vs 46.2 us), but two groups of 16384 tokens running them
+// side by side took 19.3 ms per config-2 step against 18.9 with the LDS
+// kernels: the LDS kernels read each operand tile from L2 once per workgroup,
+// the register-direct ones once per wave.  The gate/up GEMM (N = 2 x 1152,
+// gate and up subtiles paired in one wave) takes register-direct 4-wave
+// 128 x 64 tiles below kGeluLdsRows rows (sizes that only occur as one
+// group: 22.0 vs 26.3 us at M = 2048), then the 8-wave kernel.
+constexpr int kRdRows = 6144, kLds8Rows = 12288, kGeluLdsRows = 4096;
 
 hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
                    int32_t* sums, int M, int N, int K, hipStream_t s) {
@@ -436,10 +463,9 @@ hipError_t gemm_q8_gelu(const int8_t* A, int a_rows, const int8_t* W, const floa
   if (M <= 0 || Nh <= 0) return hipSuccess;
   if (K <= 0 || K % 32 || Nh % 32) return hipErrorInvalidValue;
   if (amax && !row_seq) return hipErrorInvalidValue;
-  if (M < 1024)
-    return launch_rd<2, 1, 1, 2, false, true>(A, a_rows, W, St, row_scale, G, nullptr, M, 2 * Nh, K, s, row_seq,
+  if (M < kGeluLdsRows)
+    return launch_rd<4, 1, 1, 2, false, true>(A, a_rows, W, St, row_scale, G, nullptr, M, 2 * Nh, K, s, row_seq,
                                               amax);
-  if (M < 4096) return launch_lds<4, 2, true, 6>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
   return launch_lds<8, 4, true, 3>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
 }
 

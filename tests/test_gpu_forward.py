@@ -477,8 +477,7 @@ def test_config4_full_size_properties(full_gpu):
 
 
 @pytest.mark.parametrize("lens,rows", [
-    ([1023, 1], (0, 1)),                          # T = 1024: gate/up leaves the register-direct kernel
-    ([2048, 1, 2047], (0, 1, 2)),                 # T = 4096: gate/up takes the 8-wave LDS kernel
+    ([2048, 1, 2047], (0, 1, 2)),                         # T = 4096: gate/up on the 8-wave LDS kernel
     ([2048, 2048, 2047, 1, 2048, 2048, 2048], (2, 3, 4)),  # two groups of 6144: the 4-wave LDS kernel
 ])
 def test_gemm_kernel_thresholds(full_gpu, lens, rows):

@@ -78,9 +78,8 @@ def test_gemm_fp32_config1(gpu_ctx, oracle, N, K):
 def test_ffn_gate_up_interleave_cache(gpu_ctx):
     """sg_ffn_gate_up keeps the gate/up interleave on the gate weight and
     rebuilds it only when the up weight changes: one gate with two up weights,
-    alternating, on the register-direct (M = 40) and direct-to-LDS (M = 4200)
-    kernels and back, every call equal to the unfused GEMMs + GELU * up bit
-    for bit."""
+    alternating, at M = 40 and 4200 and back, every call equal to the unfused
+    GEMMs + GELU * up bit for bit."""
     import torch
     from semantica_gpu import kernels, synth
     N, K = 256, 768
@@ -111,9 +110,10 @@ def test_ffn_gate_up_fused_bit_exact(gpu_ctx, oracle, M, K):
     """The fused gate/up GEMM with GELUQuick * up in its epilogue equals the
     unfused GEMMs followed by the GELU kernel bit for bit, and the first rows
     equal the oracle's block-serial GEMMs + geluquick * up.  The fused GEMM
-    runs register-direct below 1024 rows, then the 4-wave (6-stage ring) and
-    from 4096 rows the 8-wave direct-to-LDS kernel; K = 800 leaves a partial
-    last round of the ring-unrolled K loops."""
+    runs register-direct below 4096 rows and on the 8-wave direct-to-LDS
+    kernel from there; K = 800 leaves 25 blocks (an odd last block after the
+    register-direct block pairs, a partial last round of the ring-unrolled
+    LDS loop)."""
     import torch
     from semantica_gpu import kernels, synth
     N = 1152
@@ -252,9 +252,10 @@ def test_gemm_large_m(gpu_ctx, oracle, M, N, K):
     """Large M: 4500 rows on the register-direct kernel, 8200 on the 4-wave
     (128 x 64 tiles, 6-stage ring) and 12300 on the 8-wave (256 x 128 tiles,
     3-stage ring) direct-to-LDS kernel; ragged last tiles; K = 800 leaves 25
-    blocks, a partial last round of the ring-unrolled K loops: first and last
-    rows bit-exact to the block-serial order, every row within 1e-5 of
-    AVX2's."""
+    blocks (an odd last block after the register-direct block pairs, a
+    partial last round of the ring-unrolled LDS loops): the first and last
+    128 rows bit-exact to the block-serial order, every 7th row within 1e-5
+    of AVX2's."""
     import torch
     from semantica_gpu import kernels, synth
     rng = np.random.default_rng(N + K)
@@ -270,7 +271,8 @@ def test_gemm_large_m(gpu_ctx, oracle, M, N, K):
     for lo, hi in ((0, 128), (M - 128, M)):
         ref = oracle.matmul(raw, xq[lo:hi], rs[lo:hi], N, oracle.ORDER_BLOCK_SERIAL)
         assert np.array_equal(got[lo:hi].view(np.uint32), ref.view(np.uint32))
-    assert rel_err(got, oracle.matmul(raw, xq, rs, N, oracle.ORDER_AVX2)) <= 1e-5
+    sub = np.arange(0, M, 7)
+    assert rel_err(got[sub], oracle.matmul(raw, xq[sub], rs[sub], N, oracle.ORDER_AVX2)) <= 1e-5
 
 
 @pytest.mark.parametrize("cols", [768, 1152])

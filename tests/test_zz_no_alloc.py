@@ -33,7 +33,7 @@ def test_noalloc_matches_matmul_two_calls(gpu_ctx, sizes):
     """Two calls in a row, the second with a smaller input (so the shared
     scratch still holds the first call's operand past the second's rows):
     each output equals the allocating entry point's bit for bit.  8200 rows
-    take a direct-to-LDS kernel and 300 / 3000 / 33 the register-direct one."""
+    take the 4-wave direct-to-LDS kernel and 300 / 3000 / 33 the register-direct one."""
     from semantica_gpu import kernels, synth
     N, K = 1152, 768
     rng = np.random.default_rng(sizes[0])
