@@ -94,8 +94,10 @@ __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bq
     const float* src = qp.q + (int64_t)qr * qp.ldq + head * kHD + 8 * g4;
 #pragma unroll
     for (int ks = 0; ks < kHD / 32; ks++) {
-      *reinterpret_cast<f32x4_t*>(&x[ks][0]) = *reinterpret_cast<const f32x4_t*>(src + 32 * ks);
-      *reinterpret_cast<f32x4_t*>(&x[ks][4]) = *reinterpret_cast<const f32x4_t*>(src + 32 * ks + 4);
+      // The fp32 Q row's last read: non-temporal, leaving L2 to the K/V tiles.
+      const f32x4_t* s4 = reinterpret_cast<const f32x4_t*>(src + 32 * ks);
+      *reinterpret_cast<f32x4_t*>(&x[ks][0]) = __builtin_nontemporal_load(s4);
+      *reinterpret_cast<f32x4_t*>(&x[ks][4]) = __builtin_nontemporal_load(s4 + 1);
     }
     if (qp.w) {
 #pragma unroll

@@ -226,7 +226,9 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
   f32x4_t x[NC];
   const f32x4_t* hr = reinterpret_cast<const f32x4_t*>(h + (int64_t)row * D) + j;
 #pragma unroll
-  for (int c = 0; c < NC; c++) x[c] = hr[8 * c];
+  // Non-temporal: h is next read after the following GEMMs, and L2 is better
+  // left to the operands they re-read (two sequence groups share it).
+  for (int c = 0; c < NC; c++) x[c] = __builtin_nontemporal_load(&hr[8 * c]);
   sg_rmsnorm8_f4<NC>(x, w, tiles[threadIdx.x / SG_WAVE], r, j, eps);
   const float m = amax[row_seq[row]];
   float scale = 1.0f, inv = 0.0f;
@@ -267,9 +269,9 @@ __global__ __launch_bounds__(kThreads) void k_quantize_blocked(const float* __re
   }
   if (j == 0) row_scale[row] = scale;
   const f32x4_t* xr = reinterpret_cast<const f32x4_t*>(x + (int64_t)row * ldx) + j;
-  f32x4_t v[NC];  // every load in flight before the first store
+  f32x4_t v[NC];  // every load in flight before the first store; last use of x: non-temporal
 #pragma unroll
-  for (int c = 0; c < NC; c++) v[c] = xr[8 * c];
+  for (int c = 0; c < NC; c++) v[c] = __builtin_nontemporal_load(&xr[8 * c]);
   int8_t* qr = qf + (int64_t)row * 32 + 4 * j;
 #pragma unroll
   for (int c = 0; c < NC; c++) {

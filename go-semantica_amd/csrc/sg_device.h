@@ -300,13 +300,16 @@ __device__ __forceinline__ float sg_post_res_norm_row(const float* __restrict__ 
                                                       const float* __restrict__ w_next, float eps,
                                                       float* __restrict__ xrow, float* tile, int r, int j) {
   // o and h are loaded together: one memory round trip before the first norm.
+  // Both are last-use reads (h is rewritten below), so they go non-temporal
+  // and leave L2 to the operands other kernels re-read; the forward's two
+  // sequence groups share the cache.
   f32x4_t x[NC], hv[NC];
   const f32x4_t* op = reinterpret_cast<const f32x4_t*>(orow) + j;
   f32x4_t* hp = reinterpret_cast<f32x4_t*>(hrow) + j;
 #pragma unroll
-  for (int c = 0; c < NC; c++) x[c] = op[8 * c];
+  for (int c = 0; c < NC; c++) x[c] = __builtin_nontemporal_load(&op[8 * c]);
 #pragma unroll
-  for (int c = 0; c < NC; c++) hv[c] = hp[8 * c];
+  for (int c = 0; c < NC; c++) hv[c] = __builtin_nontemporal_load(&hp[8 * c]);
   if (w_post) sg_rmsnorm8_f4<NC>(x, w_post, tile, r, j, eps);
 #pragma unroll
   for (int c = 0; c < NC; c++) {

@@ -38,8 +38,10 @@ __device__ __forceinline__ void qk_split_group(int64_t g, int j, int r, float* t
   const int t = (int)(g / per), hh = (int)(g % per);
   const float* src = hh < H ? q + (int64_t)t * ldq + hh * 256 : k + (int64_t)t * ldk + (hh - H) * 256;
   f32x4_t x[NC];
+  // The fp32 Q/K row's last read: non-temporal, leaving L2 to re-read operands.
 #pragma unroll
-  for (int c = 0; c < NC; c++) x[c] = *reinterpret_cast<const f32x4_t*>(src + 32 * c + 4 * j);
+  for (int c = 0; c < NC; c++)
+    x[c] = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(src + 32 * c + 4 * j));
   const float* wn = hh < H ? qw : kw;
   if (wn) sg_rmsnorm8_f4<NC>(x, wn, tile, r, j, eps);
   const int pos = row_pos[t];
@@ -100,7 +102,9 @@ __device__ __forceinline__ void v_split_tile(sg_item t, int kvh, float (*tv)[kVt
     const int idx = tid + kKvThreads * u;
     const int key = idx >> 6, d4 = idx & 63;
     f32x4_t x = {0, 0, 0, 0};
-    if (k0 + key < S) x = *reinterpret_cast<const f32x4_t*>(v + (int64_t)(r0 + k0 + key) * ldv + kvh * kHD + 4 * d4);
+    if (k0 + key < S)  // the fp32 V row's last read: non-temporal
+      x = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4_t*>(v + (int64_t)(r0 + k0 + key) * ldv + kvh * kHD + 4 * d4));
     *reinterpret_cast<f32x4_t*>(&tv[key][4 * d4]) = x;
   }
   __syncthreads();
