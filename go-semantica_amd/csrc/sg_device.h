@@ -45,16 +45,30 @@ __device__ __forceinline__ float sg_fast_exp_nonpos(float x) {
   return x < -10.0f ? 0.0f : r;
 }
 
+// n / d for the sigmoid's operands (d = 1 + e in [1, 2], n in {1, e}): the
+// hardware reciprocal, one Newton-Raphson step, then the quotient corrected
+// by its exact FMA residual (Markstein's scheme).  Six instructions instead
+// of the eleven of the general IEEE sequence, whose scaling and fix-up steps
+// only matter for denormal, huge or special operands.  sg_gelu_quick's result
+// with it equals the one with the IEEE division for every one of the 2^32
+// float inputs (exhaustive comparison on MI355X).
+__device__ __forceinline__ float sg_div_sigmoid(float n, float d) {
+  float r = __builtin_amdgcn_rcpf(d);
+  r = __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+  const float q = n * r;
+  return __builtin_fmaf(__builtin_fmaf(-d, q, n), r, q);
+}
+
 // GELUQuickSIMD element, activation.go:55-75: x * sigmoid(1.702 x) with the
 // sign-split sigmoid: sx >= 0 -> 1/(1 + fastExp(-sx)), else e/(1 + e) with
 // e = fastExp(sx).  Both branches evaluate fastExp at -|sx| and differ only
-// in the numerator, so one exp and one (IEEE) division give the same bits
-// without divergent branches.
+// in the numerator, so one exp and one correctly rounded division give the
+// same bits without divergent branches.
 __device__ __forceinline__ float sg_gelu_quick(float x) {
   const float sx = 1.702f * x;
   const float e = sg_fast_exp_nonpos(-fabsf(sx));
   const float num = sx >= 0.0f ? 1.0f : e;
-  return x * (num / (1.0f + e));
+  return x * sg_div_sigmoid(num, 1.0f + e);
 }
 
 // fp16 -> fp32 with subnormal support, internal/runtime/model_int8.go:571-597.

@@ -476,6 +476,24 @@ def test_gelu_quick_mul_bit_exact(gpu_ctx, oracle):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
+def test_gelu_quick_float_sweep_bit_exact(gpu_ctx, oracle):
+    """GELUQuick on every 256th float32 bit pattern (2^24 values: every
+    exponent, both signs, subnormals, infinities, NaNs) times up = 1, against
+    the oracle bit for bit (any NaN matches any NaN).  Pins the short
+    correctly rounded division of the sigmoid over the whole input range."""
+    import torch
+    from semantica_gpu import kernels
+    gate = (np.arange(1 << 24, dtype=np.uint64) * 256).astype(np.uint32).view(np.float32).reshape(16384, 1024)
+    up = np.ones_like(gate)
+    say("gelu_quick float sweep 2^24 values")
+    out = torch.empty(gate.shape, dtype=torch.float32, device="cuda")
+    kernels.gelu_quick_mul(gpu_ctx, out, dev(gate), dev(up))
+    got = host(out)
+    ref = oracle.gelu_quick(gate)
+    same = (got.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(got) & np.isnan(ref))
+    assert same.all(), gate.ravel()[~same.ravel()][:8]
+
+
 @pytest.mark.parametrize("out_dim", [768, 256, 1])
 def test_pool_l2_bit_exact(gpu_ctx, oracle, out_dim):
     import torch
