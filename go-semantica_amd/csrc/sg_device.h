@@ -34,11 +34,13 @@ __device__ __forceinline__ float sg_fast_exp(float x) {
 // fastExp for softmax arguments x = s - max <= 0, branch-free.  Same value as
 // sg_fast_exp on (-inf, 0]: below -10 it is 0; otherwise y = x*log2e lies in
 // [-14.43, 0], so the integer part is in [-14, 0] and poly * 2^ip is exact,
-// which ldexp computes without building exponent bits.
+// which ldexp computes without building exponent bits.  float(int(y)) is
+// truncf(y) for |y| < 2^31 (a full-rate v_trunc_f32 instead of a half-rate
+// int -> float convert).
 __device__ __forceinline__ float sg_fast_exp_nonpos(float x) {
   const float y = x * 1.442695041f;
   const int ip = (int)y;
-  const float f = y - (float)ip;
+  const float f = y - __builtin_truncf(y);
   const float poly =
       1.0f + f * (0.693147180559945f + f * (0.240226506959101f + f * (0.055504108664821f + f * 0.009676036358193f)));
   const float r = __builtin_amdgcn_ldexpf(poly, ip);
