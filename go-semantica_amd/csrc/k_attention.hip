@@ -50,12 +50,6 @@ constexpr int kBK = 32;             // keys per tile
 constexpr int kQW = 16;             // (head, query) rows per wave
 constexpr int kWaves = sgk::kAttnChunks;
 constexpr int kNT = kWaves * SG_WAVE;
-// LDS row strides (halves).  For 16x16x32 operand reads (16 rows x 4 lane
-// groups of 16 B per ds_read_b128) rows of 544 B and 96 B are conflict-free
-// on gfx950, while 528 B and 80 B rows cost 1.6x (measured with a one-CU
-// ds_read_b128 throughput probe).
-constexpr int kKStride = kHD + 16;
-constexpr int kVStride = kBK + 16;
 constexpr float kQKScale = sgk::kAttnQKScale;
 constexpr float kPScale = 1024.0f, kPUnscale = 1.0f / 1024.0f;
 static_assert(sgk::kAttnChunkRows == kQW, "host chunking must match the kernel");
@@ -69,8 +63,6 @@ __device__ __forceinline__ f32x4_t mfma16(half8_t a, half8_t b, f32x4_t c) {
 // O^T += V^T P^T step.
 
 constexpr int kRegTiles = sgk::kAttnRegKeys / kBK;
-constexpr int kKBuf = 2 * kBK * kKStride;  // halves of one K tile buffer [hi/lo][key][dim]
-constexpr int kVBuf = 2 * kHD * kVStride;  // halves of one V^T tile buffer [hi/lo][dim][key]
 
 // Q^T as the B operand of one wave's 16 (head, query) rows: lane (query ln,
 // group g4), k-step ks holds dims 32ks + 8g4 .. + 7 of row qr, scaled by 8
@@ -181,248 +173,6 @@ __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bq
   }
 }
 
-// Sequences longer than kRegTiles tiles: pass 2 recomputes S^T.  One K and
-// one V^T buffer, tiles staged through registers.
-template <bool QPRE>
-__global__ __launch_bounds__(kNT, 2) void k_attn(
-    const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
-    const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vt, int ldvt, float* __restrict__ out, int ldo, const int32_t* __restrict__ seq_off,
-    const int32_t* __restrict__ voff, const sg_item* __restrict__ items, int G, float sscale,
-    float* __restrict__ amax, sg_attn_qpre qp) {
-  __shared__ __attribute__((aligned(16))) _Float16 lds[kKBuf + kVBuf];
-  __shared__ float red[kWaves];
-  auto kbuf = [&](int) { return lds; };
-  auto vbuf = [&](int) { return lds + kKBuf; };
-
-  const sg_item it = items[blockIdx.x];
-  const int kvh = blockIdx.y;
-  const int r0 = seq_off[it.seq];
-  const int S = seq_off[it.seq + 1] - r0;
-  const int vo = voff[it.seq];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int ln = lane & 15, g4 = lane >> 4;
-  const int nqb = (S + kQW - 1) / kQW;
-  const int c = it.c0 + w;
-  const bool active = c < G * nqb;  // wave-uniform
-  const int hg = active ? c / nqb : 0;
-  const int q0 = active ? (c % nqb) * kQW : 0;
-  const int head = kvh * G + hg;
-  const int qrow = q0 + ln;
-  const bool qvalid = active && qrow < S;
-
-  // Q^T as the B operand: lane (query ln, group g4), k-step c: dims 32c+8g4..+8.
-  half8_t bqh[kHD / 32], bql[kHD / 32];
-  const int qr = r0 + min(qrow, S - 1);
-
-  // Tile staging through registers: 2048 16-B chunks per tile, 4 per thread.
-  // K chunk u: hi/lo u>>1, key (tid>>5) + 16(u&1), dims 8(tid&31)..+8.
-  // V^T chunk u: hi/lo u>>1, dim (tid>>2) + 128(u&1), keys 8(tid&3)..+8.
-  half8_t stg[4];
-  const _Float16* kbase_h = kh + kvh * kHD + 8 * (tid & 31);
-  const _Float16* kbase_l = kl + kvh * kHD + 8 * (tid & 31);
-  auto load_k = [&](int kt) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int key = (tid >> 5) + 16 * (u & 1);
-      const int64_t row = r0 + min(kt + key, S - 1);
-      stg[u] = *reinterpret_cast<const half8_t*>(((u >> 1) ? kbase_l : kbase_h) + row * ldk);
-    }
-  };
-  auto store_k = [&](_Float16* kb) {
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-      *reinterpret_cast<half8_t*>(kb + ((u >> 1) * kBK + (tid >> 5) + 16 * (u & 1)) * kKStride + 8 * (tid & 31)) =
-          stg[u];
-  };
-  // V^T tile at column c of a dim row: halves 2c .. 2c+31 hi, 2c+32 .. 2c+63 lo.
-  const int64_t vrow0 = (int64_t)(kvh * kHD + (tid >> 2)) * ldvt + 2 * vo + 8 * (tid & 3);
-  auto load_v = [&](int kt) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int64_t o = vrow0 + (int64_t)(128 * (u & 1)) * ldvt + 2 * kt + 32 * (u >> 1);
-      stg[u] = *reinterpret_cast<const half8_t*>(vt + o);
-    }
-  };
-  auto store_v = [&](_Float16* vb) {
-#pragma unroll
-    for (int u = 0; u < 4; u++)
-      *reinterpret_cast<half8_t*>(vb + ((u >> 1) * kHD + (tid >> 2) + 128 * (u & 1)) * kVStride + 8 * (tid & 3)) =
-          stg[u];
-  };
-
-  // S^T subtiles 0 and 1 of a tile (keys 0..15 and 16..31 x 16 queries),
-  // scaled by 64: lane holds query ln and keys 16st + 4g4 + r in register r.
-  // Each subtile's accumulator takes ah.bh, ah.bl, al.bh of k-step ks in that
-  // order.  Reads run half a step ahead: subtile 1's K fragments of ks are
-  // read before subtile 0's MFMAs of ks, subtile 0's of ks + 1 before
-  // subtile 1's MFMAs (the scheduling groups pin that order), so each read's
-  // latency hides behind three MFMAs with two fragment pairs live.
-  auto scores2 = [&](const _Float16* kb, f32x4_t& a0, f32x4_t& a1) {
-    const _Float16* p0 = kb + ln * kKStride + 8 * g4;
-    auto rd = [&](int st, int ks, half8_t& h, half8_t& l) {
-      h = *reinterpret_cast<const half8_t*>(p0 + 16 * st * kKStride + 32 * ks);
-      l = *reinterpret_cast<const half8_t*>(p0 + (kBK + 16 * st) * kKStride + 32 * ks);
-    };
-    a0 = f32x4_t{0, 0, 0, 0};
-    a1 = f32x4_t{0, 0, 0, 0};
-    half8_t h0, l0, h1, l1;
-    rd(0, 0, h0, l0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-    for (int ks = 0; ks < kHD / 32; ks++) {
-      rd(1, ks, h1, l1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      a0 = mfma16(h0, bqh[ks], a0);
-      a0 = mfma16(h0, bql[ks], a0);
-      a0 = mfma16(l0, bqh[ks], a0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-      if (ks + 1 < kHD / 32) {
-        rd(0, ks + 1, h0, l0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
-      a1 = mfma16(h1, bqh[ks], a1);
-      a1 = mfma16(h1, bql[ks], a1);
-      a1 = mfma16(l1, bqh[ks], a1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-    }
-  };
-  auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
-  // Pass-1 max over one tile's scores (keys past S only in a sequence's last tile).
-  auto tile_max = [&](float m, int kt, const f32x4_t& a0, const f32x4_t& a1) {
-    if (kt + kBK <= S) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) m = fmaxf(m, fmaxf(a0[r], a1[r]));
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        m = key_of(kt, 0, r) < S ? fmaxf(m, a0[r]) : m;
-        m = key_of(kt, 1, r) < S ? fmaxf(m, a1[r]) : m;
-      }
-    }
-    return m;
-  };
-  // Pass-2 weights of one tile: e = fastExp(s - m), row sum, split P^T.
-  auto weights = [&](int kt, const f32x4_t& a0, const f32x4_t& a1, float m, float& lsum, half8_t& ph,
-                     half8_t& pl) {
-    const bool full = kt + kBK <= S;
-#pragma unroll
-    for (int st = 0; st < 2; st++) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        float e = sg_fast_exp_nonpos((st ? a1[r] : a0[r]) * sscale - m);
-        if (!full) e = key_of(kt, st, r) < S ? e : 0.0f;
-        lsum = lsum + e;
-        const hl16 p = split_f16(e * kPScale);
-        ph[4 * st + r] = p.hi;
-        pl[4 * st + r] = p.lo;
-      }
-    }
-  };
-  // O^T += V^T P^T for one tile, the V^T fragments of dim tile mt + 2 read
-  // from LDS while the MFMAs of mt run.
-  auto pv = [&](f32x4_t* o, const _Float16* vb, const half8_t& ph, const half8_t& pl) {
-    const _Float16* p0 = vb + ln * kVStride + 8 * g4;
-    half8_t fr[3][2];  // [buffer][hi, lo]
-    auto rd = [&](int mt, half8_t(&f)[2]) {
-      f[0] = *reinterpret_cast<const half8_t*>(p0 + 16 * mt * kVStride);
-      f[1] = *reinterpret_cast<const half8_t*>(p0 + (kHD + 16 * mt) * kVStride);
-    };
-    rd(0, fr[0]);
-    rd(1, fr[1]);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-    for (int mt = 0; mt < kHD / 16; mt++) {
-      if (mt + 2 < kHD / 16) {
-        rd(mt + 2, fr[(mt + 2) % 3]);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
-      const half8_t(&f)[2] = fr[mt % 3];
-      o[mt] = mfma16(f[0], ph, o[mt]);
-      o[mt] = mfma16(f[0], pl, o[mt]);
-      o[mt] = mfma16(f[1], ph, o[mt]);
-      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-    }
-  };
-
-  // ---- pass 1: row max ----
-  // Max of the raw (x64) scores; scaling by the power of two sscale commutes
-  // with max exactly.  Keys past S only occur in a sequence's last tile.
-  float m = -INFINITY;
-  load_k(0);  // in flight while Q is prepared
-  q_operand<QPRE>(bqh, bql, qh, ql, ldq, qp, qr, head, ln, g4, lane, reinterpret_cast<float*>(lds) + w * (16 * 40));
-  f32x4_t o[kHD / 16];
-#pragma unroll
-  for (int mt = 0; mt < kHD / 16; mt++) o[mt] = f32x4_t{0, 0, 0, 0};
-  float lsum = 0.0f;
-  {
-    for (int kt = 0; kt < S; kt += kBK) {
-      __syncthreads();  // every wave is done with the previous tile
-      store_k(kbuf(0));
-      __syncthreads();
-      if (kt + kBK < S) load_k(kt + kBK);  // in flight during the MFMAs
-      if (active) {
-        f32x4_t a0, a1;
-        scores2(kbuf(0), a0, a1);
-        m = tile_max(m, kt, a0, a1);
-      }
-    }
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
-
-    // ---- pass 2: e = fastExp(s - m), row sums, O^T += V^T P^T ----
-    load_k(0);
-    __syncthreads();  // pass 1's last tile is consumed
-    store_k(kbuf(0));
-    __syncthreads();
-    for (int kt = 0; kt < S; kt += kBK) {
-      load_v(kt);  // in flight during the score MFMAs
-      half8_t ph, pl;
-      if (active) {
-        f32x4_t a0, a1;
-        scores2(kbuf(0), a0, a1);
-        weights(kt, a0, a1, m, lsum, ph, pl);
-      }
-      store_v(vbuf(0));
-      __syncthreads();  // V^T tile staged; K tile free
-      const bool more = kt + kBK < S;
-      if (more) load_k(kt + kBK);  // in flight during the P.V MFMAs
-      if (active) pv(o, vbuf(0), ph, pl);
-      if (more) store_k(kbuf(0));  // nobody reads the K buffer between the two barriers
-      __syncthreads();             // K tile staged; V^T tile free
-    }
-  }
-  lsum = lsum + __shfl_xor(lsum, 16);
-  lsum = lsum + __shfl_xor(lsum, 32);
-  const float f = (1.0f / lsum) * kPUnscale;
-
-  // O^T tile mt: lane holds query ln, dims 16mt + 4g4 + r.
-  float mx = 0.0f;
-  if (qvalid) {
-    float* op = out + (int64_t)(r0 + qrow) * ldo + head * kHD + 4 * g4;
-#pragma unroll
-    for (int mt = 0; mt < kHD / 16; mt++) {
-      f32x4_t y;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        y[j] = o[mt][j] * f;
-        mx = fmaxf(mx, fabsf(y[j]));
-      }
-      *reinterpret_cast<f32x4_t*>(op + 16 * mt) = y;
-    }
-  }
-  if (amax) {  // all chunks of a workgroup belong to one sequence
-    mx = sg_wave_max(mx);
-    if (lane == 0) red[w] = mx;
-    __syncthreads();
-    if (tid == 0) {
-      float mm = red[0];
-#pragma unroll
-      for (int i = 1; i < kWaves; i++) mm = fmaxf(mm, red[i]);
-      sg_atomic_max_nonneg(amax + it.seq, mm);
-    }
-  }
-}
-
 // wait_vmcnt<N>: this wave's vector memory operations older than the last N
 // have completed, and its LDS reads too (s_waitcnt vmcnt(N) lgkmcnt(0)).
 template <int N>
@@ -518,7 +268,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
   // K item: copy i moves rows R = 8w + 2i and 8w + 2i + 1 (hi for waves 0-3,
   // lo for waves 4-7); lane L takes row R = 8w + 2i + L / 32 and LDS position
   // L % 32, i.e. global chunk (L % 32) ^ (R & 15).  Keys past the sequence's
-  // end are clamped to its last key (masked below), as in k_attn.
+  // end are clamped to its last key and masked out of the scores below.
   // V^T item: copy i moves dims 32w + 8i .. + 7; lane L takes dim
   // d = 32w + 8i + L / 8, position L % 8, global chunk (L % 8) ^ ((d >> 1) & 7);
   // every tile of a sequence lies inside its padded V^T columns.
@@ -709,6 +459,241 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
   }
 }
 
+// Sequences longer than kRegKeys keys: the same tile pipeline, LDS layouts
+// and products as k_attn_rs, with pass 2 recomputing each tile's S^T instead
+// of keeping the scores in registers.  One stream of 3 nt items through the
+// 3-stage ring, issued two items ahead: the nt K tiles of pass 1 (row max),
+// then K tile t and V^T tile t in turn (scores, probabilities, O^T += V^T P^T).
+// Every value and its rounding order are k_attn_rs's, so a sequence gives the
+// same bits on either kernel.
+template <bool QPRE>
+__global__ __launch_bounds__(kNT, 2) void k_attn_ring(
+    const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
+    const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vt, int ldvt, float* __restrict__ out,
+    int ldo, const int32_t* __restrict__ seq_off, const int32_t* __restrict__ voff, const sg_item* __restrict__ items,
+    int G, float sscale, float* __restrict__ amax, sg_attn_qpre qp) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kRing * kTileBytes];
+  __shared__ float red[kWaves];
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+
+  const sg_item it = items[blockIdx.x];
+  const int kvh = blockIdx.y;
+  const int r0 = seq_off[it.seq];
+  const int S = seq_off[it.seq + 1] - r0;
+  const int vo = voff[it.seq];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6) & (kWaves - 1);
+  const int ln = lane & 15, g4 = lane >> 4;
+  const int nqb = (S + kQW - 1) / kQW;
+  const int nt = (S + kBK - 1) / kBK;
+  const int c = it.c0 + w;
+  const bool active = c < G * nqb;  // wave-uniform
+  const int hg = active ? c / nqb : 0;
+  const int q0 = active ? (c % nqb) * kQW : 0;
+  const int head = kvh * G + hg;
+  const int qrow = q0 + ln;
+  const bool qvalid = active && qrow < S;
+  const int qr = r0 + min(qrow, S - 1);
+
+  // ---- copies ----
+  // Wave w's four copies of an item land at w * 4 KB + i * 1 KB of the stage.
+  // K item: copy i moves rows R = 8w + 2i and 8w + 2i + 1 (hi for waves 0-3,
+  // lo for waves 4-7); lane L takes row R = 8w + 2i + L / 32 and LDS position
+  // L % 32, i.e. global chunk (L % 32) ^ (R & 15).  Keys past the sequence's
+  // end are clamped to its last key and masked out of the scores below.
+  // V^T item: copy i moves dims 32w + 8i .. + 7; lane L takes dim
+  // d = 32w + 8i + L / 8, position L % 8, global chunk (L % 8) ^ ((d >> 1) & 7);
+  // every tile of a sequence lies inside its padded V^T columns.
+  const i32x4_t rk = raw_rsrc((w < 4 ? kh : kl) + (int64_t)r0 * ldk + kvh * kHD);
+  const i32x4_t rv = raw_rsrc(vt + (int64_t)kvh * kHD * ldvt + 2 * vo);
+  int kkey[4];
+  uint32_t kchunk[4], voffs[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int R = 8 * w + 2 * i + (lane >> 5);
+    kkey[i] = R & 31;
+    kchunk[i] = 16u * (uint32_t)((lane & 31) ^ (R & 15));
+    const int d = 32 * (w & 7) + 8 * i + (lane >> 3), cv = (lane & 7) ^ ((d >> 1) & 7);
+    voffs[i] = (uint32_t)d * (uint32_t)ldvt * 2u + 16u * (uint32_t)cv;
+  }
+  // Items: the nt K tiles of pass 1, then pass 2's K and V^T tile of every
+  // 32 keys in turn (item nt + 2t: K tile t, nt + 2t + 1: V^T tile t).
+  auto issue = [&](int item) {
+    const int last = 3 * nt - 1;
+    const int src = item < last ? item : last;
+    const uint32_t dst = (uint32_t)(uintptr_t)(lds_ptr)(lds + ((unsigned)item % kRing) * kTileBytes + w * 4096);
+    const bool isk = src < nt || ((src - nt) & 1) == 0;
+    const int tile = src < nt ? src : (src - nt) >> 1;
+    const int kt = tile * kBK;
+    const uint32_t soff = isk ? 0u : (uint32_t)tile * kBK * 4u;  // V^T: the tile's columns, 64 halves per 32 keys
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t ko = (uint32_t)min(kt + kkey[i], S - 1) * (uint32_t)ldk * 2u + kchunk[i];
+      lds_copy16(dst + 1024u * i, isk ? ko : voffs[i], isk ? rk : rv, soff);
+    }
+  };
+  issue(0);
+  issue(1);
+  half8_t bqh[kHD / 32], bql[kHD / 32];
+  // The Q prologue's LDS tiles sit in stage 2, which no copy touches before
+  // the first barrier.
+  q_operand<QPRE>(bqh, bql, qh, ql, ldq, qp, qr, head, ln, g4, lane,
+                  reinterpret_cast<float*>(lds + 2 * kTileBytes) + w * (16 * 40));
+
+  auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
+  // ---- pass 1: S^T = K Q^T per tile, kept in registers; row max ----
+  // K fragment (row R = 32 hl + 16 st + ln, chunk 4 ks + g4) at
+  // R * 512 + 16 * ((4 ks + g4) ^ ln) = (xk ^ 64 ks) + 8192 st + 16384 hl.
+  const uint32_t xk = (uint32_t)ln * 512u + 16u * (uint32_t)(g4 ^ (ln & 3)) + 64u * (uint32_t)(ln >> 2);
+  auto scores2 = [&](const unsigned char* kb, f32x4_t& a0, f32x4_t& a1) {
+    auto rd = [&](int st, int ks, half8_t& h, half8_t& l) {
+      const unsigned char* p = kb + (xk ^ (64u * ks)) + 8192 * st;
+      h = *reinterpret_cast<const half8_t*>(p);
+      l = *reinterpret_cast<const half8_t*>(p + 16384);
+    };
+    a0 = f32x4_t{0, 0, 0, 0};
+    a1 = f32x4_t{0, 0, 0, 0};
+    half8_t h0, l0, h1, l1;
+    rd(0, 0, h0, l0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+    for (int ks = 0; ks < kHD / 32; ks++) {
+      rd(1, ks, h1, l1);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      a0 = mfma16(h0, bqh[ks], a0);
+      a0 = mfma16(h0, bql[ks], a0);
+      a0 = mfma16(l0, bqh[ks], a0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+      if (ks + 1 < kHD / 32) {
+        rd(0, ks + 1, h0, l0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      a1 = mfma16(h1, bqh[ks], a1);
+      a1 = mfma16(h1, bql[ks], a1);
+      a1 = mfma16(l1, bqh[ks], a1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    }
+  };
+  float m = -INFINITY;
+  for (int t = 0; t < nt; t++) {
+    wait_vmcnt<4>();  // item t landed (item t + 1 may still be in flight)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(t + 2);
+    // Every wave computes (an inactive wave's results are never stored).
+    f32x4_t a0, a1;
+    scores2(lds + (t % kRing) * kTileBytes, a0, a1);
+    const int kt = t * kBK;
+    if (kt + kBK <= S) {  // keys past S only in a sequence's last tile
+#pragma unroll
+      for (int r = 0; r < 4; r++) m = fmaxf(m, fmaxf(a0[r], a1[r]));
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        m = key_of(kt, 0, r) < S ? fmaxf(m, a0[r]) : m;
+        m = key_of(kt, 1, r) < S ? fmaxf(m, a1[r]) : m;
+      }
+    }
+  }
+  // Max of the raw (x64) scores; scaling by the power of two sscale commutes
+  // with max exactly.
+  m = fmaxf(m, __shfl_xor(m, 16));
+  m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
+
+  // ---- pass 2: e = fastExp(s - m), row sums, O^T += V^T P^T ----
+  // V^T fragment (dim 16 mt + ln, chunk g4 hi / 4 + g4 lo) at
+  // (16 mt + ln) * 128 + 16 * (chunk ^ ((ln >> 1) & 7)): xv (+ 64 for lo)
+  // + 2048 mt.
+  const uint32_t xv = (uint32_t)ln * 128u + 16u * (uint32_t)(g4 ^ ((ln >> 1) & 7));
+  f32x4_t o[kHD / 16];
+#pragma unroll
+  for (int mt = 0; mt < kHD / 16; mt++) o[mt] = f32x4_t{0, 0, 0, 0};
+  float lsum = 0.0f;
+  auto pv = [&](const unsigned char* vb, const half8_t& ph, const half8_t& pl) {
+    const unsigned char* p0 = vb + xv;
+    half8_t fr[3][2];  // [buffer][hi, lo]
+    auto rd = [&](int mt, half8_t(&f)[2]) {
+      f[0] = *reinterpret_cast<const half8_t*>(p0 + 2048 * mt);
+      f[1] = *reinterpret_cast<const half8_t*>(vb + ((xv ^ 64u) + 2048u * mt));
+    };
+    rd(0, fr[0]);
+    rd(1, fr[1]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int mt = 0; mt < kHD / 16; mt++) {
+      if (mt + 2 < kHD / 16) {
+        rd(mt + 2, fr[(mt + 2) % 3]);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      const half8_t(&f)[2] = fr[mt % 3];
+      o[mt] = mfma16(f[0], ph, o[mt]);
+      o[mt] = mfma16(f[0], pl, o[mt]);
+      o[mt] = mfma16(f[1], ph, o[mt]);
+      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
+    }
+  };
+  for (int t = 0; t < nt; t++) {
+    const int item = nt + 2 * t;
+    wait_vmcnt<4>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(item + 2);
+    f32x4_t a0, a1;
+    scores2(lds + ((unsigned)item % kRing) * kTileBytes, a0, a1);
+    half8_t ph, pl;  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
+    const int kt = t * kBK;
+    const bool full = kt + kBK <= S;
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float e = sg_fast_exp_nonpos((st ? a1[r] : a0[r]) * sscale - m);
+        if (!full) e = key_of(kt, st, r) < S ? e : 0.0f;
+        lsum = lsum + e;
+        const hl16 q = split_f16(e * kPScale);
+        ph[4 * st + r] = q.hi;
+        pl[4 * st + r] = q.lo;
+      }
+    }
+    wait_vmcnt<4>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(item + 3);
+    pv(lds + ((unsigned)(item + 1) % kRing) * kTileBytes, ph, pl);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-copies past the last item have landed
+  lsum = lsum + __shfl_xor(lsum, 16);
+  lsum = lsum + __shfl_xor(lsum, 32);
+  const float f = (1.0f / lsum) * kPUnscale;
+
+  // O^T tile mt: lane holds query ln, dims 16mt + 4g4 + r.
+  float mx = 0.0f;
+  if (qvalid) {
+    float* op = out + (int64_t)(r0 + qrow) * ldo + head * kHD + 4 * g4;
+#pragma unroll
+    for (int mt = 0; mt < kHD / 16; mt++) {
+      f32x4_t y;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        y[j] = o[mt][j] * f;
+        mx = fmaxf(mx, fabsf(y[j]));
+      }
+      *reinterpret_cast<f32x4_t*>(op + 16 * mt) = y;
+    }
+  }
+  if (amax) {  // all chunks of a workgroup belong to one sequence
+    mx = sg_wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    if (tid == 0) {
+      float mm = red[0];
+#pragma unroll
+      for (int i = 1; i < kWaves; i++) mm = fmaxf(mm, red[i]);
+      sg_atomic_max_nonneg(amax + it.seq, mm);
+    }
+  }
+}
+
 // V^T split, one 32-key tile per workgroup (sgd::v_split_tile); kv head blockIdx.y.
 __global__ __launch_bounds__(sgd::kKvThreads) void k_v_split_t(const float* __restrict__ v, int ldv,
                                                              const int32_t* __restrict__ seq_off,
@@ -807,7 +792,7 @@ void launch_attn(dim3 grid, hipStream_t s, const _Float16* qh, const _Float16* q
     hipLaunchKernelGGL((k_attn_rs<QPRE>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
                        seq_off, voff, items, G, sscale, amax, qp);
   else
-    hipLaunchKernelGGL((k_attn<QPRE>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
+    hipLaunchKernelGGL((k_attn_ring<QPRE>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
                        seq_off, voff, items, G, sscale, amax, qp);
 }
 }  // namespace
