@@ -52,6 +52,28 @@ constexpr int kWaves = sgk::kAttnChunks;
 constexpr int kNT = kWaves * SG_WAVE;
 constexpr float kQKScale = sgk::kAttnQKScale;
 constexpr float kPScale = 1024.0f, kPUnscale = 1.0f / 1024.0f;
+
+// split_f16(e * kPScale) of two softmax weights e0, e1 in [0, 1], packed:
+// hi = {fp16(p0), fp16(p1)}, lo = {fp16(p0 - hi.x), fp16(p1 - hi.y)} with
+// p = e * kPScale.  p is exact (a power-of-two scale) and so is p - fp16(p)
+// (fp16(p) is p rounded to 11 significant bits), so each half is one
+// v_fma_mix{lo,hi}_f16 of e rounded once to fp16: the bits of rounding p and
+// p - hi, in four instructions, the lo pair reading hi's halves through
+// op_sel (the compiler forms p, packs hi and recomputes it instead).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void split_weight2(float e0, float e1, uint32_t& hi, uint32_t& lo) {
+  asm("v_fma_mixlo_f16 %0, %2, %4, 0\n\t"
+      "v_fma_mixhi_f16 %0, %3, %4, 0\n\t"
+      "v_fma_mixlo_f16 %1, %2, %4, -%0 op_sel_hi:[0,0,1]\n\t"
+      "v_fma_mixhi_f16 %1, %3, %4, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
+      : "=&v"(hi), "=&v"(lo)
+      : "v"(e0), "v"(e1), "s"(kPScale));
+}
+
+template <bool B>
+struct bool_c {
+  static constexpr bool value = B;
+};
 static_assert(sgk::kAttnChunkRows == kQW, "host chunking must match the kernel");
 
 __device__ __forceinline__ f32x4_t mfma16(half8_t a, half8_t b, f32x4_t c) {
@@ -350,23 +372,30 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
       issue(t + 2);
       // Every wave computes (an inactive wave's results are never stored).
       scores2(lds + (t % kRing) * kTileBytes, sr[t][0], sr[t][1]);
+      // The registers keep the scaled scores s = raw * sscale (exact: sscale
+      // is a power of two); a key past S (only in a sequence's last tile)
+      // keeps -inf, so pass 2's fastExp clamp gives it a weight of exactly 0
+      // without a per-key test there.
       const int kt = t * kBK;
-      if (kt + kBK <= S) {  // keys past S only in a sequence's last tile
+      if (kt + kBK <= S) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) m = fmaxf(m, fmaxf(sr[t][0][r], sr[t][1][r]));
+        for (int r = 0; r < 4; r++) {
+          sr[t][0][r] *= sscale;
+          sr[t][1][r] *= sscale;
+          m = fmaxf(m, fmaxf(sr[t][0][r], sr[t][1][r]));
+        }
       } else {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          m = key_of(kt, 0, r) < S ? fmaxf(m, sr[t][0][r]) : m;
-          m = key_of(kt, 1, r) < S ? fmaxf(m, sr[t][1][r]) : m;
+          sr[t][0][r] = key_of(kt, 0, r) < S ? sr[t][0][r] * sscale : -INFINITY;
+          sr[t][1][r] = key_of(kt, 1, r) < S ? sr[t][1][r] * sscale : -INFINITY;
+          m = fmaxf(m, fmaxf(sr[t][0][r], sr[t][1][r]));
         }
       }
     }
   }
-  // Max of the raw (x64) scores; scaling by the power of two sscale commutes
-  // with max exactly.
   m = fmaxf(m, __shfl_xor(m, 16));
-  m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
+  m = fmaxf(m, __shfl_xor(m, 32));
 
   // ---- pass 2: e = fastExp(s - m), row sums, O^T += V^T P^T ----
   // V^T fragment (dim 16 mt + ln, chunk g4 hi / 4 + g4 lo) at
@@ -404,21 +433,22 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
   for (int t = 0; t < kRegTiles; t++) {
     if (t < nt) {
       const int item = nt + t;
-      half8_t ph, pl;  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
-      const int kt = t * kBK;
-      const bool full = kt + kBK <= S;
+      float e[8];  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
 #pragma unroll
-      for (int st = 0; st < 2; st++) {
+      for (int st = 0; st < 2; st++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          float e = sg_fast_exp_nonpos(sr[t][st][r] * sscale - m);
-          if (!full) e = key_of(kt, st, r) < S ? e : 0.0f;
-          lsum = lsum + e;
-          const hl16 q = split_f16(e * kPScale);
-          ph[4 * st + r] = q.hi;
-          pl[4 * st + r] = q.lo;
-        }
+        for (int r = 0; r < 4; r++) e[4 * st + r] = sg_fast_exp_nonpos(sr[t][st][r] - m);
+#pragma unroll
+      for (int k = 0; k < 8; k++) lsum = lsum + e[k];
+      u32x4_t uh, ul;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        uint32_t h, l;
+        split_weight2(e[2 * k], e[2 * k + 1], h, l);
+        uh[k] = h;
+        ul[k] = l;
       }
+      const half8_t ph = __builtin_bit_cast(half8_t, uh), pl = __builtin_bit_cast(half8_t, ul);
       wait_vmcnt<4>();
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
@@ -632,7 +662,9 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_ring(
       __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
     }
   };
-  for (int t = 0; t < nt; t++) {
+  // One tile of pass 2; the key test only in the instance for the last tile
+  // (keys past S occur only there).
+  auto step = [&](int t, auto last) {
     const int item = nt + 2 * t;
     wait_vmcnt<4>();
     __builtin_amdgcn_s_barrier();
@@ -640,27 +672,33 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_ring(
     issue(item + 2);
     f32x4_t a0, a1;
     scores2(lds + ((unsigned)item % kRing) * kTileBytes, a0, a1);
-    half8_t ph, pl;  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
-    const int kt = t * kBK;
-    const bool full = kt + kBK <= S;
+    float e[8];  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
 #pragma unroll
-    for (int st = 0; st < 2; st++) {
+    for (int st = 0; st < 2; st++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        float e = sg_fast_exp_nonpos((st ? a1[r] : a0[r]) * sscale - m);
-        if (!full) e = key_of(kt, st, r) < S ? e : 0.0f;
-        lsum = lsum + e;
-        const hl16 q = split_f16(e * kPScale);
-        ph[4 * st + r] = q.hi;
-        pl[4 * st + r] = q.lo;
+        e[4 * st + r] = sg_fast_exp_nonpos((st ? a1[r] : a0[r]) * sscale - m);
+        if constexpr (decltype(last)::value) e[4 * st + r] = key_of(t * kBK, st, r) < S ? e[4 * st + r] : 0.0f;
       }
-    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) lsum = lsum + e[k];
+    u32x4_t uh, ul;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        uint32_t h, l;
+        split_weight2(e[2 * k], e[2 * k + 1], h, l);
+        uh[k] = h;
+        ul[k] = l;
+      }
+    const half8_t ph = __builtin_bit_cast(half8_t, uh), pl = __builtin_bit_cast(half8_t, ul);
     wait_vmcnt<4>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     issue(item + 3);
     pv(lds + ((unsigned)(item + 1) % kRing) * kTileBytes, ph, pl);
-  }
+  };
+  for (int t = 0; t + 1 < nt; t++) step(t, bool_c<false>{});
+  step(nt - 1, bool_c<true>{});
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-copies past the last item have landed
   lsum = lsum + __shfl_xor(lsum, 16);
   lsum = lsum + __shfl_xor(lsum, 32);
