@@ -296,28 +296,43 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
   // every tile of a sequence lies inside its padded V^T columns.
   const i32x4_t rk = raw_rsrc((w < 4 ? kh : kl) + (int64_t)r0 * ldk + kvh * kHD);
   const i32x4_t rv = raw_rsrc(vt + (int64_t)kvh * kHD * ldvt + 2 * vo);
-  int kkey[4];
-  uint32_t kchunk[4], voffs[4];
+  // Per-lane byte offsets, loop-invariant: K copy i at key row kkey(i) of a
+  // tile (kvo; the tile's first row goes in the scalar offset), V^T copy i
+  // (voffs; the tile's columns go in the scalar offset).
+  auto kkey = [&](int i) { return ((8 * w + 2 * i) & 31) + (lane >> 5); };
+  uint32_t kvo[4], voffs[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int R = 8 * w + 2 * i + (lane >> 5);
-    kkey[i] = R & 31;
-    kchunk[i] = 16u * (uint32_t)((lane & 31) ^ (R & 15));
+    kvo[i] = (uint32_t)kkey(i) * (uint32_t)ldk * 2u + 16u * (uint32_t)((lane & 31) ^ (R & 15));
     const int d = 32 * (w & 7) + 8 * i + (lane >> 3), cv = (lane & 7) ^ ((d >> 1) & 7);
     voffs[i] = (uint32_t)d * (uint32_t)ldvt * 2u + 16u * (uint32_t)cv;
   }
+  // This wave's four copies of K tile `tile` (isk) or V^T tile `tile` into the
+  // ring stage at dst.
+  auto copy_tile = [&](uint32_t dst, bool isk, int tile) {
+    if (!isk) {  // V^T: the tile's columns, 64 halves per 32 keys
+      const uint32_t soff = (uint32_t)tile * kBK * 4u;
+#pragma unroll
+      for (int i = 0; i < 4; i++) lds_copy16(dst + 1024u * i, voffs[i], rv, soff);
+    } else if (tile * kBK + kBK <= S) {  // a whole K tile
+      const uint32_t soff = (uint32_t)(tile * kBK) * (uint32_t)ldk * 2u;
+#pragma unroll
+      for (int i = 0; i < 4; i++) lds_copy16(dst + 1024u * i, kvo[i], rk, soff);
+    } else {  // a sequence's last K tile: rows past S re-read its last key
+      const int kt = tile * kBK;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int key = min(kt + kkey(i), S - 1);
+        lds_copy16(dst + 1024u * i, kvo[i] + (uint32_t)(key - kkey(i)) * (uint32_t)ldk * 2u, rk, 0u);
+      }
+    }
+  };
   auto issue = [&](int item) {
     const int last = 2 * nt - 1;
     const int src = item < last ? item : last;
     const uint32_t dst = (uint32_t)(uintptr_t)(lds_ptr)(lds + ((unsigned)item % kRing) * kTileBytes + w * 4096);
-    const bool isk = src < nt;
-    const int kt = src * kBK;
-    const uint32_t soff = isk ? 0u : (uint32_t)(src - nt) * kBK * 4u;  // V^T: the tile's columns, 64 halves per 32 keys
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t ko = (uint32_t)min(kt + kkey[i], S - 1) * (uint32_t)ldk * 2u + kchunk[i];
-      lds_copy16(dst + 1024u * i, isk ? ko : voffs[i], isk ? rk : rv, soff);
-    }
+    copy_tile(dst, src < nt, src < nt ? src : src - nt);
   };
   issue(0);
   issue(1);
@@ -536,31 +551,45 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_ring(
   // every tile of a sequence lies inside its padded V^T columns.
   const i32x4_t rk = raw_rsrc((w < 4 ? kh : kl) + (int64_t)r0 * ldk + kvh * kHD);
   const i32x4_t rv = raw_rsrc(vt + (int64_t)kvh * kHD * ldvt + 2 * vo);
-  int kkey[4];
-  uint32_t kchunk[4], voffs[4];
+  // Per-lane byte offsets, loop-invariant: K copy i at key row kkey(i) of a
+  // tile (kvo; the tile's first row goes in the scalar offset), V^T copy i
+  // (voffs; the tile's columns go in the scalar offset).
+  auto kkey = [&](int i) { return ((8 * w + 2 * i) & 31) + (lane >> 5); };
+  uint32_t kvo[4], voffs[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int R = 8 * w + 2 * i + (lane >> 5);
-    kkey[i] = R & 31;
-    kchunk[i] = 16u * (uint32_t)((lane & 31) ^ (R & 15));
+    kvo[i] = (uint32_t)kkey(i) * (uint32_t)ldk * 2u + 16u * (uint32_t)((lane & 31) ^ (R & 15));
     const int d = 32 * (w & 7) + 8 * i + (lane >> 3), cv = (lane & 7) ^ ((d >> 1) & 7);
     voffs[i] = (uint32_t)d * (uint32_t)ldvt * 2u + 16u * (uint32_t)cv;
   }
+  // This wave's four copies of K tile `tile` (isk) or V^T tile `tile` into the
+  // ring stage at dst.
+  auto copy_tile = [&](uint32_t dst, bool isk, int tile) {
+    if (!isk) {  // V^T: the tile's columns, 64 halves per 32 keys
+      const uint32_t soff = (uint32_t)tile * kBK * 4u;
+#pragma unroll
+      for (int i = 0; i < 4; i++) lds_copy16(dst + 1024u * i, voffs[i], rv, soff);
+    } else if (tile * kBK + kBK <= S) {  // a whole K tile
+      const uint32_t soff = (uint32_t)(tile * kBK) * (uint32_t)ldk * 2u;
+#pragma unroll
+      for (int i = 0; i < 4; i++) lds_copy16(dst + 1024u * i, kvo[i], rk, soff);
+    } else {  // a sequence's last K tile: rows past S re-read its last key
+      const int kt = tile * kBK;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int key = min(kt + kkey(i), S - 1);
+        lds_copy16(dst + 1024u * i, kvo[i] + (uint32_t)(key - kkey(i)) * (uint32_t)ldk * 2u, rk, 0u);
+      }
+    }
+  };
   // Items: the nt K tiles of pass 1, then pass 2's K and V^T tile of every
   // 32 keys in turn (item nt + 2t: K tile t, nt + 2t + 1: V^T tile t).
   auto issue = [&](int item) {
     const int last = 3 * nt - 1;
     const int src = item < last ? item : last;
     const uint32_t dst = (uint32_t)(uintptr_t)(lds_ptr)(lds + ((unsigned)item % kRing) * kTileBytes + w * 4096);
-    const bool isk = src < nt || ((src - nt) & 1) == 0;
-    const int tile = src < nt ? src : (src - nt) >> 1;
-    const int kt = tile * kBK;
-    const uint32_t soff = isk ? 0u : (uint32_t)tile * kBK * 4u;  // V^T: the tile's columns, 64 halves per 32 keys
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t ko = (uint32_t)min(kt + kkey[i], S - 1) * (uint32_t)ldk * 2u + kchunk[i];
-      lds_copy16(dst + 1024u * i, isk ? ko : voffs[i], isk ? rk : rv, soff);
-    }
+    copy_tile(dst, src < nt || ((src - nt) & 1) == 0, src < nt ? src : (src - nt) >> 1);
   };
   issue(0);
   issue(1);
