@@ -53,21 +53,21 @@ constexpr int kNT = kWaves * SG_WAVE;
 constexpr float kQKScale = sgk::kAttnQKScale;
 constexpr float kPScale = 1024.0f, kPUnscale = 1.0f / 1024.0f;
 
-// split_f16(e * kPScale) of two softmax weights e0, e1 in [0, 1], packed:
-// hi = {fp16(p0), fp16(p1)}, lo = {fp16(p0 - hi.x), fp16(p1 - hi.y)} with
-// p = e * kPScale.  p is exact (a power-of-two scale) and so is p - fp16(p)
-// (fp16(p) is p rounded to 11 significant bits), so each half is one
-// v_fma_mix{lo,hi}_f16 of e rounded once to fp16: the bits of rounding p and
-// p - hi, in four instructions, the lo pair reading hi's halves through
-// op_sel (the compiler forms p, packs hi and recomputes it instead).
+// split_f16(x * scale) of two values x0, x1, packed, for a power-of-two
+// scale: hi = {fp16(p0), fp16(p1)}, lo = {fp16(p0 - hi.x), fp16(p1 - hi.y)}
+// with p = x * scale.  p is exact and so is p - fp16(p) (fp16(p) is p rounded
+// to 11 significant bits), so each half is one v_fma_mix{lo,hi}_f16 of x
+// rounded once to fp16: the bits of rounding p and p - hi, in four
+// instructions, the lo pair reading hi's halves through op_sel (the compiler
+// forms p, packs hi and recomputes it instead).
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void split_weight2(float e0, float e1, uint32_t& hi, uint32_t& lo) {
+__device__ __forceinline__ void split_pair(float x0, float x1, float scale, uint32_t& hi, uint32_t& lo) {
   asm("v_fma_mixlo_f16 %0, %2, %4, 0\n\t"
       "v_fma_mixhi_f16 %0, %3, %4, 0\n\t"
       "v_fma_mixlo_f16 %1, %2, %4, -%0 op_sel_hi:[0,0,1]\n\t"
       "v_fma_mixhi_f16 %1, %3, %4, -%0 op_sel:[0,0,1] op_sel_hi:[0,0,1]"
       : "=&v"(hi), "=&v"(lo)
-      : "v"(e0), "v"(e1), "s"(kPScale));
+      : "v"(x0), "v"(x1), "s"(scale));
 }
 
 template <bool B>
@@ -96,14 +96,13 @@ constexpr int kRegTiles = sgk::kAttnRegKeys / kBK;
 template <bool QPRE>
 __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bql)[kHD / 32],
                                           const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq,
-                                          const sg_attn_qpre& qp, int qr, int head, int ln, int g4, int lane,
-                                          float* tile) {
+                                          const sg_attn_qpre& qp, int qr, int pos, int head, int ln, int g4,
+                                          int lane, float* tile) {
   if constexpr (QPRE) {
-    // Every global load (the row's position, Q, the norm weights, the RoPE
-    // table rows) is issued up front, so the prologue pays one memory latency
-    // instead of one per phase; the registers are free this early.
+    // Every global load (Q, the norm weights, the RoPE table rows of the
+    // row's position pos) is issued up front, so the prologue pays one memory
+    // latency instead of one per phase; the registers are free this early.
     // Lane (ln, g4) holds elements e = 32ks + 8g4 + t of row ln.
-    const int pos = qp.row_pos[qr];
     float x[kHD / 32][8], wq[kHD / 32][8];
     const float* src = qp.q + (int64_t)qr * qp.ldq + head * kHD + 8 * g4;
 #pragma unroll
@@ -178,13 +177,18 @@ __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bq
       }
     }
 #pragma unroll
-    for (int ks = 0; ks < kHD / 32; ks++)
+    for (int ks = 0; ks < kHD / 32; ks++) {
+      u32x4_t uh, ul;
 #pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const hl16 sp = split_f16(x[ks][t] * kQKScale);
-        bqh[ks][t] = sp.hi;
-        bql[ks][t] = sp.lo;
+      for (int k = 0; k < 4; k++) {
+        uint32_t h, l;
+        split_pair(x[ks][2 * k], x[ks][2 * k + 1], kQKScale, h, l);
+        uh[k] = h;
+        ul[k] = l;
       }
+      bqh[ks] = __builtin_bit_cast(half8_t, uh);
+      bql[ks] = __builtin_bit_cast(half8_t, ul);
+    }
   } else {
     const int64_t qo = (int64_t)qr * ldq + head * kHD + 8 * g4;
 #pragma unroll
@@ -339,7 +343,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
   half8_t bqh[kHD / 32], bql[kHD / 32];
   // The Q prologue's LDS tiles sit in stage 2, which no copy touches before
   // the first barrier.
-  q_operand<QPRE>(bqh, bql, qh, ql, ldq, qp, qr, head, ln, g4, lane,
+  q_operand<QPRE>(bqh, bql, qh, ql, ldq, qp, qr, qr - r0, head, ln, g4, lane,
                   reinterpret_cast<float*>(lds + 2 * kTileBytes) + w * (16 * 40));
 
   auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
@@ -459,7 +463,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         uint32_t h, l;
-        split_weight2(e[2 * k], e[2 * k + 1], h, l);
+        split_pair(e[2 * k], e[2 * k + 1], kPScale, h, l);
         uh[k] = h;
         ul[k] = l;
       }
@@ -596,7 +600,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_ring(
   half8_t bqh[kHD / 32], bql[kHD / 32];
   // The Q prologue's LDS tiles sit in stage 2, which no copy touches before
   // the first barrier.
-  q_operand<QPRE>(bqh, bql, qh, ql, ldq, qp, qr, head, ln, g4, lane,
+  q_operand<QPRE>(bqh, bql, qh, ql, ldq, qp, qr, qr - r0, head, ln, g4, lane,
                   reinterpret_cast<float*>(lds + 2 * kTileBytes) + w * (16 * 40));
 
   auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
@@ -715,7 +719,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_ring(
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         uint32_t h, l;
-        split_weight2(e[2 * k], e[2 * k + 1], h, l);
+        split_pair(e[2 * k], e[2 * k + 1], kPScale, h, l);
         uh[k] = h;
         ul[k] = l;
       }
@@ -875,7 +879,7 @@ hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Flo
   const dim3 grid(n_items, HKV);
   const bool rs = max_len <= kAttnRegKeys;
   if (qpre) {
-    if (!qpre->q || !qpre->cos_t || !qpre->sin_t || !qpre->row_pos || (qpre->ldq & 3) ||
+    if (!qpre->q || !qpre->cos_t || !qpre->sin_t || (qpre->ldq & 3) ||
         (reinterpret_cast<uintptr_t>(qpre->q) & 15) || (reinterpret_cast<uintptr_t>(qpre->w) & 15) ||
         (reinterpret_cast<uintptr_t>(qpre->cos_t) & 15) || (reinterpret_cast<uintptr_t>(qpre->sin_t) & 15))
       return hipErrorInvalidValue;  // float4 loads of Q rows, weights and table rows

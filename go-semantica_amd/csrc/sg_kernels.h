@@ -9,15 +9,15 @@
 // chunk) or V^T split tile (sequence, first key).
 struct sg_item { int32_t seq, c0; };
 // Q's QK-norm + RoPE done inside the attention kernel: fp32 q [T][ldq] as the
-// QKV GEMM wrote it, attn_q_norm weights (null: no norm), the RoPE tables
-// [pos][128] and each row's position.
+// QKV GEMM wrote it, attn_q_norm weights (null: no norm) and the RoPE tables
+// [pos][128].  A row's position is its index within its sequence (positions
+// restart at 0 in every sequence, as the forward's row_pos holds them).
 struct sg_attn_qpre {
   const float* q;
   int ldq;
   const float* w;
   const float* cos_t;
   const float* sin_t;
-  const int32_t* row_pos;
   float eps;
 };
 
