@@ -199,44 +199,6 @@ __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bq
   }
 }
 
-// wait_vmcnt<N>: this wave's vector memory operations older than the last N
-// have completed, and its LDS reads too (s_waitcnt vmcnt(N) lgkmcnt(0)).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 63, "vmcnt field");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
-}
-
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-
-// One 64-lane buffer_load_dwordx4 ... lds (1 KB to LDS at lds_addr + 16 *
-// lane, lane l reading rsrc.base + voff_l + soff), issued from inline
-// assembly.  The compiler then sees no LDS write, so it inserts no wait in
-// front of the fragment reads of the other ring stages (it cannot tell them
-// apart from the copies once several are in flight); the kernel orders copies
-// and reads itself with s_waitcnt vmcnt + s_barrier.  M0 (the copy's LDS base)
-// is saved and restored around it.
-__device__ __forceinline__ void lds_copy16(uint32_t lds_addr, uint32_t voff, i32x4_t rsrc, uint32_t soff) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %1\n\t"
-      "s_nop 0\n\t"
-      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
-      "s_nop 0\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
-      : "memory");
-}
-
-// Raw buffer descriptor over [base, base + 2 GB): stride 0, the rest as
-// __builtin_amdgcn_make_buffer_rsrc builds it.
-__device__ __forceinline__ i32x4_t raw_rsrc(const void* base) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return i32x4_t{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), 0x7fffffff, 0x00020000};  // word 3: gfx9 raw buffer
-}
-
 constexpr int kTileBytes = 32 * 1024;  // one K or V^T tile, hi and lo halves
 constexpr int kRing = 3;               // tile stages in LDS
 
@@ -298,8 +260,8 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
   // V^T item: copy i moves dims 32w + 8i .. + 7; lane L takes dim
   // d = 32w + 8i + L / 8, position L % 8, global chunk (L % 8) ^ ((d >> 1) & 7);
   // every tile of a sequence lies inside its padded V^T columns.
-  const i32x4_t rk = raw_rsrc((w < 4 ? kh : kl) + (int64_t)r0 * ldk + kvh * kHD);
-  const i32x4_t rv = raw_rsrc(vt + (int64_t)kvh * kHD * ldvt + 2 * vo);
+  const i32x4_t rk = sg_raw_rsrc((w < 4 ? kh : kl) + (int64_t)r0 * ldk + kvh * kHD);
+  const i32x4_t rv = sg_raw_rsrc(vt + (int64_t)kvh * kHD * ldvt + 2 * vo);
   // Per-lane byte offsets, loop-invariant: K copy i at key row kkey(i) of a
   // tile (kvo; the tile's first row goes in the scalar offset), V^T copy i
   // (voffs; the tile's columns go in the scalar offset).
@@ -318,17 +280,17 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
     if (!isk) {  // V^T: the tile's columns, 64 halves per 32 keys
       const uint32_t soff = (uint32_t)tile * kBK * 4u;
 #pragma unroll
-      for (int i = 0; i < 4; i++) lds_copy16(dst + 1024u * i, voffs[i], rv, soff);
+      for (int i = 0; i < 4; i++) sg_lds_copy16(dst + 1024u * i, voffs[i], rv, soff);
     } else if (tile * kBK + kBK <= S) {  // a whole K tile
       const uint32_t soff = (uint32_t)(tile * kBK) * (uint32_t)ldk * 2u;
 #pragma unroll
-      for (int i = 0; i < 4; i++) lds_copy16(dst + 1024u * i, kvo[i], rk, soff);
+      for (int i = 0; i < 4; i++) sg_lds_copy16(dst + 1024u * i, kvo[i], rk, soff);
     } else {  // a sequence's last K tile: rows past S re-read its last key
       const int kt = tile * kBK;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int key = min(kt + kkey(i), S - 1);
-        lds_copy16(dst + 1024u * i, kvo[i] + (uint32_t)(key - kkey(i)) * (uint32_t)ldk * 2u, rk, 0u);
+        sg_lds_copy16(dst + 1024u * i, kvo[i] + (uint32_t)(key - kkey(i)) * (uint32_t)ldk * 2u, rk, 0u);
       }
     }
   };
@@ -385,7 +347,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
 #pragma unroll
   for (int t = 0; t < kRegTiles; t++) {
     if (t < nt) {
-      wait_vmcnt<4>();  // item t landed (item t + 1 may still be in flight)
+      sg_wait_vmcnt<4>();  // item t landed (item t + 1 may still be in flight)
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       issue(t + 2);
@@ -468,7 +430,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
         ul[k] = l;
       }
       const half8_t ph = __builtin_bit_cast(half8_t, uh), pl = __builtin_bit_cast(half8_t, ul);
-      wait_vmcnt<4>();
+      sg_wait_vmcnt<4>();
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       issue(item + 2);
@@ -553,8 +515,8 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_ring(
   // V^T item: copy i moves dims 32w + 8i .. + 7; lane L takes dim
   // d = 32w + 8i + L / 8, position L % 8, global chunk (L % 8) ^ ((d >> 1) & 7);
   // every tile of a sequence lies inside its padded V^T columns.
-  const i32x4_t rk = raw_rsrc((w < 4 ? kh : kl) + (int64_t)r0 * ldk + kvh * kHD);
-  const i32x4_t rv = raw_rsrc(vt + (int64_t)kvh * kHD * ldvt + 2 * vo);
+  const i32x4_t rk = sg_raw_rsrc((w < 4 ? kh : kl) + (int64_t)r0 * ldk + kvh * kHD);
+  const i32x4_t rv = sg_raw_rsrc(vt + (int64_t)kvh * kHD * ldvt + 2 * vo);
   // Per-lane byte offsets, loop-invariant: K copy i at key row kkey(i) of a
   // tile (kvo; the tile's first row goes in the scalar offset), V^T copy i
   // (voffs; the tile's columns go in the scalar offset).
@@ -573,17 +535,17 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_ring(
     if (!isk) {  // V^T: the tile's columns, 64 halves per 32 keys
       const uint32_t soff = (uint32_t)tile * kBK * 4u;
 #pragma unroll
-      for (int i = 0; i < 4; i++) lds_copy16(dst + 1024u * i, voffs[i], rv, soff);
+      for (int i = 0; i < 4; i++) sg_lds_copy16(dst + 1024u * i, voffs[i], rv, soff);
     } else if (tile * kBK + kBK <= S) {  // a whole K tile
       const uint32_t soff = (uint32_t)(tile * kBK) * (uint32_t)ldk * 2u;
 #pragma unroll
-      for (int i = 0; i < 4; i++) lds_copy16(dst + 1024u * i, kvo[i], rk, soff);
+      for (int i = 0; i < 4; i++) sg_lds_copy16(dst + 1024u * i, kvo[i], rk, soff);
     } else {  // a sequence's last K tile: rows past S re-read its last key
       const int kt = tile * kBK;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int key = min(kt + kkey(i), S - 1);
-        lds_copy16(dst + 1024u * i, kvo[i] + (uint32_t)(key - kkey(i)) * (uint32_t)ldk * 2u, rk, 0u);
+        sg_lds_copy16(dst + 1024u * i, kvo[i] + (uint32_t)(key - kkey(i)) * (uint32_t)ldk * 2u, rk, 0u);
       }
     }
   };
@@ -639,7 +601,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_ring(
   };
   float m = -INFINITY;
   for (int t = 0; t < nt; t++) {
-    wait_vmcnt<4>();  // item t landed (item t + 1 may still be in flight)
+    sg_wait_vmcnt<4>();  // item t landed (item t + 1 may still be in flight)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     issue(t + 2);
@@ -699,7 +661,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_ring(
   // (keys past S occur only there).
   auto step = [&](int t, auto last) {
     const int item = nt + 2 * t;
-    wait_vmcnt<4>();
+    sg_wait_vmcnt<4>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     issue(item + 2);
@@ -724,7 +686,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_ring(
         ul[k] = l;
       }
     const half8_t ph = __builtin_bit_cast(half8_t, uh), pl = __builtin_bit_cast(half8_t, ul);
-    wait_vmcnt<4>();
+    sg_wait_vmcnt<4>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     issue(item + 3);

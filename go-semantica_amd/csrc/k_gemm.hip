@@ -28,7 +28,6 @@
 #include "sg_device.h"
 #include "sg_kernels.h"
 
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x16_t __attribute__((ext_vector_type(16)));
 
 namespace {
@@ -290,17 +289,6 @@ hipError_t launch_rd(const int8_t* A, int a_rows, const int8_t* W, const float* 
   return hipGetLastError();
 }
 
-// Publishes a ring stage: this wave's copies older than the last N have
-// landed (vmcnt) and its own LDS fragment reads have completed (lgkmcnt), so
-// after the following barrier no wave still reads the stage the next copies
-// overwrite.  (The compiler may place the last MFMAs of the previous step, and
-// their lgkmcnt waits, after an s_barrier, so the read wait is explicit.)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 63, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
-}
-
 constexpr int kBufWord3 = 0x00020000;  // raw buffer descriptor, gfx9 family
 // f(integral_constant<int, I>) for I = I0 .. N-1, unrolled at compile time.
 template <int I, int N, typename F>
@@ -392,7 +380,7 @@ __global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_lds(
   const i32x16_t bias = magic_bias();
   auto step = [&](auto stc, int b) {
     constexpr int ST = decltype(stc)::value;
-    wait_vmcnt<(STAGES - 2) * CPB>();
+    sg_wait_vmcnt<(STAGES - 2) * CPB>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     issue(min(b + STAGES - 1, nb - 1), (ST + STAGES - 1) % STAGES);
@@ -428,6 +416,185 @@ hipError_t launch_lds(const int8_t* A, int a_rows, const int8_t* W, const float*
   return hipGetLastError();
 }
 
+
+// GEMM + residual post-norm for the N = 768 projections (O and down).  In
+// the forward the output o only feeds the residual post-norm
+// (model_int8.go:203-210 / :225-232): h = RMSNorm(o; w_post) + h, then
+// xn = RMSNorm(h; w_next) with the sequences' max|xn| folded into amax (or xn
+// stored, after the last layer).  Here a workgroup computes whole rows -- 64
+// rows x all 768 columns; wave w (16 of them) the rows 32 (w / 8) .. + 31 and
+// the columns 96 (w % 8) .. + 95 (three 32x32 subtiles) -- so the norm runs in
+// the same launch on the values gemm_q8 would store: each 32-row half of the
+// tile is staged in LDS row-major and an 8-lane group per row runs the row
+// kernel's arithmetic on it (sg_post_res_norm_lds).  o never reaches HBM, and
+// the separate norm launch goes away.
+//
+// K loop: the direct-to-LDS ring of k_gemm_q8_lds (3 stages, two blocks
+// ahead).  A block is 29 1-KB copies -- the A tile (2), the 768 columns'
+// weight blocks (24) and their scales (3) -- issued as two per wave (three
+// redundant re-copies fill the 32 slots), so one vmcnt says "this wave's
+// copies of block b have landed" and the barrier after it publishes them.
+constexpr int kResN = 768;
+constexpr int kResBM = 64;
+template <int STAGES, bool XN>
+__global__ __launch_bounds__(1024, 4) void k_gemm_q8_resnorm(
+    const int8_t* __restrict__ A, int a_rows, const int8_t* __restrict__ W, const float* __restrict__ St,
+    const float* __restrict__ row_scale, int M, int K, float* __restrict__ h, const float* __restrict__ w_post,
+    const float* __restrict__ w_next, float eps, float* __restrict__ xn, const int32_t* __restrict__ row_seq,
+    float* __restrict__ amax) {
+  constexpr int N = kResN, BM = kResBM, TNW = 3, NC = N / 32, CPW = 2;
+  constexpr int A_BYTES = BM * 32, W_BYTES = N * 32, S_BYTES = N * 4;
+  constexpr int W_OFF = A_BYTES, S_OFF = A_BYTES + W_BYTES, STAGE = A_BYTES + W_BYTES + S_BYTES;
+  // Staged rows 808 floats apart (40 banks mod 64): the eight rows of a wave's
+  // lane-order reads (lane (row q, v): element 8i + v) fall in distinct banks,
+  // and the two rows of each staging store 32 banks apart.
+  constexpr int OST = N + 40;
+  constexpr int STG_BYTES = 32 * OST * 4;
+  constexpr int LDS_BYTES = STAGES * STAGE > STG_BYTES ? STAGES * STAGE : STG_BYTES;
+  static_assert((STAGES - 2) * CPW <= 63, "vmcnt covers the copies in flight");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) float wl[2][N];  // w_post, w_next
+  __shared__ float rmax[BM];
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wave >> 3, cg = wave & 7;
+  // The norm weights into LDS (published by the K loop's first barrier): the
+  // norm reads them per chunk, from LDS at LDS latency.
+  for (int i = tid; i < N; i += 1024) {
+    wl[0][i] = w_post[i];
+    wl[1][i] = w_next[i];
+  }
+  const int lr = lane & 31, lh = lane >> 5;
+  const int m0 = blockIdx.x * BM;
+  const int nb = K >> 5;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_ptr)lds;
+
+  // Copy slot s = 2 wave + i: s < 24 the weight blocks of columns
+  // 64 (s % 12) .. + 63, half s / 12; 24, 25 the A tile halves; 26..28 the
+  // scales 256 (s - 26) .. + 255; 29..31 re-copy slots 26, 27, 24.
+  auto issue = [&](int b, int st) {
+    const uint32_t base = lds0 + (uint32_t)(st * STAGE);
+#pragma unroll
+    for (int i = 0; i < CPW; i++) {
+      const int s = CPW * wave + i;  // wave-uniform
+      if (s < 24) {
+        const int hh = s / 12, g = s % 12;
+        sg_lds_copy16(base + W_OFF + hh * (N * 16) + g * 1024, (uint32_t)lane * 32u + 16u * hh,
+                      sg_raw_rsrc(W + ((int64_t)b * N + 64 * g) * 32), 0u);
+      } else {
+        const int u = s < 29 ? s - 24 : (s == 31 ? 0 : s - 27);  // 0, 1: A halves; 2..4: scales
+        if (u < 2)
+          sg_lds_copy16(base + u * 1024, (uint32_t)lane * 32u + 16u * u,
+                        sg_raw_rsrc(A + ((int64_t)b * a_rows + m0) * 32), 0u);
+        else
+          sg_lds_copy16(base + S_OFF + (u - 2) * 1024, (uint32_t)lane * 16u,
+                        sg_raw_rsrc(St + (int64_t)b * N + 256 * (u - 2)), 0u);
+      }
+    }
+  };
+  // Fragment reads (stage 0): A rows 32 rg + lr, half lh; W and scale of
+  // column 96 cg + 32 t + lr.
+  const uint32_t ra_f = lh * (BM * 16) + (32 * rg + lr) * 16;
+  const uint32_t rw_f = W_OFF + lh * (N * 16) + (96 * cg + lr) * 16;
+  const uint32_t rd_f = S_OFF + (96 * cg + lr) * 4;
+
+  f32x16_t acc[TNW];
+#pragma unroll
+  for (int t = 0; t < TNW; t++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+  const i32x16_t bias = magic_bias();
+  auto step = [&](auto stc, int b) {
+    constexpr int ST = decltype(stc)::value;
+    sg_wait_vmcnt<(STAGES - 2) * CPW>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(min(b + STAGES - 1, nb - 1), (ST + STAGES - 1) % STAGES);
+    const i32x4_t fa = *reinterpret_cast<const i32x4_t*>(lds + ra_f + ST * STAGE);
+#pragma unroll
+    for (int t = 0; t < TNW; t++) {
+      const i32x4_t fw = *reinterpret_cast<const i32x4_t*>(lds + rw_f + ST * STAGE + t * 512);
+      const float d = *reinterpret_cast<const float*>(lds + rd_f + ST * STAGE + t * 128);
+      const i32x16_t pp = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fw, bias, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[t][r] = __builtin_fmaf(__int_as_float(pp[r]) - kMagic, d, acc[t][r]);
+    }
+  };
+  static_for<0, STAGES - 1>([&](auto ic) { issue(min((int)decltype(ic)::value, nb - 1), decltype(ic)::value); });
+  for (int b = 0; b < nb; b += STAGES)
+    static_for<0, STAGES>([&](auto ic) {
+      if (b + decltype(ic)::value < nb) step(ic, b + decltype(ic)::value);
+    });
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // redundant tail copies landed: the ring is free
+  __syncthreads();
+
+  float* stg = reinterpret_cast<float*>(lds);
+  // Half p of the tile, o = acc * row_scale as gemm_q8 stores it, into LDS.
+  auto stage = [&](int p) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int rl = 8 * (r >> 2) + 4 * lh + (r & 3), row = m0 + 32 * p + rl;
+      const float rs = row_scale[row < M ? row : M - 1];
+#pragma unroll
+      for (int t = 0; t < TNW; t++) stg[rl * OST + 96 * cg + 32 * t + lr] = acc[t][r] * rs;
+    }
+  };
+  // Rows 8 cg + q of half rg (waves cg < 4), an 8-lane group each; the first
+  // quarter of each row's h is loaded ahead of the half's staging.
+  const int q = lane >> 3, j = lane & 7, rl = 8 * cg + q, nrow = m0 + 32 * rg + rl;
+  const bool nvalid = cg < 4 && nrow < M;
+  f32x4_t hv0[NC / 4];
+  auto load_h = [&]() {
+    if (nvalid) {
+      const f32x4_t* hp = reinterpret_cast<const f32x4_t*>(h + (int64_t)nrow * N) + j;
+#pragma unroll
+      for (int k = 0; k < NC / 4; k++) hv0[k] = __builtin_nontemporal_load(&hp[8 * k]);
+    }
+  };
+  auto norm_rows = [&](int p) {
+    if (cg >= 4) return;
+    float m = 0.0f;
+    if (nvalid)
+      m = sg_post_res_norm_lds<NC, XN>(stg + rl * OST, h + (int64_t)nrow * N, hv0, wl[0], wl[1], eps,
+                                       XN ? xn + (int64_t)nrow * N : nullptr, j);
+    m = sg_max8(m);
+    if (j == 0) rmax[32 * p + rl] = m;
+  };
+  // The waves of each half stage it and norm it in turn; the branch is
+  // wave-uniform and both sides pass four barriers, and a wave's
+  // accumulators die at its staging.
+  if (rg == 0) {
+    load_h();
+    stage(0);
+    __syncthreads();
+    norm_rows(0);
+    __syncthreads();
+    __syncthreads();
+    __syncthreads();
+  } else {
+    __syncthreads();
+    __syncthreads();  // half 0 normed: the staging area is free
+    load_h();
+    stage(1);
+    __syncthreads();
+    norm_rows(1);
+    __syncthreads();
+  }
+  if (amax) {  // the rows' max|xn| into their sequences' maxima
+    const int r_last = min(m0 + BM, M) - 1;
+    if (row_seq[m0] == row_seq[r_last]) {
+      if (wave == 0) {
+        const float v = sg_wave_max(rmax[lane]);
+        if (lane == 0) sg_atomic_max_nonneg(amax + row_seq[m0], v);
+      }
+    } else {
+      sg_seg_seq_max(rmax, r_last - m0 + 1, m0, row_seq, amax);
+    }
+  }
+}
+
 }  // namespace
 
 namespace sgk {
@@ -447,6 +614,9 @@ namespace sgk {
 // 128 x 64 tiles below kGeluLdsRows rows (sizes that only occur as one
 // group: 22.0 vs 26.3 us at M = 2048), then the 8-wave kernel.
 constexpr int kRdRows = 6144, kLds8Rows = 12288, kGeluLdsRows = 4096;
+// gemm_q8_res_norm: the fused kernel from kResRows rows (below, gemm_q8 and
+// post_res_norm run as two launches).
+constexpr int kResRows = 8192;
 
 hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
                    int32_t* sums, int M, int N, int K, hipStream_t s) {
@@ -467,6 +637,33 @@ hipError_t gemm_q8_gelu(const int8_t* A, int a_rows, const int8_t* W, const floa
     return launch_rd<4, 1, 1, 2, false, true>(A, a_rows, W, St, row_scale, G, nullptr, M, 2 * Nh, K, s, row_seq,
                                               amax);
   return launch_lds<8, 4, true, 3>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
+}
+
+
+bool gemm_res_norm_fused(int M, int N, const float* w_post, const float* w_next) {
+  return N == kResN && M >= kResRows && w_post && w_next;
+}
+
+hipError_t gemm_q8_res_norm(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale,
+                            float* o, int M, int N, int K, float* h, const float* w_post, const float* w_next, float eps,
+                            float* xn, const int32_t* row_seq, float* amax, hipStream_t s) {
+  if (M <= 0) return hipSuccess;
+  if (K <= 0 || K % 32) return hipErrorInvalidValue;
+  if (amax && !row_seq) return hipErrorInvalidValue;
+  if (!gemm_res_norm_fused(M, N, w_post, w_next)) {
+    const hipError_t e = gemm_q8(A, a_rows, W, St, row_scale, o, nullptr, M, N, K, s);
+    if (e != hipSuccess) return e;
+    return post_res_norm(o, h, w_post, w_next, eps, M, N, xn, row_seq, amax, s);
+  }
+  const int gm = (M + kResBM - 1) / kResBM;
+  if ((int64_t)gm * kResBM > a_rows) return hipErrorInvalidValue;
+  if (xn)
+    hipLaunchKernelGGL((k_gemm_q8_resnorm<3, true>), dim3(gm), dim3(1024), 0, s, A, a_rows, W, St, row_scale, M, K, h,
+                       w_post, w_next, eps, xn, row_seq, amax);
+  else
+    hipLaunchKernelGGL((k_gemm_q8_resnorm<3, false>), dim3(gm), dim3(1024), 0, s, A, a_rows, W, St, row_scale, M, K,
+                       h, w_post, w_next, eps, xn, row_seq, amax);
+  return hipGetLastError();
 }
 
 }  // namespace sgk

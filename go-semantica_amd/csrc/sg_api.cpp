@@ -502,18 +502,33 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
                              site(l, 1), meta.max_len, s, &qpre));
     if (tr && tr->att) SG_HIP(tap(tr->att, att, l, qd));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), quant(att, qd, site(l, 1)));
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), gemm(ly.wo, ly.so, o, d, qd));
-    SG_LAUNCH(SG_K_NORM, t * d * 12.0,
-              sgk::post_res_norm(o, h, ly.post_attn, ly.ffn_norm, eps, T, d, nullptr, meta.row_seq, site(l, 2), s));
+    // The O projection and the residual post-norm: one launch for large
+    // batches (o stays on chip), else the GEMM then k_post_res_norm.
+    if (sgk::gemm_res_norm_fused(T, d, ly.post_attn, ly.ffn_norm)) {
+      SG_LAUNCH(SG_K_GEMM_NORM, gemm_ops(d, qd),
+                sgk::gemm_q8_res_norm(a8, ar, ly.wo, ly.so, sx, o, T, d, qd, h, ly.post_attn, ly.ffn_norm, eps,
+                                      nullptr, meta.row_seq, site(l, 2), s));
+    } else {
+      SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), gemm(ly.wo, ly.so, o, d, qd));
+      SG_LAUNCH(SG_K_NORM, t * d * 12.0,
+                sgk::post_res_norm(o, h, ly.post_attn, ly.ffn_norm, eps, T, d, nullptr, meta.row_seq, site(l, 2), s));
+    }
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.ffn_norm, site(l, 2)));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(2 * ff, d),
               sgk::gemm_q8_gelu(a8, ar, ly.wgu, ly.sgu, sx, g, T, ff, d, meta.row_seq, site(l, 3), s));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(ff), quant(g, ff, site(l, 3)));
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), gemm(ly.wd, ly.sd, o, d, ff));
     const bool last = l + 1 == L;
-    SG_LAUNCH(SG_K_NORM, t * d * (last ? 16.0 : 12.0),
-              sgk::post_res_norm(o, h, ly.post_ffw, last ? m->out_norm : m->layers[l + 1].attn_norm, eps, T, d,
-                                 last ? xn : nullptr, meta.row_seq, last ? nullptr : site(l + 1, 0), s));
+    const float* w_next = last ? m->out_norm : m->layers[l + 1].attn_norm;
+    if (sgk::gemm_res_norm_fused(T, d, ly.post_ffw, w_next)) {
+      SG_LAUNCH(SG_K_GEMM_NORM, gemm_ops(d, ff),
+                sgk::gemm_q8_res_norm(a8, ar, ly.wd, ly.sd, sx, o, T, d, ff, h, ly.post_ffw, w_next, eps,
+                                      last ? xn : nullptr, meta.row_seq, last ? nullptr : site(l + 1, 0), s));
+    } else {
+      SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), gemm(ly.wd, ly.sd, o, d, ff));
+      SG_LAUNCH(SG_K_NORM, t * d * (last ? 16.0 : 12.0),
+                sgk::post_res_norm(o, h, ly.post_ffw, w_next, eps, T, d, last ? xn : nullptr, meta.row_seq,
+                                   last ? nullptr : site(l + 1, 0), s));
+    }
     if (tr && tr->h) SG_HIP(tap(tr->h, h, l, d));
   }
   if (stop >= 0) {

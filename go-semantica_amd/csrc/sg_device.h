@@ -13,6 +13,48 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+// Publishes a ring stage of the direct-to-LDS kernels: this wave's vector
+// memory operations older than the last N have completed (vmcnt) and so have
+// its LDS reads (lgkmcnt), so after the following s_barrier every wave's
+// copies of the stage have landed and no wave still reads the stage the next
+// copies overwrite.  (The compiler may place the last MFMAs of a step, and
+// their lgkmcnt waits, after an s_barrier, so the read wait is explicit.)
+template <int N>
+__device__ __forceinline__ void sg_wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt field");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+}
+
+// One 64-lane buffer_load_dwordx4 ... lds (1 KB to LDS at lds_addr + 16 *
+// lane, lane l reading rsrc.base + voff_l + soff), issued from inline
+// assembly.  The compiler then sees no LDS write, so it inserts no wait in
+// front of the fragment reads of the other ring stages (it cannot tell them
+// apart from the copies once several are in flight); the kernel orders copies
+// and reads itself with sg_wait_vmcnt + s_barrier.  M0 (the copy's LDS base)
+// is saved and restored around it.
+__device__ __forceinline__ void sg_lds_copy16(uint32_t lds_addr, uint32_t voff, i32x4_t rsrc, uint32_t soff) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %2, %3, %4 offen lds\n\t"
+      "s_nop 0\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+      : "memory");
+}
+
+// Raw buffer descriptor over [base, base + 2 GB): stride 0, the rest as
+// __builtin_amdgcn_make_buffer_rsrc builds it (word 3: gfx9 raw buffer).
+__device__ __forceinline__ i32x4_t sg_raw_rsrc(const void* base) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4_t{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), 0x7fffffff, 0x00020000};
+}
+
 #define SG_WAVE 64
 
 // fastExp, internal/kernels/activation.go:100-145: clamp at +-10, 2^(x*log2e)
@@ -304,28 +346,19 @@ __device__ __forceinline__ void sg_rmsnorm8_f4(f32x4_t (&x)[NC], const float* __
 }
 
 
-// One row of the residual post-norm (model_int8.go:203-210 / :225-232):
-// h = RMSNorm(o; w_post) + h, then xn = RMSNorm(h; w_next), the next pre-norm
-// (:194 / :216) or output_norm (:236).  An 8-lane group owns the row on the
-// float4 layout (lane j: elements 32c + 4j .. + 3); tile is the wave's
-// 8 x 40-float transpose tile and r the row's slot in it.  xn is stored when
-// xrow is non-null; returns this lane's max|xn| (max|h| without w_next).
+// The residual post-norm of one row whose o (x) and h (hv) are already in
+// the lanes of its 8-lane group (model_int8.go:203-210 / :225-232):
+// h = RMSNorm(o; w_post) + h, stored to hrow, then xn = RMSNorm(h; w_next),
+// the next pre-norm (:194 / :216) or output_norm (:236).  Float4 layout
+// (lane j: elements 32c + 4j .. + 3); tile is the wave's 8 x 40-float
+// transpose tile and r the row's slot in it.  xn is stored when xrow is
+// non-null; returns this lane's max|xn| (max|h| without w_next).
 template <int NC>
-__device__ __forceinline__ float sg_post_res_norm_row(const float* __restrict__ orow, float* __restrict__ hrow,
-                                                      const float* __restrict__ w_post,
-                                                      const float* __restrict__ w_next, float eps,
-                                                      float* __restrict__ xrow, float* tile, int r, int j) {
-  // o and h are loaded together: one memory round trip before the first norm.
-  // Both are last-use reads (h is rewritten below), so they go non-temporal
-  // and leave L2 to the operands other kernels re-read; the forward's two
-  // sequence groups share the cache.
-  f32x4_t x[NC], hv[NC];
-  const f32x4_t* op = reinterpret_cast<const f32x4_t*>(orow) + j;
+__device__ __forceinline__ float sg_post_res_norm_f4(f32x4_t (&x)[NC], const f32x4_t (&hv)[NC],
+                                                     float* __restrict__ hrow, const float* __restrict__ w_post,
+                                                     const float* __restrict__ w_next, float eps,
+                                                     float* __restrict__ xrow, float* tile, int r, int j) {
   f32x4_t* hp = reinterpret_cast<f32x4_t*>(hrow) + j;
-#pragma unroll
-  for (int c = 0; c < NC; c++) x[c] = __builtin_nontemporal_load(&op[8 * c]);
-#pragma unroll
-  for (int c = 0; c < NC; c++) hv[c] = __builtin_nontemporal_load(&hp[8 * c]);
   if (w_post) sg_rmsnorm8_f4<NC>(x, w_post, tile, r, j, eps);
 #pragma unroll
   for (int c = 0; c < NC; c++) {
@@ -345,4 +378,93 @@ __device__ __forceinline__ float sg_post_res_norm_row(const float* __restrict__ 
 #pragma unroll
     for (int t = 0; t < 4; t++) m = fmaxf(m, fabsf(x[c][t]));
   return m;
+}
+
+// sg_post_res_norm_f4 (w_post and w_next required; xn stored when XN) for a
+// row whose o sits in LDS (srow, shared by the row's 8-lane group;
+// overwritten with h).  The sums of squares read srow in the AVX2 lane order
+// directly (lane v: elements 8i + v, i ascending), the values and order the
+// transpose tile gives.  h is streamed in quarters -- hv holds the first one,
+// loaded by the caller; the next quarter's loads are issued as the current one
+// is consumed -- and the new h goes back into srow, where the second norm
+// reads it, so the row never sits in registers whole.  The norm weights may be
+// LDS copies.
+template <int NC, bool XN>
+__device__ __forceinline__ float sg_post_res_norm_lds(float* srow, float* __restrict__ hrow, f32x4_t (&hv)[NC / 4],
+                                                      const float* w_post, const float* w_next, float eps,
+                                                      float* __restrict__ xrow, int j) {
+  constexpr int D = NC * 32, QB = NC / 4;
+  static_assert(NC % 4 == 0, "four quarters of h");
+  f32x4_t* sp = reinterpret_cast<f32x4_t*>(srow) + j;
+  f32x4_t* hp = reinterpret_cast<f32x4_t*>(hrow) + j;
+  // The chain's LDS reads go in groups of 16, the group's offset passed
+  // through an empty asm that takes the chain value: the next group's reads
+  // depend on the previous group's FMAs, so at most 16 of the D / 8 values are
+  // live at once (the scheduler would otherwise issue every read first).
+  auto inv_rms = [&]() {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i0 = 0; i0 < D / 8; i0 += 16) {
+      int off = 8 * i0 + j;
+      asm volatile("" : "+v"(off) : "v"(acc));
+      float a[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) a[i] = srow[off + 8 * i];
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc = __builtin_fmaf(a[i], a[i], acc);
+    }
+    const float ms = sg_hsum8(acc) / (float)D;
+    return 1.0f / sg_sqrt(ms + eps);
+  };
+  const float inv = inv_rms();
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int k = c % QB;
+    f32x4_t v = sp[8 * c];
+    const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(w_post + 32 * c + 4 * j);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const float u = v[t] * inv;
+      v[t] = u * wv[t] + hv[k][t];
+    }
+    if (c + QB < NC) hv[k] = __builtin_nontemporal_load(&hp[8 * (c + QB)]);  // the next quarter's chunk
+    hp[8 * c] = v;
+    sp[8 * c] = v;  // every lane of the group read o of chunk c (same instruction) before
+  }
+  asm volatile("" ::: "memory");  // LDS operations of a wave complete in issue order
+  const float inv2 = inv_rms();
+  float m = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    f32x4_t v = sp[8 * c];
+    const f32x4_t wv = *reinterpret_cast<const f32x4_t*>(w_next + 32 * c + 4 * j);
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      const float u = v[t] * inv2;
+      v[t] = u * wv[t];
+      m = fmaxf(m, fabsf(v[t]));
+    }
+    if constexpr (XN) reinterpret_cast<f32x4_t*>(xrow)[8 * c + j] = v;
+  }
+  return m;
+}
+
+// sg_post_res_norm_f4 with o and h read from memory (orow, hrow).
+template <int NC>
+__device__ __forceinline__ float sg_post_res_norm_row(const float* __restrict__ orow, float* __restrict__ hrow,
+                                                      const float* __restrict__ w_post,
+                                                      const float* __restrict__ w_next, float eps,
+                                                      float* __restrict__ xrow, float* tile, int r, int j) {
+  // o and h are loaded together: one memory round trip before the first norm.
+  // Both are last-use reads (h is rewritten), so they go non-temporal and
+  // leave L2 to the operands other kernels re-read; the forward's two
+  // sequence groups share the cache.
+  f32x4_t x[NC], hv[NC];
+  const f32x4_t* op = reinterpret_cast<const f32x4_t*>(orow) + j;
+  const f32x4_t* hp = reinterpret_cast<const f32x4_t*>(hrow) + j;
+#pragma unroll
+  for (int c = 0; c < NC; c++) x[c] = __builtin_nontemporal_load(&op[8 * c]);
+#pragma unroll
+  for (int c = 0; c < NC; c++) hv[c] = __builtin_nontemporal_load(&hp[8 * c]);
+  return sg_post_res_norm_f4<NC>(x, hv, hrow, w_post, w_next, eps, xrow, tile, r, j);
 }

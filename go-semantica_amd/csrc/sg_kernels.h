@@ -102,6 +102,16 @@ hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St
 // with row_seq) collects the sequences' max|g|.
 hipError_t gemm_q8_gelu(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale,
                         float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s);
+// gemm_q8 followed by post_res_norm on its output (N = d): o = the GEMM, then
+// h = RMSNorm(o; w_post) + h, xn = RMSNorm(h; w_next) (stored when xn !=
+// null), amax (optional, with row_seq) per sequence of max|xn|.  For N = 768
+// and large M one launch computes whole rows and norms them without storing o
+// (o is then left untouched); h, xn and amax are bit-identical either way.
+hipError_t gemm_q8_res_norm(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale,
+                            float* o, int M, int N, int K, float* h, const float* w_post, const float* w_next, float eps,
+                            float* xn, const int32_t* row_seq, float* amax, hipStream_t s);
+// Whether gemm_q8_res_norm runs as one launch for these arguments.
+bool gemm_res_norm_fused(int M, int N, const float* w_post, const float* w_next);
 // Gate/up interleaving used by gemm_q8_gelu: source row r of a matrix goes to
 // row row_off + (r / 32) * 64 + r % 32 (gate: row_off 0, up: row_off 32).
 constexpr int kGeluGroup = 32;

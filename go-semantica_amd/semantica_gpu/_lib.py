@@ -73,8 +73,8 @@ class ModelDesc(ctypes.Structure):
     ]
 
 
-SG_K_CLASSES = 7
-KERNEL_CLASSES = ("gemm", "attention", "quantize", "norm", "gelu", "pool", "other")
+SG_K_CLASSES = 8
+KERNEL_CLASSES = ("gemm", "attention", "quantize", "norm", "gelu", "pool", "other", "gemm_norm")
 
 
 class TokenizerConfig(ctypes.Structure):

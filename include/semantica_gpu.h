@@ -20,7 +20,7 @@
 extern "C" {
 #endif
 
-#define SG_ABI_VERSION 1
+#define SG_ABI_VERSION 2
 
 /* Status codes.  The first four are the error cases of forwardINT8WithDim
  * (internal/runtime/model_int8.go:150-171) and ForwardWithDim
@@ -158,14 +158,16 @@ int sg_forward_trace(sg_model *model, const int32_t *d_tokens, const int32_t *se
  * for the bandwidth kernels).  sg_profile_read synchronizes and returns the
  * totals since the last enable. */
 enum {
-  SG_K_GEMM = 0,      /* Q8_0 GEMMs (QKV, O, gate/up, down)          */
+  SG_K_GEMM = 0,      /* Q8_0 GEMMs (QKV, gate/up; O and down below the fused size) */
   SG_K_ATTENTION = 1, /* fused MQA attention                          */
   SG_K_QUANTIZE = 2,  /* per-sequence int8 quantization               */
   SG_K_NORM = 3,      /* embed+norm, post-norm+residual+norm, QK-norm+RoPE */
   SG_K_GELU = 4,      /* GELUQuick * up                               */
   SG_K_POOL = 5,      /* mean-pool + L2                               */
   SG_K_OTHER = 6,     /* fills                                        */
-  SG_K_CLASSES = 7
+  SG_K_GEMM_NORM = 7, /* O / down GEMM with the residual post-norm in one launch
+                         (work: the GEMM's int8 ops)                   */
+  SG_K_CLASSES = 8
 };
 typedef struct sg_profile {
   double ms[SG_K_CLASSES];        /* summed event time of the class's launches */

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_error_string():
     from semantica_gpu import _lib
     lib = _lib.load()
-    assert lib.sg_abi_version() == 1
+    assert lib.sg_abi_version() == 2
     assert isinstance(lib.sg_last_error(), bytes)
 
 

@@ -240,7 +240,10 @@ def test_sequence_groups_match_one_stream(tiny_gpu):
     its own stream, so the kernels of the two groups overlap on the GPU.  Each
     sequence's arithmetic is unchanged.  Ragged batches of 8k to 35k tokens are
     bit-identical to the same batch on one stream (the profiled path runs one
-    group).  Out-of-range tokens in two later groups report the
+    group).  The batches of ~10k and ~13k tokens also compare the two forms of
+    the O/down projection + residual post-norm: one group of 8192+ rows runs the
+    fused whole-row GEMM kernel (o never stored), each half-size group the GEMM
+    and k_post_res_norm as two launches.  Out-of-range tokens in two later groups report the
     earlier one, as the reference's request order does (api.go:286-292), on both
     the host and the device entry points."""
     import torch
