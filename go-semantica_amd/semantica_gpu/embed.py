@@ -52,6 +52,22 @@ class EmbedError(ValueError):
     pass
 
 
+class Cancelled(EmbedError):
+    """ctx.Err() of a cancelled context (context.Canceled): raised instead of
+    starting the next unit of work."""
+
+
+def _check_ctx(ctx):
+    """The `select { case <-ctx.Done(): ... }` of EmbedSingleInput
+    (pkg/ggufembed/api.go:190-195) and embedPrompts (:268-273).  ctx: None
+    (never cancelled), an object with is_set() (threading.Event), or a
+    callable returning True once cancelled."""
+    if ctx is None:
+        return
+    if ctx.is_set() if hasattr(ctx, "is_set") else ctx():
+        raise Cancelled("context canceled")
+
+
 @dataclasses.dataclass
 class EmbedInput:
     """ggufembed.EmbedInput (tasks.go:62-82)."""
@@ -111,21 +127,26 @@ class EmbedRuntime:
     def max_seq_len(self) -> int:
         return self.model.max_seq_len
 
-    def embed(self, texts):
+    # ctx (every method): the reference's context.Context argument, see
+    # _check_ctx; a cancelled ctx raises Cancelled before the next tokenize or
+    # forward starts (work already on the GPU completes).
+
+    def embed(self, texts, ctx=None):
         """Embed (api.go:142-158): TaskSearchQuery prompts, DefaultEmbedDim."""
         if len(texts) == 0:
             return None
-        return self.embed_inputs([EmbedInput(Task.SEARCH_QUERY, t, dim=512) for t in texts])
+        return self.embed_inputs([EmbedInput(Task.SEARCH_QUERY, t, dim=512) for t in texts], ctx)
 
-    def embed_single(self, text: str):
+    def embed_single(self, text: str, ctx=None):
         """EmbedSingle (api.go:160-166)."""
-        return self.embed_single_input(EmbedInput(Task.SEARCH_QUERY, text, dim=512))
+        return self.embed_single_input(EmbedInput(Task.SEARCH_QUERY, text, dim=512), ctx)
 
-    def embed_single_input(self, inp: EmbedInput):
-        """EmbedSingleInput (api.go:189-209)."""
-        return self._embed([build_prompt(inp)], [resolve_dim(inp.dim)])[0]
+    def embed_single_input(self, inp: EmbedInput, ctx=None):
+        """EmbedSingleInput (api.go:189-209): the context is checked first."""
+        _check_ctx(ctx)
+        return self._embed([build_prompt(inp)], [resolve_dim(inp.dim)], ctx)[0]
 
-    def embed_inputs(self, inputs):
+    def embed_inputs(self, inputs, ctx=None):
         """EmbedInputs (api.go:168-187)."""
         if len(inputs) == 0:
             return None
@@ -139,11 +160,14 @@ class EmbedRuntime:
                 dims.append(resolve_dim(inp.dim))
             except ValueError as e:
                 raise EmbedError(f"input {i}: {e}") from None
-        return self._embed(prompts, dims)
+        return self._embed(prompts, dims, ctx)
 
-    def _embed(self, prompts, dims):
+    def _embed(self, prompts, dims, ctx=None):
         """embedPrompt's checks (api.go:211-234) for every prompt, then one
-        packed forward per distinct dimension; results in input order."""
+        packed forward per distinct dimension; results in input order.  The
+        context is checked before tokenizing and before each forward (the
+        reference checks it before each prompt)."""
+        _check_ctx(ctx)
         ids, off = self.tokenizer.encode_batch(prompts)
         max_len = self.model.max_seq_len
         for i in range(len(prompts)):
@@ -157,6 +181,7 @@ class EmbedRuntime:
             sub_off = np.zeros(len(sel) + 1, np.int32)
             sub_off[1:] = np.cumsum([len(s) for s in seqs])
             toks = np.concatenate(seqs).astype(np.int32) if sub_off[-1] else np.zeros(1, np.int32)
+            _check_ctx(ctx)
             try:
                 emb = self.model.forward_packed(toks, sub_off, d)
             except _lib.SemanticaError as e:

@@ -272,3 +272,44 @@ def test_build_prompt():
         build_prompt(EmbedInput(42, "q"))
     # strings.TrimSpace keeps U+001F (not unicode.IsSpace), unlike str.strip()
     assert build_prompt(EmbedInput(Task.NONE, "\x1fa\x1f")) == "\x1fa\x1f"
+
+
+def test_embed_cancellation_stops_before_work():
+    """A cancelled context (api.go:190-195, :268-273) raises before the next
+    tokenize or forward starts; a live one lets the calls through.  Stub
+    tokenizer and model record what ran (host logic only, no device)."""
+    import threading
+    from semantica_gpu.embed import Cancelled, EmbedInput, EmbedRuntime, Task
+    calls = []
+
+    class Tok:
+        def encode_batch(self, prompts):
+            calls.append("tokenize")
+            off = np.arange(len(prompts) + 1, dtype=np.int32)
+            return np.ones(len(prompts), np.int32), off
+
+    class Mdl:
+        max_seq_len = 2048
+
+        def forward_packed(self, toks, off, d):
+            calls.append(f"forward {d}")
+            if d == 768:  # cancelled during the first dimension's forward
+                ev.set()
+            return np.zeros((len(off) - 1, d), np.float32)
+
+    rt = EmbedRuntime(None, Mdl(), Tok())
+    ev = threading.Event()
+    inputs = [EmbedInput(Task.SEARCH_QUERY, "a", dim=768), EmbedInput(Task.SEARCH_QUERY, "b", dim=256)]
+    with pytest.raises(Cancelled, match="context canceled"):
+        rt.embed_inputs(inputs, ctx=ev)  # dims run largest first: 256's forward never starts
+    assert calls == ["tokenize", "forward 768"]
+    calls.clear()
+    with pytest.raises(Cancelled):
+        rt.embed(["x"], ctx=ev)  # already cancelled: nothing runs
+    with pytest.raises(Cancelled):
+        rt.embed_single_input(EmbedInput(Task.NONE, "x"), ctx=lambda: True)
+    assert calls == []
+    ev = threading.Event()
+    out = rt.embed_inputs([inputs[1]], ctx=ev)
+    assert [o.shape[0] for o in out] == [256] and calls == ["tokenize", "forward 256"]
+    assert rt.embed_single("x", ctx=None).shape == (512,)
