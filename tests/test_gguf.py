@@ -108,3 +108,71 @@ def test_errors(case, msg):
         img = img[:60]
     e = _err(img)
     assert e.code == _lib.SG_ERR_INVALID and msg in e.message, e.message
+
+
+def _hand_image():
+    """A GGUF v3 image assembled field by field in the order reader.go:98-178
+    parses it (independent of synth.py): header (magic, version, tensor
+    count, metadata count), key/value pairs (u64-length key, u32 value type,
+    value), tensor infos (name, u32 n_dims, u64 dims, u32 dtype, u64 offset),
+    then the data at the next 32-byte boundary."""
+    import struct
+
+    def s(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+
+    def kv(key, typ, payload):
+        return s(key) + struct.pack("<I", typ) + payload
+
+    def arr(typ, items):
+        return struct.pack("<IQ", typ, len(items)) + b"".join(items)
+
+    p = "gemma-embedding."
+    kvs = [
+        kv("general.architecture", 8, s("gemma-embedding")),
+        kv("x.u8", 0, struct.pack("<B", 250)), kv("x.i8", 1, struct.pack("<b", -5)),
+        kv("x.u16", 2, struct.pack("<H", 65000)), kv("x.i16", 3, struct.pack("<h", -300)),
+        kv("x.i32", 5, struct.pack("<i", -70000)), kv("x.u64", 10, struct.pack("<Q", 1 << 40)),
+        kv("x.i64", 11, struct.pack("<q", -(1 << 40))), kv("x.f64", 12, struct.pack("<d", 0.5)),
+        kv("x.bool", 7, b"\x01"),
+        kv("x.nested", 9, arr(9, [arr(0, [b"\x01"]), arr(4, [struct.pack("<I", 2), struct.pack("<I", 3)])])),
+        kv(p + "embedding_length", 4, struct.pack("<I", 768)),
+        kv(p + "block_count", 4, struct.pack("<I", 2)),
+        kv(p + "attention.head_count", 4, struct.pack("<I", 3)),
+        kv(p + "attention.head_count_kv", 4, struct.pack("<I", 1)),
+        kv(p + "feed_forward_length", 4, struct.pack("<I", 1152)),
+        kv(p + "context_length", 4, struct.pack("<I", 512)),
+        kv(p + "attention.layer_norm_rms_epsilon", 6, struct.pack("<f", 1e-6)),
+        kv(p + "rope.freq_base", 6, struct.pack("<f", 1e6)),
+        kv("tokenizer.ggml.tokens", 9, arr(8, [s("<pad>"), s("a"), s("bc")])),
+    ]
+    tensor = s("output_norm.weight") + struct.pack("<I", 1) + struct.pack("<Q", 4) + struct.pack("<IQ", 0, 0)
+    head = b"GGUF" + struct.pack("<IQQ", 3, 1, len(kvs))
+    body = head + b"".join(kvs) + tensor
+    body += b"\0" * (-len(body) % 32)
+    return body + struct.pack("<4f", 1, 2, 3, 4)
+
+
+def test_hand_assembled_image():
+    """parseConfig over an image built byte by byte from the format (not by
+    the repository's writer), with every metadata value type and a nested
+    array ahead of the model keys."""
+    from semantica_gpu import read_gguf_config
+    cfg = read_gguf_config(_hand_image())
+    assert cfg == {"embed_dim": 768, "num_layers": 2, "num_heads": 3, "num_kv_heads": 1, "interm_dim": 1152,
+                   "max_seq_len": 512, "vocab_size": 3, "norm_eps": pytest.approx(1e-6, rel=1e-6),
+                   "rope_base": 1e6}
+
+
+def test_hand_assembled_image_truncations():
+    """Every cut inside the header or a key/value pair fails as the reference
+    does (header: 'file too small for header'; later: 'read metadata i'),
+    never reading past the image."""
+    from semantica_gpu import SemanticaError, read_gguf_config
+    img = _hand_image()
+    for cut in list(range(0, 24, 5)) + list(range(24, 200, 7)):
+        with pytest.raises(SemanticaError) as ei:
+            read_gguf_config(img[:cut])
+        want = "file too small for header" if cut < 24 else "read metadata"
+        assert want in ei.value.message, (cut, ei.value.message)
