@@ -223,6 +223,10 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 3);
   const int j = threadIdx.x & 7, r = (threadIdx.x >> 3) & 7;
   if (row >= T) return;  // whole 8-lane groups: the group reductions stay complete
+  // The sequence's maximum first: its two dependent loads then overlap the
+  // row's loads instead of following the norm (whose LDS steps they cannot
+  // cross).
+  const float m = amax[row_seq[row]];
   f32x4_t x[NC];
   const f32x4_t* hr = reinterpret_cast<const f32x4_t*>(h + (int64_t)row * D) + j;
 #pragma unroll
@@ -230,7 +234,6 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
   // left to the operands they re-read (two sequence groups share it).
   for (int c = 0; c < NC; c++) x[c] = __builtin_nontemporal_load(&hr[8 * c]);
   sg_rmsnorm8_f4<NC>(x, w, tiles[threadIdx.x / SG_WAVE], r, j, eps);
-  const float m = amax[row_seq[row]];
   float scale = 1.0f, inv = 0.0f;
   if (m != 0.0f) {
     scale = m / 127.0f;
