@@ -324,9 +324,10 @@ struct Lane {
 // the other group's work, and at times one group's bandwidth-bound row kernels
 // beside the other's GEMMs), with every sequence's arithmetic unchanged.  A
 // group gets at least kLaneMinTokens tokens.  Two groups measured best at
-// 64 x 512 tokens on MI355X (19.2 ms per batch against 20.1 for one, 19.4 for
-// three; four leave two streams on one of the process's four hardware queues
-// and lose to one group).
+// 64 x 512 tokens on MI355X (first: 19.2 ms per batch against 20.1 for one,
+// 19.4 for three; with the fused GEMM + residual post-norm kernels: 16.80
+// against 17.56 for three; four leave two streams on one of the process's
+// four hardware queues and lose to one group).
 constexpr int kLanes = 2;
 constexpr int kLaneMinTokens = 4096;
 
