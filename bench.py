@@ -329,7 +329,8 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {a.gpus} requested); the path shards as "
-              "pure data parallelism over sequences, see DESIGN.md", file=sys.stderr)
+              "pure data parallelism over sequences (each rank embeds its own bin of sequences with the "
+              "replicated weights; only the embeddings are gathered)", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
