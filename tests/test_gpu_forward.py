@@ -543,3 +543,41 @@ def test_embed_texts_end_to_end(tiny_gpu, tiny_model):
             rt.embed_inputs([embed.EmbedInput(content="a", dim=300)])
     finally:
         rt.close()
+
+
+@pytest.mark.parametrize("lens", [
+    [40, 64, 33],          # small batch: register-direct GEMMs, separate post-norm kernel
+    [1024] * 16,           # 16384 tokens: the LDS GEMMs and the fused GEMM + residual post-norm
+])
+def test_teacher_forced_zero_activations(gpu_ctx, oracle, lens):
+    """Sequences whose activations are exactly zero.  Token IDs below 64 get an
+    all-zero embedding row (Q8_0 scale 0, codes 0).  Sequence 0 uses only those
+    tokens, so every quantize site sees a per-sequence max of 0 (scale 1, codes
+    0: quantize.go's m == 0 case), its attention scores are all 0 (uniform
+    weights), and its pooled vector is zero, which L2 normalization leaves as
+    is (model.go:808-820).  Sequence 1 mixes zero rows into ordinary ones
+    (RMSNorm of a zero row inside a sequence with a non-zero max).  The rest
+    are ordinary.  Teacher-forced through both layers of the 2-layer model:
+    Q|K|V, h and the final embeddings bit-identical to the oracle."""
+    import dataclasses
+    from semantica_gpu import Model, synth
+    from conftest import TINY
+    base = synth.make_model(TINY)
+    emb = base.token_embd.copy()
+    emb[:64] = 0
+    mdl = dataclasses.replace(base, token_embd=emb)
+    off = synth.offsets_from_lengths(lens)
+    T = int(off[-1])
+    toks = synth.token_ids(T, TINY["vocab_size"], seed=11)
+    rng = np.random.default_rng(12)
+    toks[off[0]:off[1]] = rng.integers(0, 64, lens[0])
+    s1 = np.arange(off[1], off[2])
+    toks[s1[::3]] = rng.integers(0, 64, len(s1[::3]))
+    m = Model(gpu_ctx, mdl)
+    try:
+        _teacher_forced(m, oracle.OracleModel(mdl), toks, off, 768, TINY["num_layers"], f"zero rows T={T}")
+        y = m.forward_packed(toks, off, 768)
+    finally:
+        m.close()
+    assert not np.any(y[0]), "an all-zero sequence embeds to the zero vector"
+    assert np.all(np.isfinite(y))
