@@ -244,6 +244,32 @@ int gemm_scratch_end(sg_ctx* c, hipStream_t s) {
   return SG_OK;
 }
 
+// Held by a GEMM entry point from gemm_scratch_begin on: every return path,
+// errors included, orders what the call enqueued on `s` before the next use
+// of the context's GEMM scratch (a8, the gate/up interleave).  The success
+// path calls finish(); an early return ends the use in the destructor
+// without touching the error message already set.  If the event cannot be
+// recorded, the stream is drained instead.
+struct ScratchUse {
+  sg_ctx* c;
+  hipStream_t s;
+  bool done = false;
+  ScratchUse(sg_ctx* c_, hipStream_t s_) : c(c_), s(s_) {}
+  ScratchUse(const ScratchUse&) = delete;
+  ScratchUse& operator=(const ScratchUse&) = delete;
+  int finish() {
+    done = true;
+    const int r = gemm_scratch_end(c, s);
+    if (r != SG_OK) (void)hipStreamSynchronize(s);
+    return r;
+  }
+  ~ScratchUse() {
+    if (done) return;
+    if (hipEventRecord(c->gemm_done, s) == hipSuccess) c->gemm_pending = true;
+    else (void)hipStreamSynchronize(s);
+  }
+};
+
 int set_device(sg_ctx* c) {
   SG_HIP(hipSetDevice(c->device));
   return SG_OK;
@@ -291,7 +317,7 @@ struct Profiler {
 
 // One sequence group's forward: activation workspace (grown on demand),
 // metadata staging, the token-error flag, and for groups after the first a
-// stream of its own (created on first use, default flags and priority) with
+// stream of its own (created on first use, non-blocking, default priority) with
 // the event that joins it back to the caller's stream.
 struct Lane {
   DevBuf h, xn, qkv, att, o, g, a8, sx, amax, meta_d, err;
@@ -990,6 +1016,7 @@ static int matmul_common(sg_ctx* ctx, float* dst, int32_t* sums, const sg_q8_wei
   const int ar = sgk::gemm_pad_rows(batch);
   SG_TRY(ctx->a8.ensure((size_t)ar * w->K));
   SG_TRY(gemm_scratch_begin(ctx, s));
+  ScratchUse use(ctx, s);
   int8_t* a8 = ctx->a8.as<int8_t>();
   SG_HIP(sgk::i8_blocked(x, batch, w->K, a8, ar, s));
   if (sums) {  // parity dump: synchronous (a temporary output buffer)
@@ -1006,7 +1033,7 @@ static int matmul_common(sg_ctx* ctx, float* dst, int32_t* sums, const sg_q8_wei
     return SG_OK;
   }
   SG_HIP(sgk::gemm_q8(a8, ar, w->w8, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s));
-  return gemm_scratch_end(ctx, s);
+  return use.finish();
 }
 
 int sg_matmul_q8_0_int8(sg_ctx* ctx, float* dst, const sg_q8_weight* w, const int8_t* x, const float* row_scale,
@@ -1024,6 +1051,7 @@ int sg_matmul_q8_0_int8_bench(sg_ctx* ctx, float* dst, const sg_q8_weight* w, co
   const int ar = sgk::gemm_pad_rows(batch);
   SG_TRY(ctx->a8.ensure((size_t)ar * w->K));
   SG_TRY(gemm_scratch_begin(ctx, s));
+  ScratchUse use(ctx, s);
   int8_t* a8 = ctx->a8.as<int8_t>();
   SG_HIP(sgk::i8_blocked(x, batch, w->K, a8, ar, s));
   auto gemm = [&]() { return sgk::gemm_q8(a8, ar, w->w8, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s); };
@@ -1043,7 +1071,7 @@ int sg_matmul_q8_0_int8_bench(sg_ctx* ctx, float* dst, const sg_q8_weight* w, co
   (void)hipEventDestroy(e1);
   SG_HIP(e);
   *us_per_launch = ms * 1000.0f / (float)reps;
-  return gemm_scratch_end(ctx, s);
+  return use.finish();
 }
 
 int sg_q8_block_sums(sg_ctx* ctx, int32_t* out, const sg_q8_weight* w, const int8_t* x, int32_t batch, void* stream) {
@@ -1055,6 +1083,9 @@ int sg_ffn_gate_up(sg_ctx* ctx, float* dst, const sg_q8_weight* w_gate, const sg
   if (!ctx || !dst || !w_gate || !w_up || !x || !row_scale) return fail(SG_ERR_INVALID, "NULL argument");
   if (w_gate->N != w_up->N || w_gate->K != w_up->K || w_gate->N % sgk::kGeluGroup)
     return fail(SG_ERR_INVALID, "gate and up must have the same shape, out_dim a multiple of 32");
+  // The interleave cache on the gate weight is guarded by its context's
+  // mutex and ordered on that context's GEMM scratch event only.
+  if (w_gate->ctx != ctx || w_up->ctx != ctx) return fail(SG_ERR_INVALID, "weights belong to another context");
   if (batch < 0) return fail(SG_ERR_INVALID, "batch < 0");
   if (batch == 0) return SG_OK;
   std::lock_guard<std::mutex> lk(ctx->mu);
@@ -1071,6 +1102,7 @@ int sg_ffn_gate_up(sg_ctx* ctx, float* dst, const sg_q8_weight* w_gate, const sg
   const size_t nch = (size_t)(K / 32) * (N / sgk::kGeluGroup);
   SG_TRY(ctx->a8.ensure((size_t)ar * K));
   SG_TRY(gemm_scratch_begin(ctx, s));
+  ScratchUse use(ctx, s);
   const bool rebuild = w_gate->pair_up != w_up->id;
   if (rebuild) {
     w_gate->pair_up = 0;  // invalid until the copies below are enqueued
@@ -1089,7 +1121,7 @@ int sg_ffn_gate_up(sg_ctx* ctx, float* dst, const sg_q8_weight* w_gate, const sg
   SG_HIP(sgk::i8_blocked(x, batch, K, a8, ar, s));
   SG_HIP(sgk::gemm_q8_gelu(a8, ar, reinterpret_cast<const int8_t*>(wi), reinterpret_cast<const float*>(si), row_scale,
                            dst, batch, N, K, nullptr, nullptr, s));
-  return gemm_scratch_end(ctx, s);
+  return use.finish();
 }
 
 int sg_rmsnorm(sg_ctx* ctx, float* dst, const float* src, const float* weight, int32_t rows, int32_t n, float eps,

@@ -66,10 +66,17 @@ extern "C" int sg_matmul_q8_0_int8_noalloc(sg_ctx* ctx, float* dst, const sg_q8_
   if (need > SG_NOALLOC_SCRATCH_BYTES)
     return fail(SG_ERR_INVALID, "batch %d x in_dim %d needs %zu bytes of operand scratch; the limit is %u", batch,
                 w->K, need, (unsigned)SG_NOALLOC_SCRATCH_BYTES);
-  SG_HIP(hipSetDevice(dev));
+  // The launches go to the context's device; the calling thread's current
+  // device is put back before returning, on every path.
+  int prev = -1;
+  SG_HIP(hipGetDevice(&prev));
+  if (prev != dev) SG_HIP(hipSetDevice(dev));
   const hipStream_t s = sgi::ctx_stream(ctx, stream);
   int8_t* a8 = static_cast<int8_t*>(p);
-  SG_HIP(sgk::i8_blocked(x, batch, w->K, a8, ar, s));
-  SG_HIP(sgk::gemm_q8(a8, ar, w->w8, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s));
+  hipError_t e = sgk::i8_blocked(x, batch, w->K, a8, ar, s);
+  if (e == hipSuccess) e = sgk::gemm_q8(a8, ar, w->w8, w->st, row_scale, dst, nullptr, batch, w->N, w->K, s);
+  const hipError_t er = prev != dev ? hipSetDevice(prev) : hipSuccess;
+  SG_HIP(e);
+  SG_HIP(er);
   return SG_OK;
 }

@@ -176,3 +176,16 @@ def test_hand_assembled_image_truncations():
             read_gguf_config(img[:cut])
         want = "file too small for header" if cut < 24 else "read metadata"
         assert want in ei.value.message, (cut, ei.value.message)
+
+
+def test_hand_assembled_model_image_config():
+    """parseConfig over the full hand-assembled model image (tests/gguf_hand.py:
+    every tensor the model reads, at unaligned and out-of-order offsets):
+    the configuration its metadata states, with the vocabulary from the
+    token list."""
+    import gguf_hand
+    from semantica_gpu import read_gguf_config
+    image, cfg, placed, norms = gguf_hand.hand_model_image()
+    assert read_gguf_config(image) == pytest.approx(cfg)
+    assert any(a % 32 for a, _ in placed.values())  # some payloads are unaligned
+    assert "output_norm.weight" not in placed and "blk.1.attn_k_norm.weight" not in placed

@@ -73,6 +73,19 @@ def _check_envelope(got, oracle_model, toks, off, dim, tag, threads=16):
     say(f"{tag}: north_star bar (max-abs <= {NORTH_STAR_MAX_ABS:g}, cos >= {NORTH_STAR_COS}) against the VNNI path: "
         f"GPU {verdict(g_mad, g_dc)}; the reference's own AVX2 / block-FMA / arm64 paths: "
         + ", ".join(f"{n} {verdict(*e)}" for n, e in zip(REF_ORDERS, env)))
+    # Against the path the GPU reproduces (the block-serial fallback order,
+    # matmul_inner_loop_fallback.go:16-43, through model_int8.go:148-256):
+    # every kernel but attention's two products is bit-exact to it
+    # (_teacher_forced), so what is left is attention's fp32-class rounding
+    # (<= 1e-5 relative per layer) carried through the int8 re-quantizations.
+    b_mad, b_dc = _stats(got, refs["block_fma"])
+    say(f"{tag}: gpu-vs-block-serial max-abs max {b_mad.max():.2e} mean {b_mad.mean():.2e} "
+        f"1-cos max {b_dc.max():.2e} mean {b_dc.mean():.2e}; north_star bar against the block-serial path: "
+        f"GPU {verdict(b_mad, b_dc)}")
+    assert b_mad.max() <= 2.0 * e_mad.max() + 1e-4
+    assert b_mad.mean() <= 2.0 * e_mad.mean() + 1e-4
+    assert b_dc.max() <= 4.0 * e_dc.max() + 1e-6
+    assert b_dc.max() <= 1e-3
     # The spread comes from int8 re-quantization flips, whose number per
     # sequence is random; a systematic error would sit far above these bounds.
     assert g_mad.max() <= 2.0 * e_mad.max() + 1e-4
@@ -185,6 +198,47 @@ def test_gguf_load_matches_descriptor_load(gpu_ctx, tiny_gpu, tiny_model, tmp_pa
     assert "expected Q8_0, got F16 for blk.0.attn_q.weight" in ei.value.message
 
 
+def test_hand_assembled_gguf_payloads_vs_oracle(gpu_ctx, oracle, tmp_path):
+    """GGUF payload parity independent of the repository's writer and loader
+    (reader.go:98-178, model.go:424-552, model_int8.go:54-140).  The image is
+    assembled field by field in tests/gguf_hand.py: a 2-layer model with the
+    token embedding, every Q8_0 matrix and norm at unaligned, out-of-order
+    offsets, one Q8_0-stored norm, three optional norms absent and an unused
+    tensor between them.  The GPU loads it through sg_model_load_gguf (from
+    bytes and from a file); the oracle gets each matrix's bytes straight out
+    of the image at the offset the assembler put them.  Teacher-forced, the
+    two agree bit for bit on Q|K|V and the residual stream at both layers and
+    on the final embeddings, with attention within 1e-5."""
+    import gguf_hand
+    from semantica_gpu import Model, synth
+    image, cfg, placed, norms = gguf_hand.hand_model_image()
+    om = oracle.OracleModel(gguf_hand.oracle_model(image, cfg, placed, norms))
+    lens = [1, 9, 32, 77, 200, 3]
+    off = synth.offsets_from_lengths(lens)
+    toks = np.random.default_rng(4).integers(0, cfg["vocab_size"], size=int(off[-1])).astype(np.int32)
+    say(f"hand-assembled gguf: {len(image)} bytes, {len(placed)} tensors, lens={lens}")
+    gm = Model.from_gguf(gpu_ctx, image)
+    try:
+        assert gm.config == pytest.approx(cfg)
+        _teacher_forced(gm, om, toks, off, 768, cfg["num_layers"], "hand gguf")
+        want = gm.forward_packed(toks, off, 256)
+        rc, ref = om.forward_batch(toks, off, 256, order=oracle.ORDER_BLOCK_SERIAL, n_threads=4)
+        assert rc == 0
+        mad, dc = _stats(want, ref)
+        say(f"hand gguf free-running vs block-serial oracle, dim 256: max-abs {mad.max():.2e} 1-cos {dc.max():.2e}")
+        assert mad.max() <= NORTH_STAR_MAX_ABS and dc.max() <= 1.0 - NORTH_STAR_COS
+    finally:
+        gm.close()
+    path = tmp_path / "hand.gguf"
+    path.write_bytes(image)
+    fm = Model.from_gguf(gpu_ctx, str(path))
+    try:
+        assert np.array_equal(fm.forward_packed(toks, off, 256).view(np.uint32), want.view(np.uint32))
+    finally:
+        fm.close()
+    om.close()
+
+
 def test_forward_errors(tiny_gpu):
     from semantica_gpu import SemanticaError, _lib
     say("forward error cases")
@@ -243,9 +297,10 @@ def test_sequence_groups_match_one_stream(tiny_gpu):
     group).  The batches of ~10k and ~13k tokens also compare the two forms of
     the O/down projection + residual post-norm: one group of 8192+ rows runs the
     fused whole-row GEMM kernel (o never stored), each half-size group the GEMM
-    and k_post_res_norm as two launches.  Out-of-range tokens in two later groups report the
-    earlier one, as the reference's request order does (api.go:286-292), on both
-    the host and the device entry points."""
+    and k_post_res_norm as two launches.  With out-of-range tokens in both
+    groups, the one in group 0 is reported, and with one only in group 1 that
+    one, as the reference's request order does (api.go:286-292), on both the
+    host and the device entry points."""
     import torch
     from semantica_gpu import SemanticaError, _lib
     rng = np.random.default_rng(11)
@@ -264,19 +319,76 @@ def test_sequence_groups_match_one_stream(tiny_gpu):
         assert np.array_equal(y.view(np.uint32), y1.view(np.uint32))
         if T < 16384:
             continue
-        bad = toks.copy()
-        i1, i2 = int(n * 0.6), int(n * 0.9)
-        bad[off[i2]] = 5000
-        bad[off[i1 + 1] - 1] = 4096 + i1
-        with pytest.raises(SemanticaError) as eh:
-            tiny_gpu.forward_packed(bad, off, 768)
-        d_tok = torch.from_numpy(bad).cuda()
-        out = torch.empty((n, 768), dtype=torch.float32, device="cuda")
-        with pytest.raises(SemanticaError) as ed:
-            tiny_gpu.forward_device(d_tok.data_ptr(), off, 768, out.data_ptr())
-        say(f"  errors at sequences {i1} and {i2}: host '{eh.value.message}' device '{ed.value.message}'")
-        expect = (_lib.SG_ERR_TOKEN, f"token ID out of range: {4096 + i1}")
-        assert (eh.value.code, eh.value.message) == (ed.value.code, ed.value.message) == expect
+        # the groups split at the sequence edge nearest T/2: sequence n//4 ends
+        # near T/4 (group 0), sequence 0.9n starts near 0.9T (group 1)
+        i1, i2 = n // 4, int(n * 0.9)
+        assert off[i1 + 1] < T // 2 < off[i2]
+        both = toks.copy()
+        both[off[i2]] = 5000
+        both[off[i1 + 1] - 1] = 4096 + i1
+        second = toks.copy()
+        second[off[i2]] = 5000
+        for bad, tok, where in ((both, 4096 + i1, f"sequences {i1} and {i2}"), (second, 5000, f"sequence {i2}")):
+            with pytest.raises(SemanticaError) as eh:
+                tiny_gpu.forward_packed(bad, off, 768)
+            d_tok = torch.from_numpy(bad).cuda()
+            out = torch.empty((n, 768), dtype=torch.float32, device="cuda")
+            with pytest.raises(SemanticaError) as ed:
+                tiny_gpu.forward_device(d_tok.data_ptr(), off, 768, out.data_ptr())
+            say(f"  errors at {where}: host '{eh.value.message}' device '{ed.value.message}'")
+            expect = (_lib.SG_ERR_TOKEN, f"token ID out of range: {tok}")
+            assert (eh.value.code, eh.value.message) == (ed.value.code, ed.value.message) == expect
+
+
+def test_concurrent_callers_match_serial(tiny_gpu):
+    """TestConcurrentBufferPooling (internal/runtime/pooling_test.go:34-75):
+    seven host threads call sg_forward on one model at once, four times each
+    (ctypes releases the GIL for the call, so the calls overlap in the
+    library).  Each result equals the same call made alone, bit for bit,
+    whatever else runs; one thread's batches hold an out-of-range token, and
+    that thread gets its own error message (sg_last_error is per thread)
+    while the others succeed.  One batch of ~9k tokens runs as two sequence
+    groups; the dims differ per thread."""
+    import threading
+    from semantica_gpu import SemanticaError, _lib, synth
+    rng = np.random.default_rng(31)
+    jobs = []
+    for j in range(6):
+        lens = rng.integers(300, 600, size=20) if j == 5 else rng.integers(1, 400, size=int(rng.integers(1, 40)))
+        off = synth.offsets_from_lengths(lens)
+        toks = rng.integers(0, 4096, size=int(off[-1])).astype(np.int32)
+        jobs.append((toks, off, (768, 256, 128)[j % 3]))
+    bad = jobs[0][0].copy()
+    bad[-1] = 4096 + 7
+    say(f"concurrent callers: batches of {[int(o[-1]) for _, o, _ in jobs]} tokens + one with a bad token")
+    serial = [tiny_gpu.forward_packed(t, o, d) for t, o, d in jobs]
+    results, errors, crashed = {}, {}, []
+
+    def worker(j):
+        try:
+            for it in range(4):
+                if j == 6:
+                    try:
+                        tiny_gpu.forward_packed(bad, jobs[0][1], 768)
+                        errors[it] = None
+                    except SemanticaError as e:
+                        errors[it] = (e.code, e.message)
+                else:
+                    t, o, d = jobs[j]
+                    results[(j, it)] = tiny_gpu.forward_packed(t, o, d)
+        except Exception as e:  # noqa: BLE001  (reported below, on the main thread)
+            crashed.append((j, repr(e)))
+
+    threads = [threading.Thread(target=worker, args=(j,)) for j in range(7)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not crashed, crashed
+    for (j, it), y in results.items():
+        assert np.array_equal(y.view(np.uint32), serial[j].view(np.uint32)), (j, it)
+    assert len(results) == 24
+    assert all(errors[it] == (_lib.SG_ERR_TOKEN, "token ID out of range: 4103") for it in range(4)), errors
 
 
 def _teacher_forced(gpu, om, toks, off, dim, n_layers, tag, seam_layers=(), threads=16):

@@ -142,6 +142,32 @@ def test_ffn_gate_up_fused_bit_exact(gpu_ctx, oracle, M, K):
     assert np.array_equal(g_host[:m].view(np.uint32), want.view(np.uint32))
 
 
+def test_ffn_gate_up_rejects_weights_of_another_context(gpu_ctx):
+    """The gate weight caches its gate/up interleave under its own context's
+    lock and scratch event, so a call through another context is refused."""
+    import torch
+    from semantica_gpu import Context, SemanticaError, _lib, kernels, synth
+    rng = np.random.default_rng(5)
+    N, K, M = 64, 64, 4
+    other = Context(0)
+    try:
+        wg = kernels.Q8Weight(other, synth.q8_0_random(rng, N, K), N, K)
+        wu = kernels.Q8Weight(other, synth.q8_0_random(rng, N, K), N, K)
+        out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        xq = dev(rng.integers(-127, 128, size=(M, K), dtype=np.int8))
+        rs = dev(np.ones(M, np.float32))
+        say("ffn gate/up with another context's weights")
+        with pytest.raises(SemanticaError) as e:
+            kernels.ffn_gate_up(gpu_ctx, out, wg, wu, xq, rs)
+        assert e.value.code == _lib.SG_ERR_INVALID and "another context" in e.value.message
+        kernels.ffn_gate_up(other, out, wg, wu, xq, rs)  # their own context accepts them
+        torch.cuda.synchronize()
+        wg.close()
+        wu.close()
+    finally:
+        other.close()
+
+
 @pytest.mark.parametrize("M", [6, 8200, 12300])
 def test_gemm_order_pins(gpu_ctx, M):
     """The hand-derived order vectors of tests/gemm_pins.py: row i and
@@ -474,6 +500,38 @@ def test_gelu_quick_mul_bit_exact(gpu_ctx, oracle):
     got = host(out)
     ref = oracle.gelu_quick(gate) * up
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_elementwise_pins_on_gpu(gpu_ctx):
+    """The hand-derived bit-level pins (tests/elementwise_pins.py) through the
+    GPU's GELUQuick*up seam (up = 1, so g is GELUQuick's value, fastExp on both
+    sigmoid branches) and its RMSNorm seam (n = 768): the GPU gives each pin's
+    bits, without the oracle in between."""
+    import torch
+    import elementwise_pins as ep
+    from semantica_gpu import kernels
+    gel = [p for p in ep.PINS if p.fn == "gelu"]
+    xs = [u for p in gel for u in p.inputs]
+    gate = np.zeros((3, 1152), np.float32)
+    gate[1, :len(xs)] = np.array(xs, np.uint32).view(np.float32)
+    up = np.ones_like(gate)
+    say("elementwise pins: gelu")
+    out = torch.empty(gate.shape, dtype=torch.float32, device="cuda")
+    kernels.gelu_quick_mul(gpu_ctx, out, dev(gate), dev(up))
+    got = host(out)[1, :len(xs)].view(np.uint32)
+    want = [u for p in gel for u in p.expected]
+    assert [int(v) for v in got] == want, [hex(int(v)) for v in got]
+
+    for pin in (p for p in ep.PINS if p.fn == "rmsnorm"):
+        x, w = ep.rmsnorm_operands(pin)
+        xr = np.zeros((5, ep.RMS_N), np.float32)
+        xr[2] = [float(v) for v in x]
+        wr = np.array([float(v) for v in w], np.float32)
+        say(f"elementwise pins: {pin.name}")
+        y = torch.empty_like(dev(xr))
+        kernels.rmsnorm(gpu_ctx, y, dev(xr), dev(wr), float(ep.EPS))
+        got = host(y)[2, :2].view(np.uint32)
+        assert tuple(int(v) for v in got) == pin.expected, (pin.name, [hex(int(v)) for v in got])
 
 
 def test_gelu_quick_float_sweep_bit_exact(gpu_ctx, oracle):

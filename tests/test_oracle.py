@@ -378,6 +378,109 @@ def test_rope_apply_identity_and_norm(oracle):
     assert abs(np.angle(np.exp(1j * (ang - 5 * fr[7])))) < 1e-5
 
 
+# ------------------------------------------ elementwise bit-level pins ----
+
+def _bits(a) -> tuple:
+    return tuple(int(u) for u in np.asarray(a, np.float32).reshape(-1).view(np.uint32))
+
+
+def _f32(bits) -> np.ndarray:
+    return np.array(bits, np.uint32).view(np.float32)
+
+
+def pin_eval_oracle(oracle, pin) -> tuple:
+    """Runs the oracle function a pin targets on the pin's inputs; returns the
+    output bit patterns in the pin's order."""
+    import elementwise_pins as ep
+    if pin.fn == "fast_exp":
+        return tuple(_bits(oracle.fast_exp(float(v)))[0] for v in _f32(pin.inputs))
+    if pin.fn == "gelu":
+        return _bits(oracle.gelu_quick(_f32(pin.inputs)))
+    if pin.fn == "softmax":
+        return _bits(oracle.softmax(_f32(pin.inputs)))
+    if pin.fn == "rmsnorm":
+        x, w = ep.rmsnorm_operands(pin)
+        xs = np.array([float(v) for v in x], np.float32)[None]
+        ws = np.array([float(v) for v in w], np.float32)
+        return _bits(oracle.rmsnorm(xs, ws, float(ep.EPS))[0, :2])
+    if pin.fn == "rope":
+        n = len(pin.inputs)
+        row = np.array([float(p[0]) for p in pin.inputs] + [float(p[1]) for p in pin.inputs], np.float32)[None]
+        cos_t = np.array([[float(p[2]) for p in pin.inputs]], np.float32)
+        sin_t = np.array([[float(p[3]) for p in pin.inputs]], np.float32)
+        return _bits(oracle.rope_apply(row, 1, 2 * n, cos_t, sin_t))
+    raise ValueError(pin.fn)
+
+
+def test_elementwise_literals_are_the_go_float32_constants():
+    """The float32 values of the Go constants in activation.go:48,101,121-124,
+    :110 and the GGUF default eps, each by two routes: numpy's correctly
+    rounded decimal parse and the exact-rational rounding the pins use."""
+    import elementwise_pins as ep
+    for text, bits in ep.LITERALS.items():
+        assert int(np.float32(text).view(np.uint32)) == bits, text
+        assert ep.to_bits(ep.r32(ep.F(text))) == bits, text
+
+
+def test_exact_rounding_helpers_match_ieee():
+    """The derivation engine: rational -> float32 rounding equals numpy's
+    float64 -> float32 cast (correctly rounded, ties to even) on random
+    doubles, subnormal and tie cases included; the rounded sqrt equals
+    libm's sqrt in float64 and numpy's in float32."""
+    import math
+    import elementwise_pins as ep
+    rng = np.random.default_rng(77)
+    ds = np.concatenate([rng.standard_normal(3000) * 10.0 ** rng.integers(-40, 38, 3000),
+                         (rng.integers(1, 1 << 24, 300) * 2 + 1) * 2.0 ** -25,   # float32 ties
+                         rng.uniform(0, 2e-38, 200)])                             # subnormals
+    for d in ds:
+        assert ep.to_bits(ep.r32(ep.F(float(d)))) == int(np.float32(d).view(np.uint32)), d
+    for d in np.abs(rng.standard_normal(500)) * 10.0 ** rng.integers(-30, 30, 500):
+        assert ep.sqrt_rnd(ep.F(float(d)), 53) == ep.F(math.sqrt(float(d)))
+        f = np.float32(d)
+        assert ep.sqrt_rnd(ep.F(float(f)), 24) == ep.F(float(np.sqrt(f)))
+
+
+def test_elementwise_pins_model_rederives_every_value():
+    """The exact-rational model of the Go statements reproduces each pin's
+    hand-derived bits (the docstrings walk the steps)."""
+    import elementwise_pins as ep
+    for pin in ep.PINS:
+        assert ep.model_eval(pin) == pin.expected, pin.name
+
+
+@pytest.mark.parametrize("scalar", [False, True], ids=["simd", "scalar"])
+def test_elementwise_pins_oracle(oracle, scalar):
+    """fastExp, GELUQuick, Softmax, RMSNorm and the RoPE rotation of the oracle
+    give every pin's bits, on its AVX2 paths and on its scalar definitions."""
+    import elementwise_pins as ep
+    lib = oracle.load()
+    lib.sgo_force_scalar(1 if scalar else 0)
+    try:
+        for pin in ep.PINS:
+            got = pin_eval_oracle(oracle, pin)
+            assert got == pin.expected, (pin.name, [hex(v) for v in got])
+    finally:
+        lib.sgo_force_scalar(0)
+
+
+def test_elementwise_pins_catch_single_mistakes():
+    """Every plausible restatement mistake changes at least one pinned value:
+    fastExp with floor for int32(), the comment's 6-digit coefficients, fused
+    or float64 Horner steps, a float64 log2e, `x <= -10` for the clamp;
+    GELUQuick with either sigmoid form on both sides or the double 1.702;
+    Softmax summed one by one or pairwise, or divided by the sum; RMSNorm as
+    x*(inv*w), with 1/sqrt rounded once, or the mean by a reciprocal; any one
+    of the four RoPE products fused into its add."""
+    import elementwise_pins as ep
+    for fn, mutants in ep.MUTANTS.items():
+        pins = [p for p in ep.PINS if p.fn == fn]
+        assert pins, fn
+        for name, knobs in mutants.items():
+            caught = [p.name for p in pins if ep.model_eval(p, **knobs) != p.expected]
+            assert caught, f"{fn}: mutant {name} passes every pin"
+
+
 # ------------------------------------------------------------ attention ----
 
 def _attn64(q, k, v, H, HKV, hd):
