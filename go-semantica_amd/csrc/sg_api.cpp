@@ -322,6 +322,7 @@ struct Profiler {
 struct Lane {
   DevBuf h, xn, qkv, att, o, g, a8, sx, amax, meta_d, err;
   DevBuf ks, vt;  // attention operands, hi/lo fp16 (K row-major; V^T); Q is split inside the attention kernel
+  DevBuf xp;      // exact-order attention: scores / weights [H][T][ldp] (SG_ATTN_EXACT only)
   HostBuf meta_h, io_h;
   hipStream_t stream = nullptr;
   hipEvent_t done = nullptr;
@@ -337,7 +338,7 @@ struct Lane {
     return SG_OK;
   }
   ~Lane() {
-    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a8, &sx, &amax, &meta_d, &err, &ks, &vt}) b->release();
+    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a8, &sx, &amax, &meta_d, &err, &ks, &vt, &xp}) b->release();
     meta_h.release();
     io_h.release();
     if (done) (void)hipEventDestroy(done);
@@ -372,6 +373,7 @@ struct sg_model {
   Lane lanes[kLanes];
   hipEvent_t fork = nullptr;  // the caller's stream position the groups start from
   DevBuf tokens, out;         // sg_forward's staging of host tokens and embeddings
+  int attn_mode = SG_ATTN_FAST;  // sg_model_set_attention_mode
   std::mutex mu;
 
   template <typename T>
@@ -516,17 +518,31 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.attn_norm, site(l, 0)));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), gemm(ly.wqkv, ly.sqkv, qkv, nqkv, d));
     if (tr && tr->qkv) SG_HIP(tap(tr->qkv, qkv, l, nqkv));
-    // K's QK-norm + RoPE + split and V's V^T split in one launch; Q's norm and
-    // RoPE run inside the attention kernel.
-    SG_LAUNCH(SG_K_NORM, t * kvd * 16.0,
-              sgk::kv_prep(qkv + qd, qkv + qd + kvd, nqkv, ly.k_norm, c.num_kv_heads, T, meta.row_pos, m->cos_t,
-                           m->sin_t, eps, ks_h, ks_l, kvd, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles, vt_h,
-                           ldvt, s));
-    const sg_attn_qpre qpre{qkv, nqkv, ly.q_norm, m->cos_t, m->sin_t, eps};
-    SG_LAUNCH(SG_K_ATTENTION, attn_flops,
-              sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, ldvt, att, qd, meta.seq_off,
-                             meta.voff, meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale,
-                             site(l, 1), meta.max_len, s, &qpre));
+    if (m->attn_mode == SG_ATTN_EXACT) {
+      // The reference's float32 order throughout: QK-norm + RoPE in place on
+      // the QKV output, then the VALU attention, then the per-sequence max of
+      // its output for the quantizer.
+      SG_LAUNCH(SG_K_NORM, t * (qd + kvd) * 8.0,
+                sgk::qknorm_rope(qkv, nqkv, qkv + qd, nqkv, ly.q_norm, ly.k_norm, c.num_heads, c.num_kv_heads, T,
+                                 meta.row_pos, m->cos_t, m->sin_t, eps, nullptr, nullptr, 0, nullptr, nullptr, 0, s));
+      SG_LAUNCH(SG_K_ATTENTION, attn_flops,
+                sgk::attention_exact(qkv, nqkv, qkv + qd, qkv + qd + kvd, nqkv, att, qd, meta.seq_off, meta.row_seq,
+                                     ns, T, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale, meta.max_len,
+                                     w.xp.as<float>(), s));
+      SG_LAUNCH(SG_K_OTHER, t * qd * 4.0, sgk::absmax_rows(att, qd, T, qd, meta.row_seq, site(l, 1), s));
+    } else {
+      // K's QK-norm + RoPE + split and V's V^T split in one launch; Q's norm and
+      // RoPE run inside the attention kernel.
+      SG_LAUNCH(SG_K_NORM, t * kvd * 16.0,
+                sgk::kv_prep(qkv + qd, qkv + qd + kvd, nqkv, ly.k_norm, c.num_kv_heads, T, meta.row_pos, m->cos_t,
+                             m->sin_t, eps, ks_h, ks_l, kvd, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles,
+                             vt_h, ldvt, s));
+      const sg_attn_qpre qpre{qkv, nqkv, ly.q_norm, m->cos_t, m->sin_t, eps};
+      SG_LAUNCH(SG_K_ATTENTION, attn_flops,
+                sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, ldvt, att, qd, meta.seq_off,
+                               meta.voff, meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd,
+                               m->attn_scale, site(l, 1), meta.max_len, s, &qpre));
+    }
     if (tr && tr->att) SG_HIP(tap(tr->att, att, l, qd));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), quant(att, qd, site(l, 1)));
     // The O projection and the residual post-norm: one launch for large
@@ -614,7 +630,8 @@ int token_error(Lane& w, const int32_t* d_tokens, hipStream_t s) {
   return fail(SG_ERR_TOKEN, "token ID out of range: %d", h[1]);
 }
 
-int ensure_workspace(const sg_model* m, Lane& w, int T, int n_seq, int Tp) {
+int ensure_workspace(const sg_model* m, Lane& w, const Meta& meta) {
+  const int T = meta.T, n_seq = meta.n_seq, Tp = meta.Tp;
   const sg_model_config& c = m->cfg;
   const size_t t = (size_t)T;
   const int amax_cols = c.embed_dim > c.interm_dim ? c.embed_dim : c.interm_dim;
@@ -631,6 +648,7 @@ int ensure_workspace(const sg_model* m, Lane& w, int T, int n_seq, int Tp) {
   SG_TRY(w.ks.ensure(2 * sizeof(_Float16) * t * m->kvd));
   SG_TRY(w.vt.ensure(2 * sizeof(_Float16) * (size_t)m->kvd * Tp));
   SG_TRY(w.err.ensure(64));
+  if (m->attn_mode == SG_ATTN_EXACT) SG_TRY(w.xp.ensure(sgk::attention_exact_scratch(T, c.num_heads, meta.max_len)));
   return SG_OK;
 }
 
@@ -690,7 +708,7 @@ int forward_device_locked(sg_model* m, const int32_t* d_tokens, const int32_t* o
     for (int i = 0; i <= n; i++) sub[i] = off[b[g] + i] - off[b[g]];
     Lane& w = m->lanes[g];
     SG_TRY(stage_meta(sub.data(), n, GQ, w.meta_h, w.meta_d, st[g], meta[g]));
-    SG_TRY(ensure_workspace(m, w, meta[g].T, n, meta[g].Tp));
+    SG_TRY(ensure_workspace(m, w, meta[g]));
   }
   int rc = SG_OK;
   if (G == 1) {
@@ -1190,6 +1208,41 @@ int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const flo
                         meta.voff, meta.items, meta.n_items, n_heads, n_kv_heads, head_dim, scale, nullptr,
                         meta.max_len, s));
   SG_HIP(hipStreamSynchronize(s));
+  return SG_OK;
+}
+
+int sg_attention_exact(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const float* k, const float* v,
+                       int32_t ldkv, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, const int32_t* off,
+                       int32_t n_seq, void* stream) {
+  if (!ctx || !out || !q || !k || !v) return fail(SG_ERR_INVALID, "NULL argument");
+  if (head_dim != 256 || n_kv_heads <= 0 || n_heads % n_kv_heads)
+    return fail(SG_ERR_INVALID, "unsupported attention shape");
+  if ((ldq & 3) || (ldkv & 3) || (reinterpret_cast<uintptr_t>(q) & 15) || (reinterpret_cast<uintptr_t>(k) & 15))
+    return fail(SG_ERR_INVALID, "q and k rows must be 16-byte aligned (strides multiples of 4)");
+  SG_TRY(check_offsets(off, n_seq, -1));
+  if ((int64_t)n_seq * n_heads > 65535) return fail(SG_ERR_INVALID, "n_seq * n_heads above 65535");
+  std::lock_guard<std::mutex> lk(ctx->mu);
+  SG_TRY(set_device(ctx));
+  hipStream_t s = pick(ctx, stream);
+  Meta meta;
+  SG_TRY(stage_meta(off, n_seq, n_heads / n_kv_heads, ctx->meta_h, ctx->meta_d, s, meta));
+  if (meta.max_len > 2048) return fail(SG_ERR_INVALID, "sequences longer than 2048 keys are not supported");
+  const float scale = 1.0f / (float)std::sqrt((double)head_dim);
+  SG_TRY(ctx->split.ensure(sgk::attention_exact_scratch(meta.T, n_heads, meta.max_len)));
+  SG_TRY(gemm_scratch_begin(ctx, s));  // after the asynchronous GEMM calls of this context
+  SG_HIP(sgk::attention_exact(q, ldq, k, v, ldkv, out, n_heads * head_dim, meta.seq_off, meta.row_seq, n_seq, meta.T,
+                              n_heads, n_kv_heads, head_dim, scale, meta.max_len, ctx->split.as<float>(), s));
+  SG_HIP(hipStreamSynchronize(s));
+  return SG_OK;
+}
+
+int sg_model_set_attention_mode(sg_model* m, int mode) {
+  if (!m) return fail(SG_ERR_INVALID, "NULL argument");
+  if (mode != SG_ATTN_FAST && mode != SG_ATTN_EXACT) return fail(SG_ERR_INVALID, "unknown attention mode %d", mode);
+  if (mode == SG_ATTN_EXACT && m->cfg.max_seq_len > 2048)
+    return fail(SG_ERR_INVALID, "exact attention supports sequences up to 2048 keys (model: %d)", m->cfg.max_seq_len);
+  std::lock_guard<std::mutex> lk(m->mu);
+  m->attn_mode = mode;
   return SG_OK;
 }
 

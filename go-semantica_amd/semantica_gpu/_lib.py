@@ -21,6 +21,8 @@ SG_ERR_INVALID = -5
 SG_ERR_DEVICE = -6
 SG_ERR_NOMEM = -7
 
+SG_ATTN_FAST, SG_ATTN_EXACT = 0, 1
+
 _ERR_NAMES = {
     SG_ERR_EMPTY: "EMPTY",
     SG_ERR_TOO_LONG: "TOO_LONG",
@@ -121,6 +123,8 @@ _PROTOS = {
     "sg_qknorm_rope": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _f32,
                                       _i32, _vp, _i32, _vp]),
     "sg_attention": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _i32, _vp]),
+    "sg_attention_exact": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _vp, _i32, _vp]),
+    "sg_model_set_attention_mode": (ctypes.c_int, [_vp, ctypes.c_int]),
     "sg_gelu_quick_mul": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _vp, _i32, _i32, _i32, _vp]),
     "sg_embed_tokens": (ctypes.c_int, [_vp, _vp, _vp, _i32, _vp]),
     "sg_pool_l2": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i32, _vp, _i32, _vp]),

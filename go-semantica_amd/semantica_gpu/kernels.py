@@ -129,6 +129,14 @@ def attention(ctx, out, q, k, v, n_heads, n_kv_heads, head_dim, offsets, stream=
                                     n_kv_heads, head_dim, offp, len(off) - 1, _stream(stream)))
 
 
+def attention_exact(ctx, out, q, k, v, n_heads, n_kv_heads, head_dim, offsets, stream=None):
+    """attention() in the reference's float32 order (sg_attention_exact): bit-identical to it."""
+    _check_dev(out, q, k, v)
+    off, offp = _off(offsets)
+    _lib.check(ctx.lib.sg_attention_exact(ctx.handle, _vp(out), _vp(q), q.shape[1], _vp(k), _vp(v), k.shape[1],
+                                          n_heads, n_kv_heads, head_dim, offp, len(off) - 1, _stream(stream)))
+
+
 def gelu_quick_mul(ctx, dst, gate, up, stream=None):
     _check_dev(dst, gate, up)
     rows, cols = gate.shape

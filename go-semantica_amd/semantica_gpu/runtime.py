@@ -203,6 +203,12 @@ class Model:
                                              len(offsets) - 1, n_layers, vp(d_qkv_ptr), vp(d_att_ptr), vp(d_h_ptr),
                                              vp(stream)))
 
+    def set_attention_mode(self, mode: int):
+        """sg_model_set_attention_mode: _lib.SG_ATTN_FAST (matrix cores, the
+        default) or _lib.SG_ATTN_EXACT (the reference's float32 order: the
+        forward then gives the block-serial path's bits)."""
+        _lib.check(self.lib.sg_model_set_attention_mode(self.handle, int(mode)))
+
     def profile_enable(self, on: bool = True):
         _lib.check(self.lib.sg_profile_enable(self.handle, 1 if on else 0))
 

@@ -177,6 +177,21 @@ typedef struct sg_profile {
 int sg_profile_enable(sg_model *model, int on);
 int sg_profile_read(sg_model *model, sg_profile *out);
 
+/* Attention arithmetic of the forward.  SG_ATTN_FAST (the default) runs the
+ * score and weight products on fp16 matrix cores as hi/lo splits (within
+ * 1e-5 relative of the reference's float32 attention).  SG_ATTN_EXACT runs
+ * multiHeadAttentionInternal's float32 operations in its order on the vector
+ * ALUs (attention.go:101-363 with dotProductSIMD's eight-lane sums,
+ * activation.go:161-213, axpyAccum): with it the whole forward gives the bits
+ * of forwardINT8WithDim on the block-serial GEMM path
+ * (matmul_inner_loop_fallback.go:16-43, model_int8.go:148-256), several times
+ * slower.  Needs max_seq_len <= 2048.  Takes effect from the next forward.
+ * No counterpart in the reference (which has one attention): the switch is
+ * for callers that need embeddings identical to it, such as parity checks. */
+#define SG_ATTN_FAST 0
+#define SG_ATTN_EXACT 1
+int sg_model_set_attention_mode(sg_model *model, int mode);
+
 /* ---- kernel seam (device pointers, work on `stream`) ---------------------
  * sg_matmul_q8_0_int8 and sg_ffn_gate_up are asynchronous: they return once
  * their work is enqueued on `stream`.  They share the context's operand
@@ -266,6 +281,14 @@ int sg_qknorm_rope(sg_ctx *ctx, float *q, int32_t ldq, float *k, int32_t ldk,
 int sg_attention(sg_ctx *ctx, float *out, const float *q, int32_t ldq, const float *k,
                  const float *v, int32_t ldkv, int32_t n_heads, int32_t n_kv_heads,
                  int32_t head_dim, const int32_t *seq_offsets, int32_t n_seq, void *stream);
+
+/* sg_attention in the reference's float32 order (MultiHeadAttentionChunked,
+ * attention.go:88-363, mask nil; see SG_ATTN_EXACT): bit-identical to it.
+ * Same arguments; any n_heads / n_kv_heads ratio, sequences up to 2048 keys,
+ * q and k 16-byte aligned with strides multiples of 4. */
+int sg_attention_exact(sg_ctx *ctx, float *out, const float *q, int32_t ldq, const float *k,
+                       const float *v, int32_t ldkv, int32_t n_heads, int32_t n_kv_heads,
+                       int32_t head_dim, const int32_t *seq_offsets, int32_t n_seq, void *stream);
 
 /* GELUQuickSIMD then VecMulF32 (activation.go:47-145, matmul.go:238-259):
  * dst[i] = geluquick(gate[i]) * up[i], for `rows` rows of `cols` (strides ldg, ldu, ldd). */

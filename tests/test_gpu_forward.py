@@ -459,6 +459,69 @@ def _teacher_forced(gpu, om, toks, off, dim, n_layers, tag, seam_layers=(), thre
     return att_err
 
 
+def _exact_forward(gpu, om, toks, off, dim, tag, threads=16):
+    """The GPU forward with SG_ATTN_EXACT against the oracle's block-serial
+    forward (matmul_inner_loop_fallback.go:16-43 through model_int8.go:148-256):
+    every embedding bit-identical.  Restores the default mode."""
+    from semantica_gpu import _lib
+    gpu.set_attention_mode(_lib.SG_ATTN_EXACT)
+    try:
+        say(f"{tag}: exact-attention forward, {len(off) - 1} sequences, {int(off[-1])} tokens, dim {dim}")
+        got = gpu.forward_packed(toks, off, dim)
+    finally:
+        gpu.set_attention_mode(_lib.SG_ATTN_FAST)
+    import oracle as o
+    say(f"{tag}: oracle block-serial forward on {threads} threads")
+    rc, ref = om.forward_batch(toks, off, dim, order=o.ORDER_BLOCK_SERIAL, n_threads=threads)
+    assert rc == 0
+    same = np.all(got.view(np.uint32) == ref.view(np.uint32), axis=1)
+    mad, dc = _stats(got, ref)
+    say(f"{tag}: {int(same.sum())}/{len(same)} embeddings bit-identical to the block-serial path "
+        f"(max-abs {mad.max():.1e}); north_star bar: {'met' if mad.max() <= NORTH_STAR_MAX_ABS else 'NOT met'}")
+    assert same.all(), np.nonzero(~same)[0][:10]
+
+
+def test_exact_attention_forward_config0(full_gpu, full_oracle):
+    """Config 0 shape (8 rows of 32 tokens, seed 0), 24 layers, exact attention:
+    bit-identical to the oracle's block-serial forward."""
+    from semantica_gpu import synth
+    toks = synth.token_ids(8 * 32, 262144, seed=0)
+    off = np.arange(0, 8 * 32 + 1, 32, dtype=np.int32)
+    _exact_forward(full_gpu, full_oracle, toks, off, 768, "c0 exact")
+
+
+def test_exact_attention_forward_config4(full_gpu, full_oracle):
+    """Config 4 at full size: 256 log-uniform lengths in [8, 512] (seed 1),
+    Matryoshka dim 256, 24 layers, two sequence groups on two streams, exact
+    attention: every embedding bit-identical to the block-serial path."""
+    from semantica_gpu import synth
+    lens = synth.lengths_log_uniform(256, 8, 512, seed=1)
+    off = synth.offsets_from_lengths(lens)
+    toks = synth.token_ids(int(off[-1]), 262144, seed=1)
+    _exact_forward(full_gpu, full_oracle, toks, off, 256, "c4 exact")
+
+
+def test_exact_attention_forward_config2(full_gpu, full_oracle):
+    """The headline shape, config 2: 64 x 512 tokens (seed 0), 24 layers, the
+    fused GEMM + residual post-norm kernels and two sequence groups, exact
+    attention: all 64 embeddings bit-identical to the block-serial path."""
+    from semantica_gpu import synth
+    toks = synth.token_ids(64 * 512, 262144, seed=0)
+    off = np.arange(0, 64 * 512 + 1, 512, dtype=np.int32)
+    _exact_forward(full_gpu, full_oracle, toks, off, 768, "c2 exact")
+
+
+def test_exact_attention_forward_config3(full_gpu, full_oracle):
+    """Config 3 at full size: 8 sequences of U[1024, 2048] tokens (seed 4),
+    past the fast path's 512-key register kernel, 24 layers, exact attention:
+    every embedding bit-identical to the block-serial path."""
+    from semantica_gpu import synth
+    lens = synth.lengths_uniform(8, 1024, 2048, seed=4)
+    off = synth.offsets_from_lengths(lens)
+    toks = synth.token_ids(int(off[-1]), 262144, seed=4)
+    _exact_forward(full_gpu, full_oracle, toks, off, 768, "c3 exact")
+
+
 def om_layers(om):
     return om.model.layers
 

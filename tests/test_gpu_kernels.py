@@ -442,6 +442,42 @@ def test_attention_vs_oracle(gpu_ctx, oracle, lens):
         assert np.max(np.abs(got[sl] - ref)) < 1e-4 * np.max(np.abs(v[sl])), i
 
 
+@pytest.mark.parametrize("lens,heads", [([1, 3, 7, 64, 65, 300, 513], (3, 1)), ([1100, 2048], (3, 1)),
+                                        ([130, 5, 64], (4, 2))])
+def test_attention_exact_bit_exact(gpu_ctx, oracle, lens, heads):
+    """sg_attention_exact against the oracle's restatement of
+    multiHeadAttentionInternal (attention.go:101-363), bit for bit: lengths
+    across the 64-key score tiles, the 4-key softmax groups and their tails,
+    up to 2048 keys, and a grouped-query shape with two KV heads.  Some query
+    rows are scaled up so that their score ranges pass fastExp's -10 clamp:
+    those weights are exact zeros and their keys are skipped."""
+    import torch
+    from semantica_gpu import kernels
+    H, HKV = heads
+    rng = np.random.default_rng(sum(lens) + H)
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(off[-1])
+    say(f"exact attention lens={lens} heads={H}/{HKV}")
+    q = (rng.standard_normal((T, H * 256)) * rng.uniform(0.5, 1.5, H * 256)).astype(np.float32)
+    q[::5] *= 6.0  # wide score ranges: clamped weights
+    k = (rng.standard_normal((T, HKV * 256)) * rng.uniform(0.5, 1.5, HKV * 256)).astype(np.float32)
+    v = (rng.standard_normal((T, HKV * 256)) * 2).astype(np.float32)
+    out = torch.full((T, H * 256), float("nan"), dtype=torch.float32, device="cuda")
+    kernels.attention_exact(gpu_ctx, out, dev(q), dev(k), dev(v), H, HKV, 256, off)
+    got = host(out)
+    clamped = 0
+    for i in range(len(lens)):
+        sl = slice(off[i], off[i + 1])
+        ref = oracle.attention(q[sl], k[sl], v[sl], H, HKV, 256)
+        assert np.array_equal(got[sl].view(np.uint32), ref.view(np.uint32)), (i, lens[i])
+        if lens[i] > 1:
+            s = (q[sl][:, :256].astype(np.float64) @ k[sl][:, :256].T.astype(np.float64)) / 16
+            clamped += int(np.sum(s - s.max(axis=1, keepdims=True) < -10))
+    say(f"  bit-identical; {clamped} clamped (query, key) pairs in head 0")
+    if max(lens) > 64:
+        assert clamped > 0
+
+
 def test_attention_register_scores_match_recomputed(gpu_ctx):
     """The same sequences with and without a 600-key companion (which moves the
     launch from register-held scores to recomputed ones) give identical bits."""
