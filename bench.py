@@ -300,6 +300,71 @@ def gemm_c1_leg(ctx, m=2048, reps=200):
             "shapes": res}
 
 
+def exact_attention_leg(model, d_tok, off, d_out, steps, B):
+    """The same config-2 forward with SG_ATTN_EXACT (attention in the
+    reference's float32 order on the VALU; the embeddings are then
+    bit-identical to the block-serial path, tests/test_gpu_forward.py::
+    test_exact_attention_forward_config2): timed like the headline, then one
+    instrumented pass for the attention class's time."""
+    import torch
+    from semantica_gpu import _lib
+    model.set_attention_mode(_lib.SG_ATTN_EXACT)
+    try:
+        model.forward_device(d_tok.data_ptr(), off, 768, d_out.data_ptr())
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            model.forward_device(d_tok.data_ptr(), off, 768, d_out.data_ptr())
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / steps
+        model.profile_enable(True)
+        model.forward_device(d_tok.data_ptr(), off, 768, d_out.data_ptr())
+        torch.cuda.synchronize()
+        prof = model.profile_read()
+        model.profile_enable(False)
+    finally:
+        model.set_attention_mode(_lib.SG_ATTN_FAST)
+    a = prof["attention"]
+    return {"mode": "SG_ATTN_EXACT", "steps": steps, "embeddings_per_s": round(B / dt, 2),
+            "ms_per_step": round(dt * 1e3, 3), "attention_ms_per_step": round(a["ms"], 3),
+            "attention_TFLOPS_algorithmic": round(a["work"] / (a["ms"] * 1e-3) / 1e12, 2) if a["ms"] > 0 else None,
+            "parity": "embeddings bit-identical to the oracle's block-serial forward at this config"}
+
+
+def hbm_reference_leg(ctx, T, d=768, reps=20):
+    """What plain streaming kernels reach on this GPU, the yardstick for the
+    bandwidth-bound row kernels, on [T, d] fp32 tensors: the library's
+    sg_hbm_probe kernels (one float4 per lane: c = a + b, 12 B per element,
+    the residual add's I/O; and the int8 codes of a, 5 B per element, the
+    quantizers' I/O; HIP events on the launch stream inside the library), and
+    torch's add and fp32 -> int8 conversion (events on torch's stream)."""
+    import torch
+    from semantica_gpu import kernels
+    a = torch.randn((T, d), device="cuda")
+    b = torch.randn((T, d), device="cuda")
+    c = torch.empty_like(a)
+    q = torch.empty((T, d), dtype=torch.int8, device="cuda")
+    torch.cuda.synchronize()
+    res = {}
+    for name, kind, out, nbytes in (("probe_add", 0, c, 12 * T * d), ("probe_quant", 1, q, 5 * T * d)):
+        us = kernels.hbm_probe_us(ctx, kind, a, b, out, reps)
+        res[name] = {"us": round(us, 2), "bytes": nbytes, "GB_s": round(nbytes / us / 1e3, 1)}
+    for name, fn, nbytes in (("torch_add", lambda: torch.add(a, b, out=c), 12 * T * d),
+                             ("torch_to_int8", lambda: q.copy_(a), 5 * T * d)):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        res[name] = {"us": round(us, 2), "bytes": nbytes, "GB_s": round(nbytes / us / 1e3, 1)}
+    del a, b, c, q
+    return {"workload": f"[{T}, {d}] fp32 tensors, {reps} launches each", **res}
+
+
 def tokenizer_leg(n_texts=64, chars=2000):
     """The host tokenizer (sg_tokenizer_*, internal/tokenizer) on a synthetic
     262,144-token vocabulary (the real one is not available offline): texts of
@@ -480,6 +545,8 @@ def main():
         "gemm_frac_of_step": round(all_ms / (dt_prof * 1e3), 3),
     }
     if not a.no_extras:
+        line["exact_attention"] = exact_attention_leg(model, d_tok, off, d_out, max(2, a.steps // 4), B)
+        line["hbm_reference"] = hbm_reference_leg(ctx, B * S)
         line["latency"] = small_batch_latency(model)
         line["gemm_c1"] = gemm_c1_leg(ctx)
     model.close()

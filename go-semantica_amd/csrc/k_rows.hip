@@ -552,6 +552,27 @@ __global__ __launch_bounds__(kThreads) void k_l2_rows(float* __restrict__ out, i
     for (int c = threadIdx.x; c < out_dim; c += kThreads) v[c] = row[c] / n;
 }
 
+// Streaming yardsticks for the bandwidth-bound kernels (sg_hbm_probe): one
+// float4 per lane, no reuse.  c = a + b (8 B read, 4 B written per element),
+// and the quantizers' I/O: 4 B read, one int8 code written, q = the code of
+// x at reciprocal scale inv (sg_quant_code, exact rounding included).
+__global__ __launch_bounds__(256) void k_stream_add(const f32x4_t* __restrict__ a, const f32x4_t* __restrict__ b,
+                                                    f32x4_t* __restrict__ c, int64_t n4) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n4) c[i] = a[i] + b[i];
+}
+
+__global__ __launch_bounds__(256) void k_stream_quant(const f32x4_t* __restrict__ a, float inv,
+                                                      int8_t* __restrict__ q, int64_t n4) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n4) return;
+  const f32x4_t v = __builtin_nontemporal_load(&a[i]);
+  float cv[4];
+#pragma unroll
+  for (int t = 0; t < 4; t++) cv[t] = sg_quant_code(v[t], inv);
+  store_codes4(q + 4 * i, cv);
+}
+
 inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
 
 }  // namespace
@@ -723,6 +744,21 @@ hipError_t pool_l2(float* out, const float* x, int ldx, int out_dim, const int32
   hipLaunchKernelGGL(k_pool_mean, dim3(n_seq, blocks_for(out_dim, kPoolCols)), dim3(kThreads), 0, s, out, x, ldx,
                      out_dim, seq_off);
   hipLaunchKernelGGL(k_l2_rows, dim3(n_seq), dim3(kThreads), 0, s, out, out_dim);
+  return hipGetLastError();
+}
+
+hipError_t stream_probe(int kind, const float* a, const float* b, void* c, int64_t n, hipStream_t s) {
+  if (n <= 0 || n % 4) return hipErrorInvalidValue;
+  const int64_t n4 = n / 4;
+  if (kind == 0)
+    hipLaunchKernelGGL(k_stream_add, dim3(blocks_for(n4, 256)), dim3(256), 0, s,
+                       reinterpret_cast<const f32x4_t*>(a), reinterpret_cast<const f32x4_t*>(b),
+                       reinterpret_cast<f32x4_t*>(c), n4);
+  else if (kind == 1)
+    hipLaunchKernelGGL(k_stream_quant, dim3(blocks_for(n4, 256)), dim3(256), 0, s,
+                       reinterpret_cast<const f32x4_t*>(a), 12.7f, static_cast<int8_t*>(c), n4);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

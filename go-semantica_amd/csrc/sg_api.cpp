@@ -1092,6 +1092,35 @@ int sg_matmul_q8_0_int8_bench(sg_ctx* ctx, float* dst, const sg_q8_weight* w, co
   return use.finish();
 }
 
+int sg_hbm_probe(sg_ctx* ctx, int32_t kind, const float* a, const float* b, void* c, int64_t n, int32_t reps,
+                 void* stream, float* us_per_launch) {
+  if (!ctx || !a || !c || !us_per_launch || (kind == 0 && !b)) return fail(SG_ERR_INVALID, "NULL argument");
+  if (kind < 0 || kind > 1) return fail(SG_ERR_INVALID, "unknown probe kind %d", kind);
+  if (n <= 0 || n % 4 || reps <= 0) return fail(SG_ERR_INVALID, "n must be a positive multiple of 4, reps positive");
+  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(c)) & 15)
+    return fail(SG_ERR_INVALID, "buffers must be 16-byte aligned");
+  SG_TRY(set_device(ctx));
+  hipStream_t s = pick(ctx, stream);
+  SG_HIP(sgk::stream_probe(kind, a, b, c, n, s));  // warm
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+    if (e0) (void)hipEventDestroy(e0);
+    return fail(SG_ERR_DEVICE, "hipEventCreate failed");
+  }
+  hipError_t e = hipEventRecord(e0, s);
+  for (int i = 0; i < reps && e == hipSuccess; i++) e = sgk::stream_probe(kind, a, b, c, n, s);
+  if (e == hipSuccess) e = hipEventRecord(e1, s);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (e != hipSuccess) (void)hipStreamSynchronize(s);
+  SG_HIP(e);
+  *us_per_launch = ms * 1000.0f / (float)reps;
+  return SG_OK;
+}
+
 int sg_q8_block_sums(sg_ctx* ctx, int32_t* out, const sg_q8_weight* w, const int8_t* x, int32_t batch, void* stream) {
   return matmul_common(ctx, nullptr, out, w, x, nullptr, batch, stream);
 }

@@ -88,6 +88,9 @@ hipError_t pool_l2(float* out, const float* x, int ldx, int out_dim, const int32
                    hipStream_t s);
 hipError_t embed_only(const int32_t* tokens, int T, const int8_t* eq, const float* es, int vocab, int d,
                       float sqrt_d, float* h, int32_t* err, hipStream_t s);
+// Streaming yardsticks over n floats (n % 4 == 0, 16-byte aligned): kind 0
+// c = a + b (fp32), kind 1 c = int8 codes of a (b unused).
+hipError_t stream_probe(int kind, const float* a, const float* b, void* c, int64_t n, hipStream_t s);
 
 // ---- GEMM (k_gemm.hip) ----
 // Y[M][N] = (sum_b float(P_b) * St[b][n]) * row_scale[m] with A int8 [M][K]

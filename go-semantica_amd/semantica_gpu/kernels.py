@@ -137,6 +137,16 @@ def attention_exact(ctx, out, q, k, v, n_heads, n_kv_heads, head_dim, offsets, s
                                           n_heads, n_kv_heads, head_dim, offp, len(off) - 1, _stream(stream)))
 
 
+def hbm_probe_us(ctx, kind: int, a, b, c, reps: int, stream=None) -> float:
+    """sg_hbm_probe: average microseconds per launch of the streaming yardstick
+    (kind 0: c = a + b fp32; kind 1: c = int8 codes of a)."""
+    _check_dev(a, c)
+    us = ctypes.c_float()
+    _lib.check(ctx.lib.sg_hbm_probe(ctx.handle, kind, _vp(a), _vp(b) if b is not None else None, _vp(c),
+                                    a.numel(), reps, _stream(stream), ctypes.byref(us)))
+    return us.value
+
+
 def gelu_quick_mul(ctx, dst, gate, up, stream=None):
     _check_dev(dst, gate, up)
     rows, cols = gate.shape

@@ -237,6 +237,16 @@ int sg_matmul_q8_0_int8(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const in
 int sg_matmul_q8_0_int8_noalloc(sg_ctx *ctx, float *dst, const sg_q8_weight *w, const int8_t *x,
                                 const float *row_scale, int32_t batch, void *stream);
 
+/* Measurement hook (no counterpart in the reference): the HBM yardstick the
+ * bandwidth-bound kernels are set against.  kind 0: c = a + b over n fp32
+ * (8 B read, 4 B written per element); kind 1: c = int8 codes of a at a fixed
+ * scale (4 B read, 1 B written: the quantizers' I/O; b unused).  One float4
+ * per lane, launched `reps` times back to back on `stream` between two HIP
+ * events; returns the average time per launch.  n a multiple of 4, device
+ * buffers 16-byte aligned.  Synchronizes the stream. */
+int sg_hbm_probe(sg_ctx *ctx, int32_t kind, const float *a, const float *b, void *c, int64_t n,
+                 int32_t reps, void *stream, float *us_per_launch);
+
 /* Measurement hook for the GEMM kernel alone (no counterpart in the
  * reference): relays x into the operand layout once, then launches the same
  * GEMM kernel sg_matmul_q8_0_int8 uses `reps` times back to back on `stream`
