@@ -520,16 +520,15 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
     if (tr && tr->qkv) SG_HIP(tap(tr->qkv, qkv, l, nqkv));
     if (m->attn_mode == SG_ATTN_EXACT) {
       // The reference's float32 order throughout: QK-norm + RoPE in place on
-      // the QKV output, then the VALU attention, then the per-sequence max of
-      // its output for the quantizer.
+      // the QKV output, then the VALU attention (which folds the sequences'
+      // max|o| into amax for the quantizer).
       SG_LAUNCH(SG_K_NORM, t * (qd + kvd) * 8.0,
                 sgk::qknorm_rope(qkv, nqkv, qkv + qd, nqkv, ly.q_norm, ly.k_norm, c.num_heads, c.num_kv_heads, T,
                                  meta.row_pos, m->cos_t, m->sin_t, eps, nullptr, nullptr, 0, nullptr, nullptr, 0, s));
       SG_LAUNCH(SG_K_ATTENTION, attn_flops,
                 sgk::attention_exact(qkv, nqkv, qkv + qd, qkv + qd + kvd, nqkv, att, qd, meta.seq_off, meta.row_seq,
                                      ns, T, c.num_heads, c.num_kv_heads, m->hd, m->attn_scale, meta.max_len,
-                                     w.xp.as<float>(), s));
-      SG_LAUNCH(SG_K_OTHER, t * qd * 4.0, sgk::absmax_rows(att, qd, T, qd, meta.row_seq, site(l, 1), s));
+                                     w.xp.as<float>(), site(l, 1), s));
     } else {
       // K's QK-norm + RoPE + split and V's V^T split in one launch; Q's norm and
       // RoPE run inside the attention kernel.
@@ -1260,7 +1259,8 @@ int sg_attention_exact(sg_ctx* ctx, float* out, const float* q, int32_t ldq, con
   SG_TRY(ctx->split.ensure(sgk::attention_exact_scratch(meta.T, n_heads, meta.max_len)));
   SG_TRY(gemm_scratch_begin(ctx, s));  // after the asynchronous GEMM calls of this context
   SG_HIP(sgk::attention_exact(q, ldq, k, v, ldkv, out, n_heads * head_dim, meta.seq_off, meta.row_seq, n_seq, meta.T,
-                              n_heads, n_kv_heads, head_dim, scale, meta.max_len, ctx->split.as<float>(), s));
+                              n_heads, n_kv_heads, head_dim, scale, meta.max_len, ctx->split.as<float>(), nullptr,
+                              s));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;
 }

@@ -154,12 +154,13 @@ hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Flo
 
 // ---- attention in the reference's float32 order (k_attn_exact.hip) ----
 // out[T][ldo] (head h at h*hd) from q[T][ldq], k/v[T][ldkv] (kv head h / (H/HKV)),
-// every operation in attention.go's order; P: attention_exact_scratch bytes.
+// every operation in attention.go's order; P: attention_exact_scratch bytes;
+// amax (optional) collects each sequence's max|out| (atomic max, >= 0).
 // hd must be 256, max_len <= 2048, q/k rows 16-byte aligned; n_seq * H <= 65535.
 size_t attention_exact_scratch(int T, int H, int max_len);
 hipError_t attention_exact(const float* q, int ldq, const float* k, const float* v, int ldkv, float* out, int ldo,
                            const int32_t* seq_off, const int32_t* row_seq, int n_seq, int T, int H, int HKV, int hd,
-                           float scale, int max_len, float* P, hipStream_t s);
+                           float scale, int max_len, float* P, float* amax, hipStream_t s);
 
 // ---- brute-force search (k_search.hip) ----
 // Storage modes, the values of brute.QuantizationMode (search/brute/quant.go:8-15).

@@ -442,15 +442,19 @@ def test_attention_vs_oracle(gpu_ctx, oracle, lens):
         assert np.max(np.abs(got[sl] - ref)) < 1e-4 * np.max(np.abs(v[sl])), i
 
 
-@pytest.mark.parametrize("lens,heads", [([1, 3, 7, 64, 65, 300, 513], (3, 1)), ([1100, 2048], (3, 1)),
-                                        ([130, 5, 64], (4, 2))])
-def test_attention_exact_bit_exact(gpu_ctx, oracle, lens, heads):
+@pytest.mark.parametrize("lens,heads,nonfinite", [([1, 3, 7, 64, 65, 300, 513], (3, 1), False),
+                                                  ([1100, 2048], (3, 1), False),
+                                                  ([130, 5, 64], (4, 2), False),
+                                                  ([90, 200], (3, 1), True)])
+def test_attention_exact_bit_exact(gpu_ctx, oracle, lens, heads, nonfinite):
     """sg_attention_exact against the oracle's restatement of
     multiHeadAttentionInternal (attention.go:101-363), bit for bit: lengths
     across the 64-key score tiles, the 4-key softmax groups and their tails,
     up to 2048 keys, and a grouped-query shape with two KV heads.  Some query
     rows are scaled up so that their score ranges pass fastExp's -10 clamp:
-    those weights are exact zeros and their keys are skipped."""
+    those weights are exact zeros and their keys are skipped.  In the last
+    case some values are infinite or NaN, where skipping a zero-weight key
+    (rather than adding 0 * v) decides the result (any NaN matches any NaN)."""
     import torch
     from semantica_gpu import kernels
     H, HKV = heads
@@ -462,6 +466,8 @@ def test_attention_exact_bit_exact(gpu_ctx, oracle, lens, heads):
     q[::5] *= 6.0  # wide score ranges: clamped weights
     k = (rng.standard_normal((T, HKV * 256)) * rng.uniform(0.5, 1.5, HKV * 256)).astype(np.float32)
     v = (rng.standard_normal((T, HKV * 256)) * 2).astype(np.float32)
+    if nonfinite:
+        v[7, 3], v[50, 100], v[150, 9] = np.inf, -np.inf, np.nan
     out = torch.full((T, H * 256), float("nan"), dtype=torch.float32, device="cuda")
     kernels.attention_exact(gpu_ctx, out, dev(q), dev(k), dev(v), H, HKV, 256, off)
     got = host(out)
@@ -469,7 +475,10 @@ def test_attention_exact_bit_exact(gpu_ctx, oracle, lens, heads):
     for i in range(len(lens)):
         sl = slice(off[i], off[i + 1])
         ref = oracle.attention(q[sl], k[sl], v[sl], H, HKV, 256)
-        assert np.array_equal(got[sl].view(np.uint32), ref.view(np.uint32)), (i, lens[i])
+        same = (got[sl].view(np.uint32) == ref.view(np.uint32)) | (np.isnan(got[sl]) & np.isnan(ref))
+        assert same.all(), (i, lens[i])
+        if nonfinite:  # finite and non-finite outputs both occur
+            assert np.isfinite(ref).any() and not np.isfinite(ref).all()
         if lens[i] > 1:
             s = (q[sl][:, :256].astype(np.float64) @ k[sl][:, :256].T.astype(np.float64)) / 16
             clamped += int(np.sum(s - s.max(axis=1, keepdims=True) < -10))
