@@ -163,7 +163,9 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
 // GELU (WN = 1, TN even): W holds gate and up rows interleaved in groups of
 // 32 (kGeluGroup), subtile pairs (2p, 2p+1) of a wave are gate and up of the
 // same features, and gemm_epilogue writes g [M][N/2] with the sequences'
-// max|g| in amax.
+// max|g| in amax.  PIPE (PF >= 3) issues each block's MFMAs one step ahead of
+// its FMA chain, for grids too small to cover a wave's MFMA latency with
+// other waves.
 template <int TM, int TN>
 struct Stage {
   i32x4_t a[TM], w[TN];
@@ -183,15 +185,18 @@ __device__ __forceinline__ void fetch(Stage<TM, TN>& st, const int8_t* const (&a
   }
 }
 
-template <int TM, int TN, bool SUMS>
-__device__ __forceinline__ void compute(const Stage<TM, TN>& st, f32x16_t (&acc)[TM][TN], int32_t* sums, int M,
-                                        int N, int nb, int b, int m_base, int n_base, int lr, int lh,
-                                        const i32x16_t& bias) {
-  i32x16_t p[TM][TN];
+template <int TM, int TN>
+__device__ __forceinline__ void block_mfma(const Stage<TM, TN>& st, i32x16_t (&p)[TM][TN], const i32x16_t& bias) {
 #pragma unroll
   for (int tm = 0; tm < TM; tm++)
 #pragma unroll
     for (int tn = 0; tn < TN; tn++) p[tm][tn] = __builtin_amdgcn_mfma_i32_32x32x32_i8(st.a[tm], st.w[tn], bias, 0, 0, 0);
+}
+
+template <int TM, int TN, bool SUMS>
+__device__ __forceinline__ void block_fma(const i32x16_t (&p)[TM][TN], const float (&d)[TN], f32x16_t (&acc)[TM][TN],
+                                          int32_t* sums, int M, int N, int nb, int b, int m_base, int n_base, int lr,
+                                          int lh) {
 #pragma unroll
   for (int tm = 0; tm < TM; tm++)
 #pragma unroll
@@ -206,11 +211,20 @@ __device__ __forceinline__ void compute(const Stage<TM, TN>& st, f32x16_t (&acc)
       }
 #pragma unroll
       for (int r = 0; r < 16; r++)
-        acc[tm][tn][r] = __builtin_fmaf(__int_as_float(p[tm][tn][r]) - kMagic, st.d[tn], acc[tm][tn][r]);
+        acc[tm][tn][r] = __builtin_fmaf(__int_as_float(p[tm][tn][r]) - kMagic, d[tn], acc[tm][tn][r]);
     }
 }
 
-template <int WM, int WN, int TM, int TN, bool SUMS, bool GELU, int PF>
+template <int TM, int TN, bool SUMS>
+__device__ __forceinline__ void compute(const Stage<TM, TN>& st, f32x16_t (&acc)[TM][TN], int32_t* sums, int M,
+                                        int N, int nb, int b, int m_base, int n_base, int lr, int lh,
+                                        const i32x16_t& bias) {
+  i32x16_t p[TM][TN];
+  block_mfma<TM, TN>(st, p, bias);
+  block_fma<TM, TN, SUMS>(p, st.d, acc, sums, M, N, nb, b, m_base, n_base, lr, lh);
+}
+
+template <int WM, int WN, int TM, int TN, bool SUMS, bool GELU, int PF, bool PIPE>
 __global__ __launch_bounds__(WM* WN* SG_WAVE, 2) void k_gemm_q8_rd(
     const int8_t* __restrict__ A, int a_rows, const int8_t* __restrict__ W, const float* __restrict__ St,
     const float* __restrict__ row_scale, float* __restrict__ Y, int32_t* __restrict__ sums, int M, int N, int K,
@@ -260,23 +274,58 @@ __global__ __launch_bounds__(WM* WN* SG_WAVE, 2) void k_gemm_q8_rd(
     fetch<TM, TN>(st[I], ap, wp, sp, min(I, nb - 1), a_bstride, w_bstride, N);
   });
   int b = 0;
-  for (; b + PF <= nb; b += PF)
-    static_for<0, PF>([&](auto ic) {
+  if constexpr (PIPE) {
+    // MFMA one block ahead: step b issues block b+1's MFMAs (its stage was
+    // fetched PF - 2 >= 1 steps earlier) before block b's FMA chain, so a
+    // wave's FMAs wait on no MFMA latency.  Past the last block the MFMAs
+    // run on re-loaded or stale stages and their results are never used.
+    static_assert(PF >= 3 && !SUMS, "the pipelined loop keeps a fetched stage between fetch and MFMA");
+    i32x16_t p[TM][TN];
+    block_mfma<TM, TN>(st[0], p, bias);
+    for (; b + PF <= nb; b += PF)
+      static_for<0, PF>([&](auto ic) {
+        constexpr int I = decltype(ic)::value;
+        fetch<TM, TN>(st[(I + PF - 1) % PF], ap, wp, sp, min(b + I + PF - 1, nb - 1), a_bstride, w_bstride, N);
+        __builtin_amdgcn_sched_barrier(0);
+        i32x16_t pn[TM][TN];
+        block_mfma<TM, TN>(st[(I + 1) % PF], pn, bias);
+        __builtin_amdgcn_sched_barrier(0);
+        block_fma<TM, TN, false>(p, st[I].d, acc, nullptr, M, N, nb, b + I, m_base, n_base, lr, lh);
+        static_for<0, TM>([&](auto mc) {
+          static_for<0, TN>([&](auto nc) { p[decltype(mc)::value][decltype(nc)::value] = pn[decltype(mc)::value][decltype(nc)::value]; });
+        });
+      });
+    static_for<0, PF - 1>([&](auto ic) {  // the last nb % PF blocks, already in stages 0 ..
       constexpr int I = decltype(ic)::value;
-      fetch<TM, TN>(st[(I + PF - 1) % PF], ap, wp, sp, min(b + I + PF - 1, nb - 1), a_bstride, w_bstride, N);
-      __builtin_amdgcn_sched_barrier(0);
-      compute<TM, TN, SUMS>(st[I], acc, sums, M, N, nb, b + I, m_base, n_base, lr, lh, bias);
+      if (b + I < nb) {
+        i32x16_t pn[TM][TN];
+        block_mfma<TM, TN>(st[(I + 1) % PF], pn, bias);
+        __builtin_amdgcn_sched_barrier(0);
+        block_fma<TM, TN, false>(p, st[I].d, acc, nullptr, M, N, nb, b + I, m_base, n_base, lr, lh);
+        static_for<0, TM>([&](auto mc) {
+          static_for<0, TN>([&](auto nc) { p[decltype(mc)::value][decltype(nc)::value] = pn[decltype(mc)::value][decltype(nc)::value]; });
+        });
+      }
     });
-  static_for<0, PF - 1>([&](auto ic) {  // the last nb % PF blocks, already in stages 0 ..
-    constexpr int I = decltype(ic)::value;
-    if (b + I < nb) compute<TM, TN, SUMS>(st[I], acc, sums, M, N, nb, b + I, m_base, n_base, lr, lh, bias);
-  });
+  } else {
+    for (; b + PF <= nb; b += PF)
+      static_for<0, PF>([&](auto ic) {
+        constexpr int I = decltype(ic)::value;
+        fetch<TM, TN>(st[(I + PF - 1) % PF], ap, wp, sp, min(b + I + PF - 1, nb - 1), a_bstride, w_bstride, N);
+        __builtin_amdgcn_sched_barrier(0);
+        compute<TM, TN, SUMS>(st[I], acc, sums, M, N, nb, b + I, m_base, n_base, lr, lh, bias);
+      });
+    static_for<0, PF - 1>([&](auto ic) {  // the last nb % PF blocks, already in stages 0 ..
+      constexpr int I = decltype(ic)::value;
+      if (b + I < nb) compute<TM, TN, SUMS>(st[I], acc, sums, M, N, nb, b + I, m_base, n_base, lr, lh, bias);
+    });
+  }
 
   gemm_epilogue<WM, TM, TN, GELU>(acc, m_base, by, n_base, lr, lh, lane, wave, threadIdx.x, M, N, row_scale, Y,
                                   row_seq, amax);
 }
 
-template <int WM, int WN, int TM, int TN, bool SUMS, bool GELU = false, int PF = 2>
+template <int WM, int WN, int TM, int TN, bool SUMS, bool GELU = false, int PF = 2, bool PIPE = false>
 hipError_t launch_rd(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* rs, float* Y,
                      int32_t* sums, int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr,
                      float* amax = nullptr) {
@@ -284,7 +333,7 @@ hipError_t launch_rd(const int8_t* A, int a_rows, const int8_t* W, const float* 
   const int gm = (M + BM - 1) / BM;
   if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;  // A must cover the padded rows
   dim3 grid((N + BN - 1) / BN, gm);
-  hipLaunchKernelGGL((k_gemm_q8_rd<WM, WN, TM, TN, SUMS, GELU, PF>), grid, dim3(WM * WN * SG_WAVE), 0, s, A, a_rows, W,
+  hipLaunchKernelGGL((k_gemm_q8_rd<WM, WN, TM, TN, SUMS, GELU, PF, PIPE>), grid, dim3(WM * WN * SG_WAVE), 0, s, A, a_rows, W,
                      St, rs, Y, sums, M, N, K, row_seq, amax);
   return hipGetLastError();
 }
@@ -622,13 +671,25 @@ constexpr int kRdRows = 6144, kLds8Rows = 12288, kGeluLdsRows = 4096;
 // gemm_q8_res_norm: the fused kernel from kResRows rows (below, gemm_q8 and
 // post_res_norm run as two launches).
 constexpr int kResRows = 8192;
+// Register-direct launches of at most kPipeTiles workgroups -- fewer than
+// two waves per SIMD, so the other waves cannot fill a wave's MFMA latency --
+// take the MFMA-ahead loop with a 3-stage ring (at M = 32: 4.8 vs 5.4 us for
+// K = 768; at M = 2048, N = 256: 5.5 vs 6.0 us); larger grids keep the plain
+// 2-stage loop, whose lower register count gives more waves per SIMD (QKV at
+// M = 2048: 10.3 vs 10.8 us).
+constexpr int kPipeTiles = 384;
+inline int rd_tiles(int M, int N, int BM, int BN) { return ((M + BM - 1) / BM) * ((N + BN - 1) / BN); }
 
 hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
                    int32_t* sums, int M, int N, int K, hipStream_t s) {
   if (M <= 0 || N <= 0) return hipSuccess;
   if (K <= 0 || K % 32) return hipErrorInvalidValue;
   if (sums) return launch_rd<1, 1, 1, 1, true>(A, a_rows, W, St, row_scale, Y, sums, M, N, K, s);
-  if (M < kRdRows) return launch_rd<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
+  if (M < kRdRows) {
+    if (rd_tiles(M, N, 64, 64) <= kPipeTiles)
+      return launch_rd<2, 2, 1, 1, false, false, 3, true>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
+    return launch_rd<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
+  }
   if (M < kLds8Rows) return launch_lds<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   return launch_lds<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
 }
@@ -638,6 +699,9 @@ hipError_t gemm_q8_gelu(const int8_t* A, int a_rows, const int8_t* W, const floa
   if (M <= 0 || Nh <= 0) return hipSuccess;
   if (K <= 0 || K % 32 || Nh % 32) return hipErrorInvalidValue;
   if (amax && !row_seq) return hipErrorInvalidValue;
+  if (M < kGeluLdsRows && rd_tiles(M, 2 * Nh, 128, 64) <= kPipeTiles)
+    return launch_rd<4, 1, 1, 2, false, true, 3, true>(A, a_rows, W, St, row_scale, G, nullptr, M, 2 * Nh, K, s,
+                                                       row_seq, amax);
   if (M < kGeluLdsRows)
     return launch_rd<4, 1, 1, 2, false, true>(A, a_rows, W, St, row_scale, G, nullptr, M, 2 * Nh, K, s, row_seq,
                                               amax);
