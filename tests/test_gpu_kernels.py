@@ -196,6 +196,56 @@ def test_gemm_order_pins(gpu_ctx, M):
         assert got[r, r % n] == float(p.expected["block_serial"]), (M, r, p.name, got[r, r % n])
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 768, 768), (2049, 768, 768), (6143, 256, 800), (33, 768, 1152)])
+def test_gemm_mfma_ahead_threshold(gpu_ctx, oracle, M, N, K):
+    """Register-direct launches of at most 384 workgroups run the MFMA-ahead
+    loop (3-stage ring), larger ones the plain 2-stage loop: 2048 x 768 is
+    exactly 384 64x64 tiles, 2049 rows 396; 6143 x 256 is 384 tiles with
+    K = 800 (25 blocks: a partial last ring round); 33 x 768 x 1152 one row
+    of tiles with 36 blocks.  The first and last 64 rows and every 37th row
+    bit-exact to the block-serial order."""
+    import torch
+    from semantica_gpu import kernels, synth
+    rng = np.random.default_rng(M + N + K)
+    say(f"gemm MFMA-ahead threshold M={M} N={N} K={K}")
+    raw = synth.q8_0_random(rng, N, K)
+    xq = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    rs = rng.uniform(1e-3, 2.0, size=M).astype(np.float32)
+    w = kernels.Q8Weight(gpu_ctx, raw, N, K)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    kernels.matmul_q8_0(gpu_ctx, y, w, dev(xq), dev(rs))
+    got = host(y)
+    w.close()
+    rows = np.unique(np.concatenate([np.arange(min(64, M)), np.arange(max(0, M - 64), M), np.arange(0, M, 37)]))
+    ref = oracle.matmul(raw, xq[rows], rs[rows], N, oracle.ORDER_BLOCK_SERIAL)
+    assert np.array_equal(got[rows].view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("M", [1280, 1408])
+def test_ffn_gate_up_mfma_ahead_threshold(gpu_ctx, oracle, M):
+    """The fused gate/up GEMM on both sides of the 384-workgroup MFMA-ahead
+    threshold (128 x 64 tiles over 2 x 1152 columns: 1280 rows are 360
+    workgroups, 1408 rows 396): bit-identical to the unfused GEMMs + GELU."""
+    import torch
+    from semantica_gpu import kernels, synth
+    N, K = 1152, 768
+    rng = np.random.default_rng(M)
+    say(f"ffn gate/up MFMA-ahead threshold M={M}")
+    wg = kernels.Q8Weight(gpu_ctx, synth.q8_0_random(rng, N, K), N, K)
+    wu = kernels.Q8Weight(gpu_ctx, synth.q8_0_random(rng, N, K), N, K)
+    xq = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    rs = rng.uniform(1e-3, 2e-2, M).astype(np.float32)
+    gate = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    up, ref, got = torch.empty_like(gate), torch.empty_like(gate), torch.empty_like(gate)
+    kernels.matmul_q8_0(gpu_ctx, gate, wg, dev(xq), dev(rs))
+    kernels.matmul_q8_0(gpu_ctx, up, wu, dev(xq), dev(rs))
+    kernels.gelu_quick_mul(gpu_ctx, ref, gate, up)
+    kernels.ffn_gate_up(gpu_ctx, got, wg, wu, dev(xq), dev(rs))
+    wg.close()
+    wu.close()
+    assert np.array_equal(host(got).view(np.uint32), host(ref).view(np.uint32))
+
+
 def test_gemm_ragged_m_and_extremes(gpu_ctx, oracle):
     """M not a multiple of any tile; blocks at +-127 extremes; per-row scales."""
     import torch
