@@ -227,7 +227,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
     const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
     const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vt, int ldvt, float* __restrict__ out,
     int ldo, const int32_t* __restrict__ seq_off, const int32_t* __restrict__ voff, const sg_item* __restrict__ items,
-    int G, float sscale, float* __restrict__ amax, sg_attn_qpre qp) {
+    int G, float sscale, float* __restrict__ amax, sg_attn_qpre qp, sg_attn_qout qo) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kRing * kTileBytes];
   __shared__ float red[kWaves];
   typedef __attribute__((address_space(3))) void* lds_ptr;
@@ -466,6 +466,33 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
 #pragma unroll
       for (int i = 1; i < kWaves; i++) mm = fmaxf(mm, red[i]);
       sg_atomic_max_nonneg(amax + it.seq, mm);
+    }
+    // The workgroup holds the whole sequence (every row of every head; the
+    // caller passes qo.q8 only then), so its maximum is the sequence's and
+    // the output is quantized here, from the values just stored, as the
+    // quantizer would quantize them: lane (query ln, group g4) codes dims
+    // 16 mt + 4 g4 .. + 3 of its head, 4 bytes of K-block (head * 256 +
+    // 16 mt) / 32 per mt.
+    if (qo.q8 && qvalid) {
+      float mm = red[0];
+#pragma unroll
+      for (int i = 1; i < kWaves; i++) mm = fmaxf(mm, red[i]);
+      float scale = 1.0f, inv = 0.0f;
+      if (mm != 0.0f) {
+        scale = mm / 127.0f;
+        inv = 1.0f / scale;
+      }
+      const int row = r0 + qrow;
+      if (hg == 0 && g4 == 0) qo.row_scale[row] = scale;
+#pragma unroll
+      for (int mt = 0; mt < kHD / 16; mt++) {
+        const int col = head * kHD + 16 * mt + 4 * g4;
+        uint32_t u = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          u |= (uint32_t)(uint8_t)(int8_t)(int)sg_quant_code(o[mt][j] * f, inv) << (8 * j);
+        *reinterpret_cast<uint32_t*>(qo.q8 + ((int64_t)(col >> 5) * qo.a_rows + row) * 32 + (col & 31)) = u;
+      }
     }
   }
 }
@@ -820,10 +847,10 @@ template <bool QPRE, bool RS>
 void launch_attn(dim3 grid, hipStream_t s, const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh,
                  const _Float16* kl, int ldk, const _Float16* vt, int ldvt, float* out, int ldo,
                  const int32_t* seq_off, const int32_t* voff, const sg_item* items, int G, float sscale, float* amax,
-                 const sg_attn_qpre& qp) {
+                 const sg_attn_qpre& qp, const sg_attn_qout& qo) {
   if constexpr (RS)
     hipLaunchKernelGGL((k_attn_rs<QPRE>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
-                       seq_off, voff, items, G, sscale, amax, qp);
+                       seq_off, voff, items, G, sscale, amax, qp, qo);
   else
     hipLaunchKernelGGL((k_attn_ring<QPRE>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
                        seq_off, voff, items, G, sscale, amax, qp);
@@ -833,9 +860,16 @@ void launch_attn(dim3 grid, hipStream_t s, const _Float16* qh, const _Float16* q
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
                      const _Float16* vt, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
-                     float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre) {
+                     float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre,
+                     const sg_attn_qout* qout) {
   if (n_items <= 0) return hipSuccess;
   if (hd != kHD || HKV <= 0 || H % HKV || max_len <= 0) return hipErrorInvalidValue;
+  // The quantizing epilogue needs the register-scores kernel, one workgroup per
+  // sequence (one kv head, every chunk of the sequence in one item) and amax.
+  if (qout && (!qout->q8 || !qout->row_scale || HKV != 1 || max_len > kAttnRegKeys || !amax ||
+               (H / HKV) * ((max_len + kQW - 1) / kQW) > kWaves))
+    return hipErrorInvalidValue;
+  const sg_attn_qout qo = qout ? *qout : sg_attn_qout{nullptr, 0, nullptr};
   if ((ldk | ldvt) & 7 || (ldo & 3)) return hipErrorInvalidValue;
   const float sscale = scale / (kQKScale * kQKScale);
   const dim3 grid(n_items, HKV);
@@ -846,12 +880,13 @@ hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Flo
         (reinterpret_cast<uintptr_t>(qpre->cos_t) & 15) || (reinterpret_cast<uintptr_t>(qpre->sin_t) & 15))
       return hipErrorInvalidValue;  // float4 loads of Q rows, weights and table rows
     (rs ? launch_attn<true, true> : launch_attn<true, false>)(grid, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out,
-                                                              ldo, seq_off, voff, items, H / HKV, sscale, amax, *qpre);
+                                                              ldo, seq_off, voff, items, H / HKV, sscale, amax, *qpre,
+                                                              qo);
   } else {
     if (ldq & 7) return hipErrorInvalidValue;
     (rs ? launch_attn<false, true> : launch_attn<false, false>)(grid, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt,
                                                                 out, ldo, seq_off, voff, items, H / HKV, sscale, amax,
-                                                                sg_attn_qpre{});
+                                                                sg_attn_qpre{}, qo);
   }
   return hipGetLastError();
 }

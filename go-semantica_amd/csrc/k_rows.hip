@@ -15,6 +15,7 @@
 namespace {
 
 constexpr int kRowsPerBlock = 32;  // 256 threads, 8 lanes per row
+static_assert(kRowsPerBlock == sgk::kRowKernelRows, "row kernels' workgroup rows");
 constexpr int kThreads = 256;
 
 __device__ __forceinline__ uint16_t rd_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
@@ -346,6 +347,71 @@ __global__ __launch_bounds__(kThreads) void k_post_res_norm(const float* __restr
     m = sg_max8(m);
     const int r0 = blockIdx.x * kRowsPerBlock;
     sg_block_seq_max<kThreads>(m, valid && j == 0, row, r0, min(r0 + kRowsPerBlock, T) - 1, row_seq, amax);
+  }
+}
+
+// k_post_res_norm followed by the next GEMM's operand, in one launch, for
+// batches in which every sequence's rows lie inside one workgroup's
+// kRowsPerBlock rows (the caller checks; short sequences, the serving case).
+// Each sequence's max|xn| is then complete inside the workgroup, so xn --
+// still in the lanes that formed it -- is quantized with it right away, as
+// k_norm_quantize would quantize the xn it recomputes from h: the same values,
+// scale, reciprocal and codes (quantize.go:29-103 per sequence), into the
+// block-major operand q8 [D/32][a_rows][32] and row_scale.  The sequences'
+// maxima also go to amax, as k_post_res_norm leaves them.
+template <int NC>
+__global__ __launch_bounds__(kThreads) void k_post_res_norm_q(const float* __restrict__ o, float* __restrict__ h,
+                                                              const float* __restrict__ w_post,
+                                                              const float* __restrict__ w_next, float eps, int T,
+                                                              const int32_t* __restrict__ row_seq,
+                                                              float* __restrict__ amax, int8_t* __restrict__ q8,
+                                                              int a_rows, float* __restrict__ row_scale) {
+  constexpr int D = NC * 32;
+  __shared__ __attribute__((aligned(16))) float tiles[kThreads / SG_WAVE][8 * 40];
+  __shared__ float rmax[kRowsPerBlock];
+  __shared__ int rseq[kRowsPerBlock];
+  const int rl = threadIdx.x >> 3, row = blockIdx.x * kRowsPerBlock + rl;
+  const int j = threadIdx.x & 7, r = rl & 7;
+  const bool valid = row < T;
+  f32x4_t x[NC];
+  float m = 0.0f;
+  if (valid) {
+    f32x4_t hv[NC];
+    const f32x4_t* op = reinterpret_cast<const f32x4_t*>(o + (int64_t)row * D) + j;
+    const f32x4_t* hp = reinterpret_cast<const f32x4_t*>(h + (int64_t)row * D) + j;
+#pragma unroll
+    for (int c = 0; c < NC; c++) x[c] = __builtin_nontemporal_load(&op[8 * c]);
+#pragma unroll
+    for (int c = 0; c < NC; c++) hv[c] = __builtin_nontemporal_load(&hp[8 * c]);
+    m = sg_post_res_norm_f4<NC>(x, hv, h + (int64_t)row * D, w_post, w_next, eps, nullptr,
+                                tiles[threadIdx.x / SG_WAVE], r, j);
+  }
+  m = sg_max8(m);
+  if (j == 0) {
+    rmax[rl] = m;  // 0 for rows past T
+    rseq[rl] = valid ? row_seq[row] : -1;
+  }
+  __syncthreads();
+  if (!valid) return;
+  // The row's sequence maximum over this workgroup's rows (all of them).
+  const int sq = rseq[rl];
+  float sm = 0.0f;
+  for (int i = 0; i < kRowsPerBlock; i++) sm = rseq[i] == sq ? fmaxf(sm, rmax[i]) : sm;
+  const bool first = rl == 0 || rseq[rl - 1] != sq;
+  if (amax && first && j == 0) sg_atomic_max_nonneg(amax + sq, sm);
+  float scale = 1.0f, inv = 0.0f;
+  if (sm != 0.0f) {
+    scale = sm / 127.0f;
+    inv = 1.0f / scale;
+  }
+  if (j == 0) row_scale[row] = scale;
+  int8_t* qr = q8 + (int64_t)row * 32 + 4 * j;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    float cv[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) cv[t] = sg_quant_code(x[c][t], inv);
+    store_codes4(qr + (int64_t)c * a_rows * 32, cv);
   }
 }
 
@@ -725,6 +791,17 @@ hipError_t post_res_norm(const float* o, float* h, const float* w_post, const fl
   SG_DISPATCH_NPL(d, NPL,
                   hipLaunchKernelGGL(k_post_res_norm<NPL / 4>, dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads),
                                      0, s, o, h, w_post, w_next, eps, T, xn, row_seq, amax));
+  return hipGetLastError();
+}
+
+hipError_t post_res_norm_quantize(const float* o, float* h, const float* w_post, const float* w_next, float eps,
+                                  int T, int d, const int32_t* row_seq, float* amax, int8_t* q8, int a_rows,
+                                  float* row_scale, hipStream_t s) {
+  if (T <= 0) return hipSuccess;
+  if (!q8 || !row_scale || !w_next || a_rows < T) return hipErrorInvalidValue;
+  SG_DISPATCH_NPL(d, NPL,
+                  hipLaunchKernelGGL(k_post_res_norm_q<NPL / 4>, dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads),
+                                     0, s, o, h, w_post, w_next, eps, T, row_seq, amax, q8, a_rows, row_scale));
   return hipGetLastError();
 }
 

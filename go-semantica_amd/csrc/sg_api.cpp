@@ -58,6 +58,10 @@ struct Meta {
   int Tp = 0;         // V^T columns: every sequence padded to whole 32-key tiles
   int max_len = 0;    // longest sequence
   double sum_sq = 0;  // sum over sequences of S^2 (attention work)
+  // Every sequence inside one row-kernel workgroup's rows / one attention
+  // work item: the post-norms and the attention then quantize the next GEMM
+  // operand themselves (the short-sequence serving case).
+  bool seq_in_row_block = false, seq_one_item = false;
   // device views into one buffer
   int32_t* row_seq = nullptr;
   int32_t* row_pos = nullptr;
@@ -154,6 +158,11 @@ int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev,
   }
   m.n_items = n_items;
   m.n_vtiles = n_vt;
+  m.seq_one_item = n_items == n_seq;
+  m.seq_in_row_block = true;
+  for (int i = 0; i < n_seq; i++)
+    if (off[i + 1] > off[i] && off[i] / sgk::kRowKernelRows != (off[i + 1] - 1) / sgk::kRowKernelRows)
+      m.seq_in_row_block = false;
   m.Tp = vo[n_seq];
   m.row_seq = d;
   m.row_pos = d + T;
@@ -511,11 +520,22 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
               sgk::embed_norm(d_tokens, T, m->emb_q, m->emb_s, c.vocab_size, d, m->sqrt_d, m->layers[0].attn_norm,
                               eps, meta.row_seq, h, nullptr, site(0, 0), w.err.as<int32_t>(), s));
   }
+  // Short sequences (each inside one row-kernel workgroup / attention item):
+  // the unfused post-norms quantize the next GEMM operand in the same launch,
+  // and the attention its own output, so the separate quantizer launches go.
+  // a8_ready: the operand of the next QKV GEMM is already in a8.
+  const bool q_rows = meta.seq_in_row_block;
+  const bool q_attn = meta.seq_one_item && c.num_kv_heads == 1 && meta.max_len <= sgk::kAttnRegKeys;
+  bool a8_ready = false;
+  auto post_norm_q = [&](const float* w_post, const float* w_next, float* am) {
+    return sgk::post_res_norm_quantize(o, h, w_post, w_next, eps, T, d, meta.row_seq, am, a8, ar, sx, s);
+  };
   for (int l = l0; l < l1; l++) {
     if (l == stop) break;
     const LayerDev& ly = m->layers[l];
     // The pre-norm's output xn is never stored: recomputed from h while quantizing.
-    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.attn_norm, site(l, 0)));
+    if (!a8_ready) SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.attn_norm, site(l, 0)));
+    a8_ready = false;
     SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), gemm(ly.wqkv, ly.sqkv, qkv, nqkv, d));
     if (tr && tr->qkv) SG_HIP(tap(tr->qkv, qkv, l, nqkv));
     if (m->attn_mode == SG_ATTN_EXACT) {
@@ -537,25 +557,31 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
                              m->sin_t, eps, ks_h, ks_l, kvd, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles,
                              vt_h, ldvt, s));
       const sg_attn_qpre qpre{qkv, nqkv, ly.q_norm, m->cos_t, m->sin_t, eps};
+      const sg_attn_qout qout{a8, ar, sx};
       SG_LAUNCH(SG_K_ATTENTION, attn_flops,
                 sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, ldvt, att, qd, meta.seq_off,
                                meta.voff, meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd,
-                               m->attn_scale, site(l, 1), meta.max_len, s, &qpre));
+                               m->attn_scale, site(l, 1), meta.max_len, s, &qpre, q_attn ? &qout : nullptr));
     }
     if (tr && tr->att) SG_HIP(tap(tr->att, att, l, qd));
-    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), quant(att, qd, site(l, 1)));
+    if (!(q_attn && m->attn_mode != SG_ATTN_EXACT))
+      SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(qd), quant(att, qd, site(l, 1)));
     // The O projection and the residual post-norm: one launch for large
     // batches (o stays on chip), else the GEMM then k_post_res_norm.
     if (sgk::gemm_res_norm_fused(T, d, ly.post_attn, ly.ffn_norm)) {
       SG_LAUNCH(SG_K_GEMM_NORM, gemm_ops(d, qd),
                 sgk::gemm_q8_res_norm(a8, ar, ly.wo, ly.so, sx, o, T, d, qd, h, ly.post_attn, ly.ffn_norm, eps,
                                       nullptr, meta.row_seq, site(l, 2), s));
+    } else if (q_rows) {
+      SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), gemm(ly.wo, ly.so, o, d, qd));
+      SG_LAUNCH(SG_K_NORM, t * d * 13.0, post_norm_q(ly.post_attn, ly.ffn_norm, site(l, 2)));
     } else {
       SG_LAUNCH(SG_K_GEMM, gemm_ops(d, qd), gemm(ly.wo, ly.so, o, d, qd));
       SG_LAUNCH(SG_K_NORM, t * d * 12.0,
                 sgk::post_res_norm(o, h, ly.post_attn, ly.ffn_norm, eps, T, d, nullptr, meta.row_seq, site(l, 2), s));
     }
-    SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.ffn_norm, site(l, 2)));
+    if (!(q_rows && !sgk::gemm_res_norm_fused(T, d, ly.post_attn, ly.ffn_norm)))
+      SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.ffn_norm, site(l, 2)));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(2 * ff, d),
               sgk::gemm_q8_gelu(a8, ar, ly.wgu, ly.sgu, sx, g, T, ff, d, meta.row_seq, site(l, 3), s));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(ff), quant(g, ff, site(l, 3)));
@@ -565,6 +591,10 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
       SG_LAUNCH(SG_K_GEMM_NORM, gemm_ops(d, ff),
                 sgk::gemm_q8_res_norm(a8, ar, ly.wd, ly.sd, sx, o, T, d, ff, h, ly.post_ffw, w_next, eps,
                                       last ? xn : nullptr, meta.row_seq, last ? nullptr : site(l + 1, 0), s));
+    } else if (q_rows && !last) {
+      SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), gemm(ly.wd, ly.sd, o, d, ff));
+      SG_LAUNCH(SG_K_NORM, t * d * 13.0, post_norm_q(ly.post_ffw, w_next, site(l + 1, 0)));
+      a8_ready = true;
     } else {
       SG_LAUNCH(SG_K_GEMM, gemm_ops(d, ff), gemm(ly.wd, ly.sd, o, d, ff));
       SG_LAUNCH(SG_K_NORM, t * d * (last ? 16.0 : 12.0),

@@ -21,6 +21,17 @@ struct sg_attn_qpre {
   float eps;
 };
 
+// Optional attention epilogue: the attention output quantized per sequence
+// into the block-major GEMM operand q8[H*hd/32][a_rows][32] and row_scale
+// (quantize's arithmetic on the values written to out), for launches in which
+// one workgroup holds every row and head of its sequence (one work item per
+// sequence and a single kv head); the caller checks.
+struct sg_attn_qout {
+  int8_t* q8;
+  int a_rows;
+  float* row_scale;
+};
+
 namespace sgk {
 
 // GEMM operands are block-major int8 [K/32][rows][32]; activation buffers hold
@@ -81,6 +92,17 @@ hipError_t qknorm_rope(float* q, int ldq, float* k, int ldk, const float* qw, co
 // amax (optional) per sequence of max|xn|.
 hipError_t post_res_norm(const float* o, float* h, const float* w_post, const float* w_next, float eps, int T,
                          int d, float* xn, const int32_t* row_seq, float* amax, hipStream_t s);
+// Rows per workgroup of the row kernels (post_res_norm, norm_quantize, ...).
+constexpr int kRowKernelRows = 32;
+// post_res_norm, then xn quantized per sequence into the block-major GEMM
+// operand q8[d/32][a_rows][32] and row_scale[T] -- the values, scale and codes
+// norm_quantize would produce from the new h -- in one launch.  Valid only when
+// every sequence's rows lie inside one block of kRowKernelRows rows
+// (off[s] / kRowKernelRows == (off[s+1] - 1) / kRowKernelRows); amax (optional)
+// receives the sequences' max|xn| as post_res_norm leaves them.
+hipError_t post_res_norm_quantize(const float* o, float* h, const float* w_post, const float* w_next, float eps,
+                                  int T, int d, const int32_t* row_seq, float* amax, int8_t* q8, int a_rows,
+                                  float* row_scale, hipStream_t s);
 // g = geluquick(gate)*up over rows x cols; amax (optional) per sequence of max|g|.
 hipError_t gelu_mul(float* g, int ldd, const float* gate, int ldg, const float* up, int ldu, int rows, int cols,
                     const int32_t* row_seq, float* amax, hipStream_t s);
@@ -150,7 +172,8 @@ hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, 
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
                      const _Float16* vt, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
-                     float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre = nullptr);
+                     float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre = nullptr,
+                     const sg_attn_qout* qout = nullptr);
 
 // ---- attention in the reference's float32 order (k_attn_exact.hip) ----
 // out[T][ldo] (head h at h*hd) from q[T][ldq], k/v[T][ldkv] (kv head h / (H/HKV)),

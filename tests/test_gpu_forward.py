@@ -340,6 +340,46 @@ def test_sequence_groups_match_one_stream(tiny_gpu):
             assert (eh.value.code, eh.value.message) == (ed.value.code, ed.value.message) == expect
 
 
+@pytest.mark.parametrize("mode", ["fast", "exact"])
+def test_short_sequence_fusions_match_unfused(full_gpu, mode):
+    """Short sequences take fused launches.  When every sequence of a batch
+    lies inside one 32-row workgroup of the row kernels, the post-norms
+    quantize the next GEMM operand themselves (k_post_res_norm_q), and when
+    every sequence is one attention work item (at most 32 tokens with 3 query
+    heads) the attention kernel quantizes its own output (fast mode).  A
+    sequence's embedding does not depend on the rest of its batch, so the same
+    sequences embedded in batches that take both fused forms, only the
+    attention one (a sequence crosses a 32-row boundary), or neither (a
+    40-token sequence crosses it and needs two attention items) agree bit for
+    bit, over 24 layers at full size."""
+    from semantica_gpu import _lib
+    rng = np.random.default_rng(31)
+    x1, x2, x3, x40 = (rng.integers(2, 262144, size=n).astype(np.int32) for n in (32, 7, 19, 40))
+    batches = {
+        "fused (one 32-token sequence)": [x1],
+        "fused (7 + 19 tokens in one row block)": [x2, x3],
+        "fused (four sequences in row blocks)": [x1, x2, x3, x2[:5]],
+        "attention-fused only (7 + 32: a sequence crosses row 32)": [x2, x1, x3],
+        "unfused (a 40-token sequence first)": [x40, x1, x2, x3],
+    }
+    full_gpu.set_attention_mode(_lib.SG_ATTN_EXACT if mode == "exact" else _lib.SG_ATTN_FAST)
+    try:
+        got = {}
+        for name, seqs in batches.items():
+            toks = np.concatenate(seqs)
+            off = np.concatenate([[0], np.cumsum([len(q) for q in seqs])]).astype(np.int32)
+            say(f"short-sequence fusions ({mode}): {name}")
+            y = full_gpu.forward_packed(toks, off, 768)
+            for q, e in zip(seqs, y):
+                got.setdefault(q.tobytes(), []).append((name, e))
+    finally:
+        full_gpu.set_attention_mode(_lib.SG_ATTN_FAST)
+    for key, runs in got.items():
+        ref_name, ref = runs[0]
+        for name, e in runs[1:]:
+            assert np.array_equal(e.view(np.uint32), ref.view(np.uint32)), (len(key) // 4, ref_name, name)
+
+
 def test_concurrent_callers_match_serial(tiny_gpu):
     """TestConcurrentBufferPooling (internal/runtime/pooling_test.go:34-75):
     seven host threads call sg_forward on one model at once, four times each
