@@ -373,6 +373,9 @@ __global__ __launch_bounds__(kThreads) void k_post_res_norm_q(const float* __res
   const int rl = threadIdx.x >> 3, row = blockIdx.x * kRowsPerBlock + rl;
   const int j = threadIdx.x & 7, r = rl & 7;
   const bool valid = row < T;
+  // The row's sequence now: its load overlaps the row loads instead of
+  // following the norms.
+  const int sq = valid ? row_seq[row] : -1;
   f32x4_t x[NC];
   float m = 0.0f;
   if (valid) {
@@ -389,12 +392,11 @@ __global__ __launch_bounds__(kThreads) void k_post_res_norm_q(const float* __res
   m = sg_max8(m);
   if (j == 0) {
     rmax[rl] = m;  // 0 for rows past T
-    rseq[rl] = valid ? row_seq[row] : -1;
+    rseq[rl] = sq;
   }
   __syncthreads();
   if (!valid) return;
   // The row's sequence maximum over this workgroup's rows (all of them).
-  const int sq = rseq[rl];
   float sm = 0.0f;
   for (int i = 0; i < kRowsPerBlock; i++) sm = rseq[i] == sq ? fmaxf(sm, rmax[i]) : sm;
   const bool first = rl == 0 || rseq[rl - 1] != sq;
