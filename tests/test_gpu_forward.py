@@ -530,6 +530,33 @@ def test_exact_attention_forward_config0(full_gpu, full_oracle):
     _exact_forward(full_gpu, full_oracle, toks, off, 768, "c0 exact")
 
 
+@pytest.mark.parametrize("case", ["short_mixed", "long_mixed", "many_tiny", "singletons", "one_row_block"])
+def test_exact_attention_forward_random_batches(full_gpu, full_oracle, case):
+    """Exact attention makes every embedding comparable bit for bit with the
+    oracle's block-serial forward, so ragged batches chosen to cross the
+    forward's dispatch boundaries are checked that way over all 24 layers:
+    short mixed lengths (register-direct GEMMs with and without the
+    MFMA-ahead loop, attention items of one and several workgroups), long
+    sequences next to short ones (the ring attention kernel, 2048 keys),
+    hundreds of tiny sequences, single-token sequences (the short-sequence
+    fused post-norm quantize), and one 32-row block of several sequences."""
+    rng = np.random.default_rng({"short_mixed": 41, "long_mixed": 42, "many_tiny": 43, "singletons": 44,
+                                 "one_row_block": 45}[case])
+    if case == "short_mixed":
+        lens = np.exp(rng.uniform(0, np.log(300), size=37)).astype(int) + 1
+    elif case == "long_mixed":
+        lens = np.array([1, 2048, 700, 33, 1200, 513])
+    elif case == "many_tiny":
+        lens = rng.integers(1, 65, size=200)
+    elif case == "singletons":
+        lens = np.ones(3, int)
+    else:
+        lens = np.array([5, 11, 2, 14])
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    toks = rng.integers(2, 262144, size=int(off[-1])).astype(np.int32)
+    _exact_forward(full_gpu, full_oracle, toks, off, 768, f"random batch {case}")
+
+
 def test_exact_attention_forward_config4(full_gpu, full_oracle):
     """Config 4 at full size: 256 log-uniform lengths in [8, 512] (seed 1),
     Matryoshka dim 256, 24 layers, two sequence groups on two streams, exact
