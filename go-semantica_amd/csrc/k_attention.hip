@@ -201,18 +201,22 @@ __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bq
 
 constexpr int kTileBytes = 32 * 1024;  // one K or V^T tile, hi and lo halves
 constexpr int kRing = 3;               // tile stages in LDS
+constexpr int kScoreBytes = kWaves * 2048;  // one tile's scores, 8 floats per lane and wave
 
-// Sequences of at most kRegTiles tiles (every sequence of the launch at most
-// kRegKeys keys): pass 1 keeps each lane's raw scores in registers (8 per
-// 32-key tile, 128 VGPRs at 512 keys) and pass 2 reads them back instead of
-// recomputing S^T, so K is streamed once and a third of the MFMAs and LDS
-// reads go away.  The tiles reach LDS by buffer_load ... lds (no staging
-// registers): one stream of 2 nt items, the nt K tiles then the nt V^T tiles,
-// item i in ring stage i % 3, issued two items ahead; each wave issues four
-// 1-KB copies per item (past the last item it re-copies that one into the free
-// stage), so one constant vmcnt per step says "item i has landed" and the
-// barrier after it publishes every wave's copies and retires the stage the
-// next copies overwrite.
+// Two passes over a sequence's 32-key tiles: pass 1 keeps each lane's scaled
+// scores in registers (8 per tile, 128 VGPRs for the first kRegTiles tiles)
+// and pass 2 reads them back instead of recomputing S^T, so K is streamed once
+// and a third of the MFMAs and LDS reads go away.  SPILL (a launch with a
+// sequence longer than kRegKeys keys): the tiles past kRegTiles write their
+// scores to a per-workgroup spill range in pass 1 and read them back in pass 2
+// through LDS, carried by the V^T item before their own.  The tiles reach LDS
+// by buffer_load ... lds (no staging registers): one stream of 2 nt items, the
+// nt K tiles then the nt V^T tiles, item i in ring stage i % 3, issued two
+// items ahead; each wave issues four 1-KB copies per item (six when it also
+// carries scores; past the last item it re-copies that one into the free
+// stage), so a vmcnt of the next item's copy count says "item i has landed"
+// and the barrier after it publishes every wave's copies and retires the
+// stage the next copies overwrite.
 //
 // LDS layouts, XOR-swizzled in 16-byte chunks so that the 16x16x32 fragment
 // reads (16 rows x 4 lane groups) hit distinct banks with unpadded rows:
@@ -222,13 +226,15 @@ constexpr int kRing = 3;               // tile stages in LDS
 //              layout); chunk c at position c ^ ((d >> 1) & 7).
 // A copy lane picks the global chunk its LDS position holds, so the swizzle
 // costs nothing at copy time; fragment addresses are one XOR per k-step.
-template <bool QPRE>
+template <bool QPRE, bool SPILL>
 __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
     const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
     const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vt, int ldvt, float* __restrict__ out,
     int ldo, const int32_t* __restrict__ seq_off, const int32_t* __restrict__ voff, const sg_item* __restrict__ items,
-    int G, float sscale, float* __restrict__ amax, sg_attn_qpre qp, sg_attn_qout qo) {
+    int G, float sscale, float* __restrict__ amax, sg_attn_qpre qp, sg_attn_qout qo, float* __restrict__ spill,
+    int spill_tiles) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kRing * kTileBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char slds[SPILL ? kRing * kScoreBytes : 16];
   __shared__ float red[kWaves];
   typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -241,7 +247,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6) & (kWaves - 1);
   const int ln = lane & 15, g4 = lane >> 4;
   const int nqb = (S + kQW - 1) / kQW;
-  const int nt = (S + kBK - 1) / kBK;  // <= kRegTiles (the host checks the longest sequence)
+  const int nt = (S + kBK - 1) / kBK;  // <= kRegTiles unless SPILL (the host checks the longest sequence)
   const int c = it.c0 + w;
   const bool active = c < G * nqb;  // wave-uniform
   const int hg = active ? c / nqb : 0;
@@ -294,11 +300,33 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
       }
     }
   };
+  // SPILL: this workgroup's spilled scores, spill_tiles tiles of kScoreBytes
+  // (wave w's 2 KB at w * 2048: lane l's keys 4g4 + r at 16 l, 16 + 4g4 + r at
+  // 1024 + 16 l).  V^T item nt + t - 1 also carries tile t's scores when
+  // t >= kRegTiles, two more copies per wave into the item's score stage.
+  float* const wspill = SPILL ? spill + (size_t)(blockIdx.y * gridDim.x + blockIdx.x) * spill_tiles * (kScoreBytes / 4)
+                              : nullptr;
+  const i32x4_t rsp = sg_raw_rsrc(wspill);
+  const int last = 2 * nt - 1;
+  auto carries = [&](int src) { return SPILL && src >= nt + kRegTiles - 1 && src < last; };
   auto issue = [&](int item) {
-    const int last = 2 * nt - 1;
     const int src = item < last ? item : last;
     const uint32_t dst = (uint32_t)(uintptr_t)(lds_ptr)(lds + ((unsigned)item % kRing) * kTileBytes + w * 4096);
     copy_tile(dst, src < nt, src < nt ? src : src - nt);
+    if (carries(src)) {
+      const uint32_t sd = (uint32_t)(uintptr_t)(lds_ptr)(slds + ((unsigned)item % kRing) * kScoreBytes + w * 2048);
+      const uint32_t so = (uint32_t)((src - nt + 1 - kRegTiles) * kScoreBytes + w * 2048);
+      sg_lds_copy16(sd, 16u * lane, rsp, so);
+      sg_lds_copy16(sd + 1024u, 16u * lane + 1024u, rsp, so);
+    }
+  };
+  // Wait until item i has landed, item i + 1 (4 copies per wave, or 6 when it
+  // carries scores) may still be in flight.
+  auto wait_item = [&](int i) {
+    if (carries(i + 1 < last ? i + 1 : last))
+      sg_wait_vmcnt<6>();
+    else
+      sg_wait_vmcnt<4>();
   };
   issue(0);
   issue(1);
@@ -344,19 +372,19 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
   };
   float m = -INFINITY;
   f32x4_t sr[kRegTiles][2];
+  // The scores are kept as s = raw * sscale (exact: sscale is a power of
+  // two); a key past S (only in a sequence's last tile) keeps -inf, so pass
+  // 2's fastExp clamp gives it a weight of exactly 0 without a per-key test
+  // there.
 #pragma unroll
   for (int t = 0; t < kRegTiles; t++) {
     if (t < nt) {
-      sg_wait_vmcnt<4>();  // item t landed (item t + 1 may still be in flight)
+      wait_item(t);  // item t landed (item t + 1 may still be in flight)
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       issue(t + 2);
       // Every wave computes (an inactive wave's results are never stored).
       scores2(lds + (t % kRing) * kTileBytes, sr[t][0], sr[t][1]);
-      // The registers keep the scaled scores s = raw * sscale (exact: sscale
-      // is a power of two); a key past S (only in a sequence's last tile)
-      // keeps -inf, so pass 2's fastExp clamp gives it a weight of exactly 0
-      // without a per-key test there.
       const int kt = t * kBK;
       if (kt + kBK <= S) {
 #pragma unroll
@@ -373,6 +401,36 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
           m = fmaxf(m, fmaxf(sr[t][0][r], sr[t][1][r]));
         }
       }
+    }
+  }
+  if constexpr (SPILL) {
+    // Tiles past kRegTiles: their scores go to this wave's spill slots.
+    for (int t = kRegTiles; t < nt; t++) {
+      wait_item(t);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      issue(t + 2);
+      f32x4_t s0, s1;
+      scores2(lds + (t % kRing) * kTileBytes, s0, s1);
+      const int kt = t * kBK;
+      if (kt + kBK <= S) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          s0[r] *= sscale;
+          s1[r] *= sscale;
+          m = fmaxf(m, fmaxf(s0[r], s1[r]));
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          s0[r] = key_of(kt, 0, r) < S ? s0[r] * sscale : -INFINITY;
+          s1[r] = key_of(kt, 1, r) < S ? s1[r] * sscale : -INFINITY;
+          m = fmaxf(m, fmaxf(s0[r], s1[r]));
+        }
+      }
+      float* sp = wspill + (size_t)(t - kRegTiles) * (kScoreBytes / 4) + w * 512 + 4 * lane;
+      *reinterpret_cast<f32x4_t*>(sp) = s0;
+      *reinterpret_cast<f32x4_t*>(sp + 256) = s1;
     }
   }
   m = fmaxf(m, __shfl_xor(m, 16));
@@ -410,31 +468,41 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
       __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
     }
   };
+  // One tile of pass 2: the weights from its scores, then P.V on its V^T item.
+  auto tile2 = [&](const f32x4_t& s0, const f32x4_t& s1, int t) {
+    const int item = nt + t;
+    float e[8];  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
 #pragma unroll
-  for (int t = 0; t < kRegTiles; t++) {
-    if (t < nt) {
-      const int item = nt + t;
-      float e[8];  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
+    for (int r = 0; r < 4; r++) {
+      e[r] = sg_fast_exp_nonpos(s0[r] - m);
+      e[4 + r] = sg_fast_exp_nonpos(s1[r] - m);
+    }
 #pragma unroll
-      for (int st = 0; st < 2; st++)
+    for (int k = 0; k < 8; k++) lsum = lsum + e[k];
+    u32x4_t uh, ul;
 #pragma unroll
-        for (int r = 0; r < 4; r++) e[4 * st + r] = sg_fast_exp_nonpos(sr[t][st][r] - m);
+    for (int k = 0; k < 4; k++) {
+      uint32_t h, l;
+      split_pair(e[2 * k], e[2 * k + 1], kPScale, h, l);
+      uh[k] = h;
+      ul[k] = l;
+    }
+    const half8_t ph = __builtin_bit_cast(half8_t, uh), pl = __builtin_bit_cast(half8_t, ul);
+    wait_item(item);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    issue(item + 2);
+    pv(lds + ((unsigned)item % kRing) * kTileBytes, ph, pl);
+  };
 #pragma unroll
-      for (int k = 0; k < 8; k++) lsum = lsum + e[k];
-      u32x4_t uh, ul;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        uint32_t h, l;
-        split_pair(e[2 * k], e[2 * k + 1], kPScale, h, l);
-        uh[k] = h;
-        ul[k] = l;
-      }
-      const half8_t ph = __builtin_bit_cast(half8_t, uh), pl = __builtin_bit_cast(half8_t, ul);
-      sg_wait_vmcnt<4>();
-      __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
-      issue(item + 2);
-      pv(lds + ((unsigned)item % kRing) * kTileBytes, ph, pl);
+  for (int t = 0; t < kRegTiles; t++)
+    if (t < nt) tile2(sr[t][0], sr[t][1], t);
+  if constexpr (SPILL) {
+    // Tile t's scores landed with item nt + t - 1 (published by its barrier);
+    // the stage is overwritten only after the next barrier.
+    for (int t = kRegTiles; t < nt; t++) {
+      const unsigned char* sb = slds + ((unsigned)(nt + t - 1) % kRing) * kScoreBytes + w * 2048 + 16 * lane;
+      tile2(*reinterpret_cast<const f32x4_t*>(sb), *reinterpret_cast<const f32x4_t*>(sb + 1024), t);
     }
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-copies past the last item have landed
@@ -493,263 +561,6 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
           u |= (uint32_t)(uint8_t)(int8_t)(int)sg_quant_code(o[mt][j] * f, inv) << (8 * j);
         *reinterpret_cast<uint32_t*>(qo.q8 + ((int64_t)(col >> 5) * qo.a_rows + row) * 32 + (col & 31)) = u;
       }
-    }
-  }
-}
-
-// Sequences longer than kRegKeys keys: the same tile pipeline, LDS layouts
-// and products as k_attn_rs, with pass 2 recomputing each tile's S^T instead
-// of keeping the scores in registers.  One stream of 3 nt items through the
-// 3-stage ring, issued two items ahead: the nt K tiles of pass 1 (row max),
-// then K tile t and V^T tile t in turn (scores, probabilities, O^T += V^T P^T).
-// Every value and its rounding order are k_attn_rs's, so a sequence gives the
-// same bits on either kernel.
-template <bool QPRE>
-__global__ __launch_bounds__(kNT, 2) void k_attn_ring(
-    const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
-    const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vt, int ldvt, float* __restrict__ out,
-    int ldo, const int32_t* __restrict__ seq_off, const int32_t* __restrict__ voff, const sg_item* __restrict__ items,
-    int G, float sscale, float* __restrict__ amax, sg_attn_qpre qp) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kRing * kTileBytes];
-  __shared__ float red[kWaves];
-  typedef __attribute__((address_space(3))) void* lds_ptr;
-
-  const sg_item it = items[blockIdx.x];
-  const int kvh = blockIdx.y;
-  const int r0 = seq_off[it.seq];
-  const int S = seq_off[it.seq + 1] - r0;
-  const int vo = voff[it.seq];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6) & (kWaves - 1);
-  const int ln = lane & 15, g4 = lane >> 4;
-  const int nqb = (S + kQW - 1) / kQW;
-  const int nt = (S + kBK - 1) / kBK;
-  const int c = it.c0 + w;
-  const bool active = c < G * nqb;  // wave-uniform
-  const int hg = active ? c / nqb : 0;
-  const int q0 = active ? (c % nqb) * kQW : 0;
-  const int head = kvh * G + hg;
-  const int qrow = q0 + ln;
-  const bool qvalid = active && qrow < S;
-  const int qr = r0 + min(qrow, S - 1);
-
-  // ---- copies ----
-  // Wave w's four copies of an item land at w * 4 KB + i * 1 KB of the stage.
-  // K item: copy i moves rows R = 8w + 2i and 8w + 2i + 1 (hi for waves 0-3,
-  // lo for waves 4-7); lane L takes row R = 8w + 2i + L / 32 and LDS position
-  // L % 32, i.e. global chunk (L % 32) ^ (R & 15).  Keys past the sequence's
-  // end are clamped to its last key and masked out of the scores below.
-  // V^T item: copy i moves dims 32w + 8i .. + 7; lane L takes dim
-  // d = 32w + 8i + L / 8, position L % 8, global chunk (L % 8) ^ ((d >> 1) & 7);
-  // every tile of a sequence lies inside its padded V^T columns.
-  const i32x4_t rk = sg_raw_rsrc((w < 4 ? kh : kl) + (int64_t)r0 * ldk + kvh * kHD);
-  const i32x4_t rv = sg_raw_rsrc(vt + (int64_t)kvh * kHD * ldvt + 2 * vo);
-  // Per-lane byte offsets, loop-invariant: K copy i at key row kkey(i) of a
-  // tile (kvo; the tile's first row goes in the scalar offset), V^T copy i
-  // (voffs; the tile's columns go in the scalar offset).
-  auto kkey = [&](int i) { return ((8 * w + 2 * i) & 31) + (lane >> 5); };
-  uint32_t kvo[4], voffs[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int R = 8 * w + 2 * i + (lane >> 5);
-    kvo[i] = (uint32_t)kkey(i) * (uint32_t)ldk * 2u + 16u * (uint32_t)((lane & 31) ^ (R & 15));
-    const int d = 32 * (w & 7) + 8 * i + (lane >> 3), cv = (lane & 7) ^ ((d >> 1) & 7);
-    voffs[i] = (uint32_t)d * (uint32_t)ldvt * 2u + 16u * (uint32_t)cv;
-  }
-  // This wave's four copies of K tile `tile` (isk) or V^T tile `tile` into the
-  // ring stage at dst.
-  auto copy_tile = [&](uint32_t dst, bool isk, int tile) {
-    if (!isk) {  // V^T: the tile's columns, 64 halves per 32 keys
-      const uint32_t soff = (uint32_t)tile * kBK * 4u;
-#pragma unroll
-      for (int i = 0; i < 4; i++) sg_lds_copy16(dst + 1024u * i, voffs[i], rv, soff);
-    } else if (tile * kBK + kBK <= S) {  // a whole K tile
-      const uint32_t soff = (uint32_t)(tile * kBK) * (uint32_t)ldk * 2u;
-#pragma unroll
-      for (int i = 0; i < 4; i++) sg_lds_copy16(dst + 1024u * i, kvo[i], rk, soff);
-    } else {  // a sequence's last K tile: rows past S re-read its last key
-      const int kt = tile * kBK;
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int key = min(kt + kkey(i), S - 1);
-        sg_lds_copy16(dst + 1024u * i, kvo[i] + (uint32_t)(key - kkey(i)) * (uint32_t)ldk * 2u, rk, 0u);
-      }
-    }
-  };
-  // Items: the nt K tiles of pass 1, then pass 2's K and V^T tile of every
-  // 32 keys in turn (item nt + 2t: K tile t, nt + 2t + 1: V^T tile t).
-  auto issue = [&](int item) {
-    const int last = 3 * nt - 1;
-    const int src = item < last ? item : last;
-    const uint32_t dst = (uint32_t)(uintptr_t)(lds_ptr)(lds + ((unsigned)item % kRing) * kTileBytes + w * 4096);
-    copy_tile(dst, src < nt || ((src - nt) & 1) == 0, src < nt ? src : (src - nt) >> 1);
-  };
-  issue(0);
-  issue(1);
-  half8_t bqh[kHD / 32], bql[kHD / 32];
-  // The Q prologue's LDS tiles sit in stage 2, which no copy touches before
-  // the first barrier.
-  q_operand<QPRE>(bqh, bql, qh, ql, ldq, qp, qr, qr - r0, head, ln, g4, lane,
-                  reinterpret_cast<float*>(lds + 2 * kTileBytes) + w * (16 * 40));
-
-  auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
-  // ---- pass 1: S^T = K Q^T per tile, kept in registers; row max ----
-  // K fragment (row R = 32 hl + 16 st + ln, chunk 4 ks + g4) at
-  // R * 512 + 16 * ((4 ks + g4) ^ ln) = (xk ^ 64 ks) + 8192 st + 16384 hl.
-  const uint32_t xk = (uint32_t)ln * 512u + 16u * (uint32_t)(g4 ^ (ln & 3)) + 64u * (uint32_t)(ln >> 2);
-  auto scores2 = [&](const unsigned char* kb, f32x4_t& a0, f32x4_t& a1) {
-    auto rd = [&](int st, int ks, half8_t& h, half8_t& l) {
-      const unsigned char* p = kb + (xk ^ (64u * ks)) + 8192 * st;
-      h = *reinterpret_cast<const half8_t*>(p);
-      l = *reinterpret_cast<const half8_t*>(p + 16384);
-    };
-    a0 = f32x4_t{0, 0, 0, 0};
-    a1 = f32x4_t{0, 0, 0, 0};
-    half8_t h0, l0, h1, l1;
-    rd(0, 0, h0, l0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-#pragma unroll
-    for (int ks = 0; ks < kHD / 32; ks++) {
-      rd(1, ks, h1, l1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      a0 = mfma16(h0, bqh[ks], a0);
-      a0 = mfma16(h0, bql[ks], a0);
-      a0 = mfma16(l0, bqh[ks], a0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-      if (ks + 1 < kHD / 32) {
-        rd(0, ks + 1, h0, l0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
-      a1 = mfma16(h1, bqh[ks], a1);
-      a1 = mfma16(h1, bql[ks], a1);
-      a1 = mfma16(l1, bqh[ks], a1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-    }
-  };
-  float m = -INFINITY;
-  for (int t = 0; t < nt; t++) {
-    sg_wait_vmcnt<4>();  // item t landed (item t + 1 may still be in flight)
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    issue(t + 2);
-    // Every wave computes (an inactive wave's results are never stored).
-    f32x4_t a0, a1;
-    scores2(lds + (t % kRing) * kTileBytes, a0, a1);
-    const int kt = t * kBK;
-    if (kt + kBK <= S) {  // keys past S only in a sequence's last tile
-#pragma unroll
-      for (int r = 0; r < 4; r++) m = fmaxf(m, fmaxf(a0[r], a1[r]));
-    } else {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        m = key_of(kt, 0, r) < S ? fmaxf(m, a0[r]) : m;
-        m = key_of(kt, 1, r) < S ? fmaxf(m, a1[r]) : m;
-      }
-    }
-  }
-  // Max of the raw (x64) scores; scaling by the power of two sscale commutes
-  // with max exactly.
-  m = fmaxf(m, __shfl_xor(m, 16));
-  m = fmaxf(m, __shfl_xor(m, 32)) * sscale;
-
-  // ---- pass 2: e = fastExp(s - m), row sums, O^T += V^T P^T ----
-  // V^T fragment (dim 16 mt + ln, chunk g4 hi / 4 + g4 lo) at
-  // (16 mt + ln) * 128 + 16 * (chunk ^ ((ln >> 1) & 7)): xv (+ 64 for lo)
-  // + 2048 mt.
-  const uint32_t xv = (uint32_t)ln * 128u + 16u * (uint32_t)(g4 ^ ((ln >> 1) & 7));
-  f32x4_t o[kHD / 16];
-#pragma unroll
-  for (int mt = 0; mt < kHD / 16; mt++) o[mt] = f32x4_t{0, 0, 0, 0};
-  float lsum = 0.0f;
-  auto pv = [&](const unsigned char* vb, const half8_t& ph, const half8_t& pl) {
-    const unsigned char* p0 = vb + xv;
-    half8_t fr[3][2];  // [buffer][hi, lo]
-    auto rd = [&](int mt, half8_t(&f)[2]) {
-      f[0] = *reinterpret_cast<const half8_t*>(p0 + 2048 * mt);
-      f[1] = *reinterpret_cast<const half8_t*>(vb + ((xv ^ 64u) + 2048u * mt));
-    };
-    rd(0, fr[0]);
-    rd(1, fr[1]);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-#pragma unroll
-    for (int mt = 0; mt < kHD / 16; mt++) {
-      if (mt + 2 < kHD / 16) {
-        rd(mt + 2, fr[(mt + 2) % 3]);
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      }
-      const half8_t(&f)[2] = fr[mt % 3];
-      o[mt] = mfma16(f[0], ph, o[mt]);
-      o[mt] = mfma16(f[0], pl, o[mt]);
-      o[mt] = mfma16(f[1], ph, o[mt]);
-      __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);
-    }
-  };
-  // One tile of pass 2; the key test only in the instance for the last tile
-  // (keys past S occur only there).
-  auto step = [&](int t, auto last) {
-    const int item = nt + 2 * t;
-    sg_wait_vmcnt<4>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    issue(item + 2);
-    f32x4_t a0, a1;
-    scores2(lds + ((unsigned)item % kRing) * kTileBytes, a0, a1);
-    float e[8];  // slots 0..3: keys 4g4+r, slots 4..7: 16+4g4+r
-#pragma unroll
-    for (int st = 0; st < 2; st++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        e[4 * st + r] = sg_fast_exp_nonpos((st ? a1[r] : a0[r]) * sscale - m);
-        if constexpr (decltype(last)::value) e[4 * st + r] = key_of(t * kBK, st, r) < S ? e[4 * st + r] : 0.0f;
-      }
-#pragma unroll
-    for (int k = 0; k < 8; k++) lsum = lsum + e[k];
-    u32x4_t uh, ul;
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        uint32_t h, l;
-        split_pair(e[2 * k], e[2 * k + 1], kPScale, h, l);
-        uh[k] = h;
-        ul[k] = l;
-      }
-    const half8_t ph = __builtin_bit_cast(half8_t, uh), pl = __builtin_bit_cast(half8_t, ul);
-    sg_wait_vmcnt<4>();
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    issue(item + 3);
-    pv(lds + ((unsigned)(item + 1) % kRing) * kTileBytes, ph, pl);
-  };
-  for (int t = 0; t + 1 < nt; t++) step(t, bool_c<false>{});
-  step(nt - 1, bool_c<true>{});
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the re-copies past the last item have landed
-  lsum = lsum + __shfl_xor(lsum, 16);
-  lsum = lsum + __shfl_xor(lsum, 32);
-  const float f = (1.0f / lsum) * kPUnscale;
-
-  // O^T tile mt: lane holds query ln, dims 16mt + 4g4 + r.
-  float mx = 0.0f;
-  if (qvalid) {
-    float* op = out + (int64_t)(r0 + qrow) * ldo + head * kHD + 4 * g4;
-#pragma unroll
-    for (int mt = 0; mt < kHD / 16; mt++) {
-      f32x4_t y;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        y[j] = o[mt][j] * f;
-        mx = fmaxf(mx, fabsf(y[j]));
-      }
-      *reinterpret_cast<f32x4_t*>(op + 16 * mt) = y;
-    }
-  }
-  if (amax) {  // all chunks of a workgroup belong to one sequence
-    mx = sg_wave_max(mx);
-    if (lane == 0) red[w] = mx;
-    __syncthreads();
-    if (tid == 0) {
-      float mm = red[0];
-#pragma unroll
-      for (int i = 1; i < kWaves; i++) mm = fmaxf(mm, red[i]);
-      sg_atomic_max_nonneg(amax + it.seq, mm);
     }
   }
 }
@@ -843,25 +654,26 @@ hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, 
 }
 
 namespace {
-template <bool QPRE, bool RS>
+template <bool QPRE, bool SPILL>
 void launch_attn(dim3 grid, hipStream_t s, const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh,
                  const _Float16* kl, int ldk, const _Float16* vt, int ldvt, float* out, int ldo,
                  const int32_t* seq_off, const int32_t* voff, const sg_item* items, int G, float sscale, float* amax,
-                 const sg_attn_qpre& qp, const sg_attn_qout& qo) {
-  if constexpr (RS)
-    hipLaunchKernelGGL((k_attn_rs<QPRE>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
-                       seq_off, voff, items, G, sscale, amax, qp, qo);
-  else
-    hipLaunchKernelGGL((k_attn_ring<QPRE>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
-                       seq_off, voff, items, G, sscale, amax, qp);
+                 const sg_attn_qpre& qp, const sg_attn_qout& qo, float* spill, int spill_tiles) {
+  hipLaunchKernelGGL((k_attn_rs<QPRE, SPILL>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
+                     seq_off, voff, items, G, sscale, amax, qp, qo, spill, spill_tiles);
 }
 }  // namespace
+
+size_t attention_spill_bytes(int n_items, int HKV, int max_len) {
+  const int tiles = (max_len + kBK - 1) / kBK - kRegTiles;
+  return tiles > 0 && n_items > 0 ? (size_t)n_items * HKV * tiles * kScoreBytes : 0;
+}
 
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
                      const _Float16* vt, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
                      float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre,
-                     const sg_attn_qout* qout) {
+                     const sg_attn_qout* qout, float* spill) {
   if (n_items <= 0) return hipSuccess;
   if (hd != kHD || HKV <= 0 || H % HKV || max_len <= 0) return hipErrorInvalidValue;
   // The quantizing epilogue needs the register-scores kernel, one workgroup per
@@ -871,23 +683,27 @@ hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Flo
     return hipErrorInvalidValue;
   const sg_attn_qout qo = qout ? *qout : sg_attn_qout{nullptr, 0, nullptr};
   if ((ldk | ldvt) & 7 || (ldo & 3)) return hipErrorInvalidValue;
+  const int spill_tiles = (max_len + kBK - 1) / kBK - kRegTiles;
+  if (spill_tiles > 0 && (!spill || (reinterpret_cast<uintptr_t>(spill) & 15))) return hipErrorInvalidValue;
   const float sscale = scale / (kQKScale * kQKScale);
   const dim3 grid(n_items, HKV);
-  const bool rs = max_len <= kAttnRegKeys;
+  sg_attn_qpre qp{};
   if (qpre) {
     if (!qpre->q || !qpre->cos_t || !qpre->sin_t || (qpre->ldq & 3) ||
         (reinterpret_cast<uintptr_t>(qpre->q) & 15) || (reinterpret_cast<uintptr_t>(qpre->w) & 15) ||
         (reinterpret_cast<uintptr_t>(qpre->cos_t) & 15) || (reinterpret_cast<uintptr_t>(qpre->sin_t) & 15))
       return hipErrorInvalidValue;  // float4 loads of Q rows, weights and table rows
-    (rs ? launch_attn<true, true> : launch_attn<true, false>)(grid, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out,
-                                                              ldo, seq_off, voff, items, H / HKV, sscale, amax, *qpre,
-                                                              qo);
-  } else {
-    if (ldq & 7) return hipErrorInvalidValue;
-    (rs ? launch_attn<false, true> : launch_attn<false, false>)(grid, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt,
-                                                                out, ldo, seq_off, voff, items, H / HKV, sscale, amax,
-                                                                sg_attn_qpre{}, qo);
+    qp = *qpre;
+  } else if (ldq & 7) {
+    return hipErrorInvalidValue;
   }
+  using fn = void (*)(dim3, hipStream_t, const _Float16*, const _Float16*, int, const _Float16*, const _Float16*, int,
+                      const _Float16*, int, float*, int, const int32_t*, const int32_t*, const sg_item*, int, float,
+                      float*, const sg_attn_qpre&, const sg_attn_qout&, float*, int);
+  static const fn table[2][2] = {{launch_attn<false, false>, launch_attn<false, true>},
+                                 {launch_attn<true, false>, launch_attn<true, true>}};
+  table[qpre != nullptr][spill_tiles > 0](grid, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo, seq_off, voff, items, H / HKV,
+                               sscale, amax, qp, qo, spill, spill_tiles > 0 ? spill_tiles : 0);
   return hipGetLastError();
 }
 

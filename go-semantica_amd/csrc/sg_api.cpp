@@ -332,6 +332,7 @@ struct Lane {
   DevBuf h, xn, qkv, att, o, g, a8, sx, amax, meta_d, err;
   DevBuf ks, vt;  // attention operands, hi/lo fp16 (K row-major; V^T); Q is split inside the attention kernel
   DevBuf xp;      // exact-order attention: scores / weights [H][T][ldp] (SG_ATTN_EXACT only)
+  DevBuf spill;   // attention scores past the kernel's register tiles (sequences > 512 keys)
   HostBuf meta_h, io_h;
   hipStream_t stream = nullptr;
   hipEvent_t done = nullptr;
@@ -347,7 +348,7 @@ struct Lane {
     return SG_OK;
   }
   ~Lane() {
-    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a8, &sx, &amax, &meta_d, &err, &ks, &vt, &xp}) b->release();
+    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a8, &sx, &amax, &meta_d, &err, &ks, &vt, &xp, &spill}) b->release();
     meta_h.release();
     io_h.release();
     if (done) (void)hipEventDestroy(done);
@@ -561,7 +562,8 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
       SG_LAUNCH(SG_K_ATTENTION, attn_flops,
                 sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, ldvt, att, qd, meta.seq_off,
                                meta.voff, meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd,
-                               m->attn_scale, site(l, 1), meta.max_len, s, &qpre, q_attn ? &qout : nullptr));
+                               m->attn_scale, site(l, 1), meta.max_len, s, &qpre, q_attn ? &qout : nullptr,
+                               w.spill.as<float>()));
     }
     if (tr && tr->att) SG_HIP(tap(tr->att, att, l, qd));
     if (!(q_attn && m->attn_mode != SG_ATTN_EXACT))
@@ -677,7 +679,10 @@ int ensure_workspace(const sg_model* m, Lane& w, const Meta& meta) {
   SG_TRY(w.ks.ensure(2 * sizeof(_Float16) * t * m->kvd));
   SG_TRY(w.vt.ensure(2 * sizeof(_Float16) * (size_t)m->kvd * Tp));
   SG_TRY(w.err.ensure(64));
-  if (m->attn_mode == SG_ATTN_EXACT) SG_TRY(w.xp.ensure(sgk::attention_exact_scratch(T, c.num_heads, meta.max_len)));
+  if (m->attn_mode == SG_ATTN_EXACT)
+    SG_TRY(w.xp.ensure(sgk::attention_exact_scratch(T, c.num_heads, meta.max_len)));
+  else
+    SG_TRY(w.spill.ensure(sgk::attention_spill_bytes(meta.n_items, c.num_kv_heads, meta.max_len)));
   return SG_OK;
 }
 
@@ -1251,7 +1256,8 @@ int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const flo
   const float scale = 1.0f / (float)std::sqrt((double)head_dim);
   // Split operands as the forward's producers write them.
   const size_t T = (size_t)meta.T, qd = (size_t)n_heads * head_dim, kvd = (size_t)n_kv_heads * head_dim;
-  SG_TRY(ctx->split.ensure(2 * sizeof(_Float16) * (T * qd + T * kvd + kvd * (size_t)meta.Tp)));
+  const size_t split_bytes = (2 * sizeof(_Float16) * (T * qd + T * kvd + kvd * (size_t)meta.Tp) + 255) & ~(size_t)255;
+  SG_TRY(ctx->split.ensure(split_bytes + sgk::attention_spill_bytes(meta.n_items, n_kv_heads, meta.max_len)));
   SG_TRY(gemm_scratch_begin(ctx, s));  // after the asynchronous GEMM calls of this context
   _Float16* qs_h = ctx->split.as<_Float16>();
   _Float16* qs_l = qs_h + T * qd;
@@ -1264,7 +1270,8 @@ int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const flo
   SG_HIP(sgk::v_split_t(v, ldkv, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles, n_kv_heads, vt_h, ldvt, s));
   SG_HIP(sgk::attention(qs_h, qs_l, (int)qd, ks_h, ks_l, (int)kvd, vt_h, ldvt, out, (int)qd, meta.seq_off,
                         meta.voff, meta.items, meta.n_items, n_heads, n_kv_heads, head_dim, scale, nullptr,
-                        meta.max_len, s));
+                        meta.max_len, s, nullptr, nullptr,
+                        reinterpret_cast<float*>(ctx->split.as<unsigned char>() + split_bytes)));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;
 }

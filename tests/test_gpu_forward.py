@@ -537,7 +537,7 @@ def test_exact_attention_forward_random_batches(full_gpu, full_oracle, case):
     forward's dispatch boundaries are checked that way over all 24 layers:
     short mixed lengths (register-direct GEMMs with and without the
     MFMA-ahead loop, attention items of one and several workgroups), long
-    sequences next to short ones (the ring attention kernel, 2048 keys),
+    sequences next to short ones (spilled attention scores, 2048 keys),
     hundreds of tiny sequences, single-token sequences (the short-sequence
     fused post-norm quantize), and one 32-row block of several sequences."""
     rng = np.random.default_rng({"short_mixed": 41, "long_mixed": 42, "many_tiny": 43, "singletons": 44,

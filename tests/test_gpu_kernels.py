@@ -467,9 +467,9 @@ def test_qknorm_rope_bit_exact(gpu_ctx, oracle):
 ATTN_REL_TOL = 1e-5
 
 
-# Batches whose longest sequence has at most 512 keys run the kernel that keeps
-# pass 1's scores in registers; a longer one switches the whole launch to the
-# kernel that recomputes them.
+# Batches whose longest sequence has at most 512 keys keep all of pass 1's
+# scores in registers; a longer one switches the whole launch to the variant
+# that spills the scores past 512 keys.
 @pytest.mark.parametrize("lens", [[1, 31, 32, 33, 100, 517], [1, 31, 32, 33, 100, 512]])
 def test_attention_vs_oracle(gpu_ctx, oracle, lens):
     import torch
@@ -488,6 +488,32 @@ def test_attention_vs_oracle(gpu_ctx, oracle, lens):
     for i in range(len(lens)):
         sl = slice(off[i], off[i + 1])
         ref = oracle.attention(q[sl], k[sl], v[sl], 3, 1, 256)
+        assert rel_err(got[sl], ref) < ATTN_REL_TOL, (i, rel_err(got[sl], ref))
+        assert np.max(np.abs(got[sl] - ref)) < 1e-4 * np.max(np.abs(v[sl])), i
+
+
+# Past 512 keys the tiles beyond the register-held ones keep their scores in a
+# global spill buffer (one slot range per workgroup and kv head) and reach pass
+# 2 through the V^T items' copies: the longest sequence (2048 keys, 48 spilled
+# tiles), a sequence ending one key into a tile, and grouped kv heads.
+@pytest.mark.parametrize("lens,heads", [([2048, 700, 1, 513], (3, 1)), ([1000, 40, 545], (4, 2))])
+def test_attention_spilled_scores_vs_oracle(gpu_ctx, oracle, lens, heads):
+    import torch
+    from semantica_gpu import kernels
+    H, HKV = heads
+    rng = np.random.default_rng(32)
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(off[-1])
+    say(f"attention spilled scores lens={lens} heads={heads}")
+    q = (rng.standard_normal((T, H * 256)) * rng.uniform(0.5, 1.5, H * 256)).astype(np.float32)
+    k = (rng.standard_normal((T, HKV * 256)) * rng.uniform(0.5, 1.5, HKV * 256)).astype(np.float32)
+    v = (rng.standard_normal((T, HKV * 256)) * 2).astype(np.float32)
+    out = torch.empty((T, H * 256), dtype=torch.float32, device="cuda")
+    kernels.attention(gpu_ctx, out, dev(q), dev(k), dev(v), H, HKV, 256, off)
+    got = host(out)
+    for i in range(len(lens)):
+        sl = slice(off[i], off[i + 1])
+        ref = oracle.attention(q[sl], k[sl], v[sl], H, HKV, 256)
         assert rel_err(got[sl], ref) < ATTN_REL_TOL, (i, rel_err(got[sl], ref))
         assert np.max(np.abs(got[sl] - ref)) < 1e-4 * np.max(np.abs(v[sl])), i
 
@@ -537,9 +563,10 @@ def test_attention_exact_bit_exact(gpu_ctx, oracle, lens, heads, nonfinite):
         assert clamped > 0
 
 
-def test_attention_register_scores_match_recomputed(gpu_ctx):
+def test_attention_register_scores_match_spilling_launch(gpu_ctx):
     """The same sequences with and without a 600-key companion (which moves the
-    launch from register-held scores to recomputed ones) give identical bits."""
+    launch to the kernel variant that spills scores past 512 keys) give
+    identical bits."""
     import torch
     from semantica_gpu import kernels
     rng = np.random.default_rng(77)
@@ -547,7 +574,7 @@ def test_attention_register_scores_match_recomputed(gpu_ctx):
     long_len = 600
     T0 = sum(lens)
     T = T0 + long_len
-    say(f"attention register vs recomputed scores lens={lens} + [{long_len}]")
+    say(f"attention register-only vs spilling launch lens={lens} + [{long_len}]")
     q = (rng.standard_normal((T, 768)) * rng.uniform(0.5, 1.5, 768)).astype(np.float32)
     k = (rng.standard_normal((T, 256)) * rng.uniform(0.5, 1.5, 256)).astype(np.float32)
     v = (rng.standard_normal((T, 256)) * 2).astype(np.float32)
