@@ -56,6 +56,8 @@ def parse():
                     help="skip the small-batch latency and config-1 GEMM legs (profiles then hold only config-2 steps)")
     ap.add_argument("--search-vectors", type=int, default=1_000_000)
     ap.add_argument("--search-batch", type=int, default=64)
+    ap.add_argument("--config-only", type=int, choices=(3, 4), default=0,
+                    help="run only the config-3 or config-4 leg and print its object (profiling runs)")
     ap.add_argument("--search-only", action="store_true",
                     help="run only the search measurement and print its JSON (for profiling)")
     ap.add_argument("--no-gpu-events", action="store_true",
@@ -262,6 +264,51 @@ def small_batch_latency(model, shapes=((1, 32), (8, 32), (1, 512), (8, 512)), re
     return res
 
 
+def ragged_config_leg(model, which, steps=10, warmup=3):
+    """Config 3 (8 sequences, lengths U[1024, 2048] seed 4, the attention-heavy
+    case: every launch past the 512 keys held in registers) or config 4 (256
+    sequences, log-uniform lengths in [8, 512] seed 1, Matryoshka 256 dims):
+    device-resident forwards timed like the headline, then one instrumented pass
+    (one sequence group) for the attention and GEMM classes.  Same synthetic
+    model and token stream as the headline."""
+    import numpy as np
+    import torch
+    from semantica_gpu import synth
+    if which == 3:
+        lens, out_dim, desc = synth.lengths_uniform(8, 1024, 2048, seed=4), 768, "8 x U[1024, 2048] (seed 4)"
+    else:
+        lens, out_dim, desc = synth.lengths_log_uniform(256, 8, 512, seed=1), 256, \
+            "256 x log-uniform [8, 512] (seed 1), 256 dims"
+    off = synth.offsets_from_lengths(lens)
+    T, n = int(off[-1]), len(lens)
+    toks = torch.from_numpy(synth.token_ids(T, 262144, seed=0)).cuda()
+    out = torch.empty((n, out_dim), dtype=torch.float32, device="cuda")
+    for _ in range(warmup):
+        model.forward_device(toks.data_ptr(), off, out_dim, out.data_ptr())
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        model.forward_device(toks.data_ptr(), off, out_dim, out.data_ptr())
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    model.profile_enable(True)
+    model.forward_device(toks.data_ptr(), off, out_dim, out.data_ptr())
+    torch.cuda.synchronize()
+    prof = model.profile_read()
+    model.profile_enable(False)
+    emb = out.cpu().numpy()
+    assert np.all(np.isfinite(emb)) and np.allclose(np.sum(emb.astype(np.float64) ** 2, axis=1), 1.0, atol=1e-4)
+    res = {"workload": f"config {which}: {desc}, {T} tokens", "steps": steps, "ms_per_step": round(dt * 1e3, 3),
+           "embeddings_per_s": round(n / dt, 2), "tokens_per_s": round(T / dt)}
+    for name in ("attention", "gemm", "gemm_norm"):
+        p = prof.get(name)
+        if p and p["launches"]:
+            rate = p["work"] / (p["ms"] * 1e-3) / 1e12
+            res[f"{name}_one_group_ms"] = round(p["ms"], 3)
+            res[f"{name}_{'TFLOPS' if name == 'attention' else 'TOPS_int8'}"] = round(rate, 2)
+    return res
+
+
 C1_SHAPES = (("Q/O", 768, 768), ("K/V", 256, 768), ("gate/up", 1152, 768), ("down", 768, 1152),
              ("3072x768", 3072, 768), ("768x3072", 768, 3072))
 
@@ -416,6 +463,15 @@ def main():
         print(json.dumps({"search": res}), flush=True)
         return
 
+    if a.config_only:
+        ctx = Context(0)
+        model = Model(ctx, synth.make_model())
+        res = ragged_config_leg(model, a.config_only, steps=a.steps, warmup=a.warmup)
+        model.close()
+        ctx.close()
+        print(json.dumps({f"config{a.config_only}": res}), flush=True)
+        return
+
     B, S = a.batch, a.seq_len
     mdl = synth.make_model()
     toks = synth.token_ids(B * S, mdl.config["vocab_size"], seed=0)
@@ -549,6 +605,8 @@ def main():
         line["hbm_reference"] = hbm_reference_leg(ctx, B * S)
         line["latency"] = small_batch_latency(model)
         line["gemm_c1"] = gemm_c1_leg(ctx)
+        line["config3"] = ragged_config_leg(model, 3)
+        line["config4"] = ragged_config_leg(model, 4)
     model.close()
     if not a.no_search:
         line["tokenizer"] = tokenizer_leg()
