@@ -611,7 +611,7 @@ def test_teacher_forced_config4_slice(full_gpu, full_oracle):
 
 
 def test_teacher_forced_long_sequences(gpu_ctx, oracle):
-    """Config 3's lengths past 512 keys (the recomputing attention kernel), 4 layers."""
+    """Config 3's lengths past 512 keys (attention with the scores past 512 keys spilled), 4 layers."""
     from semantica_gpu import Model, synth
     cfg = dict(synth.EMBEDDINGGEMMA_300M, num_layers=4, vocab_size=8192)
     mdl = synth.make_model(cfg, seed_weights=9)
