@@ -676,18 +676,25 @@ constexpr int kResRows = 8192;
 // take the MFMA-ahead loop with a 3-stage ring (at M = 32: 4.8 vs 5.4 us for
 // K = 768; at M = 2048, N = 256: 5.5 vs 6.0 us); larger grids keep the plain
 // 2-stage loop, whose lower register count gives more waves per SIMD (QKV at
-// M = 2048: 10.3 vs 10.8 us).
+// M = 2048: 10.3 vs 10.8 us).  With cold weights (the forward: every layer's
+// weights were last read a whole forward earlier, so their loads come from
+// MALL or HBM) those small grids take a 6-stage ring instead, which keeps
+// twice the blocks' loads in flight per wave: a 1 x 32 forward 2.24 -> 2.05
+// ms, 1 x 512 3.52 -> 3.36 ms.  With the weights in L2 (one weight called
+// again and again) the 3-stage ring is faster (M = 2048: Q/O 7.5 vs 8.2 us).
 constexpr int kPipeTiles = 384;
 inline int rd_tiles(int M, int N, int BM, int BN) { return ((M + BM - 1) / BM) * ((N + BN - 1) / BN); }
 
 hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
-                   int32_t* sums, int M, int N, int K, hipStream_t s) {
+                   int32_t* sums, int M, int N, int K, hipStream_t s, bool cold_weights) {
   if (M <= 0 || N <= 0) return hipSuccess;
   if (K <= 0 || K % 32) return hipErrorInvalidValue;
   if (sums) return launch_rd<1, 1, 1, 1, true>(A, a_rows, W, St, row_scale, Y, sums, M, N, K, s);
   if (M < kRdRows) {
     if (rd_tiles(M, N, 64, 64) <= kPipeTiles)
-      return launch_rd<2, 2, 1, 1, false, false, 3, true>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
+      return cold_weights
+                 ? launch_rd<2, 2, 1, 1, false, false, 6, true>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s)
+                 : launch_rd<2, 2, 1, 1, false, false, 3, true>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
     return launch_rd<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
   }
   if (M < kLds8Rows) return launch_lds<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
@@ -695,13 +702,16 @@ hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St
 }
 
 hipError_t gemm_q8_gelu(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale,
-                        float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s) {
+                        float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s,
+                        bool cold_weights) {
   if (M <= 0 || Nh <= 0) return hipSuccess;
   if (K <= 0 || K % 32 || Nh % 32) return hipErrorInvalidValue;
   if (amax && !row_seq) return hipErrorInvalidValue;
   if (M < kGeluLdsRows && rd_tiles(M, 2 * Nh, 128, 64) <= kPipeTiles)
-    return launch_rd<4, 1, 1, 2, false, true, 3, true>(A, a_rows, W, St, row_scale, G, nullptr, M, 2 * Nh, K, s,
-                                                       row_seq, amax);
+    return cold_weights ? launch_rd<4, 1, 1, 2, false, true, 6, true>(A, a_rows, W, St, row_scale, G, nullptr, M,
+                                                                      2 * Nh, K, s, row_seq, amax)
+                        : launch_rd<4, 1, 1, 2, false, true, 3, true>(A, a_rows, W, St, row_scale, G, nullptr, M,
+                                                                      2 * Nh, K, s, row_seq, amax);
   if (M < kGeluLdsRows)
     return launch_rd<4, 1, 1, 2, false, true>(A, a_rows, W, St, row_scale, G, nullptr, M, 2 * Nh, K, s, row_seq,
                                               amax);

@@ -511,7 +511,7 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
                           s);
   };
   auto gemm = [&](const int8_t* w8, const float* st, float* y, int N, int K) {
-    return sgk::gemm_q8(a8, ar, w8, st, sx, y, nullptr, T, N, K, s);
+    return sgk::gemm_q8(a8, ar, w8, st, sx, y, nullptr, T, N, K, s, true);
   };
 
   if (l0 == 0) {
@@ -585,7 +585,7 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
     if (!(q_rows && !sgk::gemm_res_norm_fused(T, d, ly.post_attn, ly.ffn_norm)))
       SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.ffn_norm, site(l, 2)));
     SG_LAUNCH(SG_K_GEMM, gemm_ops(2 * ff, d),
-              sgk::gemm_q8_gelu(a8, ar, ly.wgu, ly.sgu, sx, g, T, ff, d, meta.row_seq, site(l, 3), s));
+              sgk::gemm_q8_gelu(a8, ar, ly.wgu, ly.sgu, sx, g, T, ff, d, meta.row_seq, site(l, 3), s, true));
     SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(ff), quant(g, ff, site(l, 3)));
     const bool last = l + 1 == L;
     const float* w_next = last ? m->out_norm : m->layers[l + 1].attn_norm;

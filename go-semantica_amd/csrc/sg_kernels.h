@@ -118,15 +118,18 @@ hipError_t stream_probe(int kind, const float* a, const float* b, void* c, int64
 // Y[M][N] = (sum_b float(P_b) * St[b][n]) * row_scale[m] with A int8 [M][K]
 // block-major [K/32][a_rows][32] (a_rows >= gemm_pad_rows(M)), W int8 [N][K]
 // block-major [K/32][N][32], St [K/32][N].  sums != null additionally dumps
-// the exact block sums int32 [M][N][K/32].
+// the exact block sums int32 [M][N][K/32].  cold_weights: W is not expected
+// in L2 (the forward, one layer after another), which selects deeper load
+// pipelines for small grids; the results are the same either way.
 hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
-                   int32_t* sums, int M, int N, int K, hipStream_t s);
+                   int32_t* sums, int M, int N, int K, hipStream_t s, bool cold_weights = false);
 // FFN gate/up GEMM with GELUQuick(gate) * up in the epilogue: W holds 2*Nh rows,
 // gate and up interleaved in groups of kGeluGroup (see repack_q8_0's grouping);
 // G[M][Nh] is bit-identical to the unfused GEMMs + gelu_mul; amax (optional,
 // with row_seq) collects the sequences' max|g|.
 hipError_t gemm_q8_gelu(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale,
-                        float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s);
+                        float* G, int M, int Nh, int K, const int32_t* row_seq, float* amax, hipStream_t s,
+                        bool cold_weights = false);
 // gemm_q8 followed by post_res_norm on its output (N = d): o = the GEMM, then
 // h = RMSNorm(o; w_post) + h, xn = RMSNorm(h; w_next) (stored when xn !=
 // null), amax (optional, with row_seq) per sequence of max|xn|.  For N = 768

@@ -557,6 +557,26 @@ def test_exact_attention_forward_random_batches(full_gpu, full_oracle, case):
     _exact_forward(full_gpu, full_oracle, toks, off, 768, f"random batch {case}")
 
 
+@pytest.mark.parametrize("interm", [1088, 1120])
+def test_exact_attention_forward_ragged_k_blocks(gpu_ctx, oracle, interm):
+    """Small batches run the forward's GEMMs on the register-direct kernel with
+    a 6-stage load ring (cold weights); the model's own widths (24 and 36
+    K-blocks) fill its rounds exactly, so FFN widths of 34 and 35 blocks leave
+    partial last rounds of 4 and 5 blocks in the down GEMM.  Two layers, exact
+    attention, bit-identical to the oracle's block-serial forward."""
+    from semantica_gpu import Model, synth
+    cfg = dict(synth.EMBEDDINGGEMMA_300M, num_layers=2, vocab_size=4096, interm_dim=interm)
+    mdl = synth.make_model(cfg, seed_weights=13)
+    m = Model(gpu_ctx, mdl)
+    try:
+        for lens in ([32], [7, 19, 3, 40]):
+            off = synth.offsets_from_lengths(lens)
+            toks = synth.token_ids(int(off[-1]), 4096, seed=3)
+            _exact_forward(m, oracle.OracleModel(mdl), toks, off, 768, f"ffn {interm} lens {lens}", threads=4)
+    finally:
+        m.close()
+
+
 def test_exact_attention_forward_config4(full_gpu, full_oracle):
     """Config 4 at full size: 256 log-uniform lengths in [8, 512] (seed 1),
     Matryoshka dim 256, 24 layers, two sequence groups on two streams, exact
