@@ -201,7 +201,8 @@ __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bq
 
 constexpr int kTileBytes = 32 * 1024;  // one K or V^T tile, hi and lo halves
 constexpr int kRing = 3;               // tile stages in LDS
-constexpr int kScoreBytes = kWaves * 2048;  // one tile's scores, 8 floats per lane and wave
+constexpr int kScoreBytes = sgk::kAttnSpillTileBytes;  // one tile's scores, 8 floats per lane and wave
+static_assert(kScoreBytes == kWaves * 2048, "spill tile layout");
 
 // Two passes over a sequence's 32-key tiles: pass 1 keeps each lane's scaled
 // scores in registers (8 per tile, 128 VGPRs for the first kRegTiles tiles)
@@ -231,8 +232,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
     const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq, const _Float16* __restrict__ kh,
     const _Float16* __restrict__ kl, int ldk, const _Float16* __restrict__ vt, int ldvt, float* __restrict__ out,
     int ldo, const int32_t* __restrict__ seq_off, const int32_t* __restrict__ voff, const sg_item* __restrict__ items,
-    int G, float sscale, float* __restrict__ amax, sg_attn_qpre qp, sg_attn_qout qo, float* __restrict__ spill,
-    int spill_tiles) {
+    int G, float sscale, float* __restrict__ amax, sg_attn_qpre qp, sg_attn_qout qo, sg_attn_spill sp) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kRing * kTileBytes];
   __shared__ __attribute__((aligned(16))) unsigned char slds[SPILL ? kRing * kScoreBytes : 16];
   __shared__ float red[kWaves];
@@ -300,12 +300,16 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
       }
     }
   };
-  // SPILL: this workgroup's spilled scores, spill_tiles tiles of kScoreBytes
-  // (wave w's 2 KB at w * 2048: lane l's keys 4g4 + r at 16 l, 16 + 4g4 + r at
-  // 1024 + 16 l).  V^T item nt + t - 1 also carries tile t's scores when
-  // t >= kRegTiles, two more copies per wave into the item's score stage.
-  float* const wspill = SPILL ? spill + (size_t)(blockIdx.y * gridDim.x + blockIdx.x) * spill_tiles * (kScoreBytes / 4)
-                              : nullptr;
+  // SPILL: this workgroup's spilled scores, nt - kRegTiles tiles of
+  // kScoreBytes (wave w's 2 KB at w * 2048: lane l's keys 4g4 + r at 16 l,
+  // 16 + 4g4 + r at 1024 + 16 l).  V^T item nt + t - 1 also carries tile t's
+  // scores when t >= kRegTiles, two more copies per wave into the item's
+  // score stage.
+  float* const wspill =
+      SPILL && nt > kRegTiles
+          ? sp.buf + ((size_t)kvh * sp.total + sp.off[it.seq] + (size_t)(it.c0 / kWaves) * (nt - kRegTiles)) *
+                         (kScoreBytes / 4)
+          : nullptr;
   const i32x4_t rsp = sg_raw_rsrc(wspill);
   const int last = 2 * nt - 1;
   auto carries = [&](int src) { return SPILL && src >= nt + kRegTiles - 1 && src < last; };
@@ -658,22 +662,17 @@ template <bool QPRE, bool SPILL>
 void launch_attn(dim3 grid, hipStream_t s, const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh,
                  const _Float16* kl, int ldk, const _Float16* vt, int ldvt, float* out, int ldo,
                  const int32_t* seq_off, const int32_t* voff, const sg_item* items, int G, float sscale, float* amax,
-                 const sg_attn_qpre& qp, const sg_attn_qout& qo, float* spill, int spill_tiles) {
+                 const sg_attn_qpre& qp, const sg_attn_qout& qo, const sg_attn_spill& sp) {
   hipLaunchKernelGGL((k_attn_rs<QPRE, SPILL>), grid, dim3(kNT), 0, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo,
-                     seq_off, voff, items, G, sscale, amax, qp, qo, spill, spill_tiles);
+                     seq_off, voff, items, G, sscale, amax, qp, qo, sp);
 }
 }  // namespace
-
-size_t attention_spill_bytes(int n_items, int HKV, int max_len) {
-  const int tiles = (max_len + kBK - 1) / kBK - kRegTiles;
-  return tiles > 0 && n_items > 0 ? (size_t)n_items * HKV * tiles * kScoreBytes : 0;
-}
 
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
                      const _Float16* vt, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
                      float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre,
-                     const sg_attn_qout* qout, float* spill) {
+                     const sg_attn_qout* qout, const sg_attn_spill* spill) {
   if (n_items <= 0) return hipSuccess;
   if (hd != kHD || HKV <= 0 || H % HKV || max_len <= 0) return hipErrorInvalidValue;
   // The quantizing epilogue needs the register-scores kernel, one workgroup per
@@ -683,8 +682,12 @@ hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Flo
     return hipErrorInvalidValue;
   const sg_attn_qout qo = qout ? *qout : sg_attn_qout{nullptr, 0, nullptr};
   if ((ldk | ldvt) & 7 || (ldo & 3)) return hipErrorInvalidValue;
-  const int spill_tiles = (max_len + kBK - 1) / kBK - kRegTiles;
-  if (spill_tiles > 0 && (!spill || (reinterpret_cast<uintptr_t>(spill) & 15))) return hipErrorInvalidValue;
+  static_assert(kBK == 32 && kRegTiles == sgk::kAttnRegKeys / 32, "attention_spill_tiles");
+  const bool spills = attention_spill_tiles(max_len) > 0;
+  if (spills && (!spill || !spill->buf || !spill->off || spill->total <= 0 ||
+                 (reinterpret_cast<uintptr_t>(spill->buf) & 15)))
+    return hipErrorInvalidValue;
+  const sg_attn_spill sp = spills ? *spill : sg_attn_spill{nullptr, nullptr, 0};
   const float sscale = scale / (kQKScale * kQKScale);
   const dim3 grid(n_items, HKV);
   sg_attn_qpre qp{};
@@ -699,11 +702,11 @@ hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Flo
   }
   using fn = void (*)(dim3, hipStream_t, const _Float16*, const _Float16*, int, const _Float16*, const _Float16*, int,
                       const _Float16*, int, float*, int, const int32_t*, const int32_t*, const sg_item*, int, float,
-                      float*, const sg_attn_qpre&, const sg_attn_qout&, float*, int);
+                      float*, const sg_attn_qpre&, const sg_attn_qout&, const sg_attn_spill&);
   static const fn table[2][2] = {{launch_attn<false, false>, launch_attn<false, true>},
                                  {launch_attn<true, false>, launch_attn<true, true>}};
-  table[qpre != nullptr][spill_tiles > 0](grid, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo, seq_off, voff, items, H / HKV,
-                               sscale, amax, qp, qo, spill, spill_tiles > 0 ? spill_tiles : 0);
+  table[qpre != nullptr][spills](grid, s, qh, ql, ldq, kh, kl, ldk, vt, ldvt, out, ldo, seq_off, voff, items, H / HKV,
+                                 sscale, amax, qp, qo, sp);
   return hipGetLastError();
 }
 

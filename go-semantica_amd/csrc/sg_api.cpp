@@ -69,6 +69,8 @@ struct Meta {
   int32_t* voff = nullptr;   // [n_seq + 1] V^T column of each sequence
   sg_item* items = nullptr;  // attention workgroups (sequence, first chunk)
   sg_item* vtiles = nullptr; // V^T split tiles (sequence, first key)
+  int32_t* spill_off = nullptr;  // [n_seq] first attention spill tile of each sequence
+  int spill_total = 0;           // attention spill tiles per kv head
 };
 
 // Attention workgroups of one sequence: G*ceil(S/16) chunks, kAttnChunks each.
@@ -77,7 +79,8 @@ int seq_groups(int S, int G) {
   return (chunks + sgk::kAttnChunks - 1) / sgk::kAttnChunks;
 }
 
-// Fills `host` with [row_seq | row_pos | seq_off | voff | items | vtiles] and
+// Fills `host` with [row_seq | row_pos | seq_off | voff | items | vtiles |
+// spill_off] and
 // copies it to `dev` on stream s, asynchronously: kernels launched on s after
 // this see the metadata, and the next stage_meta waits for the copy before it
 // rewrites `host`.
@@ -92,12 +95,16 @@ int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev,
   constexpr int kXcd = 8;
   const int T = off[n_seq];
   int n_items = 0, n_vt = 0;
+  int64_t n_spill = 0;
   for (int i = 0; i < n_seq; i++) {
-    n_items += seq_groups(off[i + 1] - off[i], G);
-    n_vt += (off[i + 1] - off[i] + 31) / 32;
+    const int S = off[i + 1] - off[i];
+    n_items += seq_groups(S, G);
+    n_vt += (S + 31) / 32;
+    n_spill += (int64_t)seq_groups(S, G) * sgk::attention_spill_tiles(S);
   }
+  if (n_spill > INT32_MAX) return fail(SG_ERR_INVALID, "batch too large for the attention spill layout");
   const size_t bytes = sizeof(int32_t) * ((size_t)2 * T + 2 * (n_seq + 1)) +
-                       sizeof(sg_item) * ((size_t)n_items + n_vt) + 64;
+                       sizeof(sg_item) * ((size_t)n_items + n_vt) + sizeof(int32_t) * (size_t)n_seq + 64;
   SG_TRY(host.ensure(bytes));
   SG_TRY(dev.ensure(bytes));
   int32_t* h = host.as<int32_t>();
@@ -107,7 +114,8 @@ int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev,
   int32_t* vo = so + n_seq + 1;
   sg_item* it = reinterpret_cast<sg_item*>(vo + n_seq + 1);
   sg_item* vt = it + n_items;
-  int nv = 0;
+  int32_t* sp = reinterpret_cast<int32_t*>(vt + n_vt);
+  int nv = 0, ns = 0;
   vo[0] = 0;
   for (int i = 0; i < n_seq; i++) {
     const int S = off[i + 1] - off[i];
@@ -118,6 +126,8 @@ int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev,
       rp[r] = r - off[i];
     }
     for (int k0 = 0; k0 < S; k0 += 32) vt[nv++] = sg_item{i, k0};
+    sp[i] = ns;
+    ns += seq_groups(S, G) * sgk::attention_spill_tiles(S);
   }
   so[n_seq] = off[n_seq];
   {
@@ -170,6 +180,8 @@ int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev,
   m.voff = d + 2 * T + n_seq + 1;
   m.items = reinterpret_cast<sg_item*>(d + 2 * T + 2 * (n_seq + 1));
   m.vtiles = m.items + n_items;
+  m.spill_off = reinterpret_cast<int32_t*>(m.vtiles + n_vt);
+  m.spill_total = ns;
   return SG_OK;
 }
 
@@ -559,11 +571,12 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
                              vt_h, ldvt, s));
       const sg_attn_qpre qpre{qkv, nqkv, ly.q_norm, m->cos_t, m->sin_t, eps};
       const sg_attn_qout qout{a8, ar, sx};
+      const sg_attn_spill spill{w.spill.as<float>(), meta.spill_off, meta.spill_total};
       SG_LAUNCH(SG_K_ATTENTION, attn_flops,
                 sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, ldvt, att, qd, meta.seq_off,
                                meta.voff, meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd,
                                m->attn_scale, site(l, 1), meta.max_len, s, &qpre, q_attn ? &qout : nullptr,
-                               w.spill.as<float>()));
+                               &spill));
     }
     if (tr && tr->att) SG_HIP(tap(tr->att, att, l, qd));
     if (!(q_attn && m->attn_mode != SG_ATTN_EXACT))
@@ -682,7 +695,7 @@ int ensure_workspace(const sg_model* m, Lane& w, const Meta& meta) {
   if (m->attn_mode == SG_ATTN_EXACT)
     SG_TRY(w.xp.ensure(sgk::attention_exact_scratch(T, c.num_heads, meta.max_len)));
   else
-    SG_TRY(w.spill.ensure(sgk::attention_spill_bytes(meta.n_items, c.num_kv_heads, meta.max_len)));
+    SG_TRY(w.spill.ensure((size_t)c.num_kv_heads * meta.spill_total * sgk::kAttnSpillTileBytes));
   return SG_OK;
 }
 
@@ -1257,7 +1270,7 @@ int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const flo
   // Split operands as the forward's producers write them.
   const size_t T = (size_t)meta.T, qd = (size_t)n_heads * head_dim, kvd = (size_t)n_kv_heads * head_dim;
   const size_t split_bytes = (2 * sizeof(_Float16) * (T * qd + T * kvd + kvd * (size_t)meta.Tp) + 255) & ~(size_t)255;
-  SG_TRY(ctx->split.ensure(split_bytes + sgk::attention_spill_bytes(meta.n_items, n_kv_heads, meta.max_len)));
+  SG_TRY(ctx->split.ensure(split_bytes + (size_t)n_kv_heads * meta.spill_total * sgk::kAttnSpillTileBytes));
   SG_TRY(gemm_scratch_begin(ctx, s));  // after the asynchronous GEMM calls of this context
   _Float16* qs_h = ctx->split.as<_Float16>();
   _Float16* qs_l = qs_h + T * qd;
@@ -1268,10 +1281,11 @@ int sg_attention(sg_ctx* ctx, float* out, const float* q, int32_t ldq, const flo
   SG_HIP(sgk::split_rows(q, ldq, meta.T, (int)qd, sgk::kAttnQKScale, qs_h, qs_l, (int)qd, s));
   SG_HIP(sgk::split_rows(k, ldkv, meta.T, (int)kvd, sgk::kAttnQKScale, ks_h, ks_l, (int)kvd, s));
   SG_HIP(sgk::v_split_t(v, ldkv, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles, n_kv_heads, vt_h, ldvt, s));
+  const sg_attn_spill spill{reinterpret_cast<float*>(ctx->split.as<unsigned char>() + split_bytes), meta.spill_off,
+                            meta.spill_total};
   SG_HIP(sgk::attention(qs_h, qs_l, (int)qd, ks_h, ks_l, (int)kvd, vt_h, ldvt, out, (int)qd, meta.seq_off,
                         meta.voff, meta.items, meta.n_items, n_heads, n_kv_heads, head_dim, scale, nullptr,
-                        meta.max_len, s, nullptr, nullptr,
-                        reinterpret_cast<float*>(ctx->split.as<unsigned char>() + split_bytes)));
+                        meta.max_len, s, nullptr, nullptr, &spill));
   SG_HIP(hipStreamSynchronize(s));
   return SG_OK;
 }

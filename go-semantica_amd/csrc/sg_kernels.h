@@ -32,6 +32,16 @@ struct sg_attn_qout {
   float* row_scale;
 };
 
+// Where attention() keeps the scores of the tiles past its register-held ones
+// (sequences longer than sgk::kAttnRegKeys keys): per kv head, `total` tiles of
+// sgk::kAttnSpillTileBytes at buf (16-byte aligned); sequence i's workgroups
+// at tile off[i] + (c0 / sgk::kAttnChunks) * sgk::attention_spill_tiles(S_i).
+struct sg_attn_spill {
+  float* buf;
+  const int32_t* off;
+  int total;
+};
+
 namespace sgk {
 
 // GEMM operands are block-major int8 [K/32][rows][32]; activation buffers hold
@@ -171,17 +181,21 @@ hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, 
 // qpre != null: Q is taken from qpre (fp32, normed and rotated in the kernel
 // exactly as qknorm_rope does) and qh/ql/ldq are ignored.  max_len: the
 // longest sequence of the launch.  Pass 1's scores stay in registers up to
-// kAttnRegKeys keys; a longer sequence keeps the rest in spill
-// (attention_spill_bytes, 16-byte aligned; required when max_len exceeds
-// kAttnRegKeys).  A sequence gives the same bits whatever the launch's max_len.
+// kAttnRegKeys keys; a longer sequence keeps the rest in spill (required
+// when max_len exceeds kAttnRegKeys).  A sequence gives the same bits
+// whatever the launch's max_len.
 hipError_t attention(const _Float16* qh, const _Float16* ql, int ldq, const _Float16* kh, const _Float16* kl, int ldk,
                      const _Float16* vt, int ldvt, float* out, int ldo, const int32_t* seq_off,
                      const int32_t* voff, const sg_item* items, int n_items, int H, int HKV, int hd, float scale,
                      float* amax, int max_len, hipStream_t s, const sg_attn_qpre* qpre = nullptr,
-                     const sg_attn_qout* qout = nullptr, float* spill = nullptr);
-// Bytes of attention()'s spill buffer for n_items workgroups of HKV kv heads
-// (0 when max_len <= kAttnRegKeys).
-size_t attention_spill_bytes(int n_items, int HKV, int max_len);
+                     const sg_attn_qout* qout = nullptr, const sg_attn_spill* spill = nullptr);
+// Score tiles a sequence of S keys spills per attention workgroup (one 32-key
+// tile of one workgroup: kAttnSpillTileBytes).
+constexpr int kAttnSpillTileBytes = kAttnChunks * 2048;
+inline int attention_spill_tiles(int S) {
+  const int t = (S + 31) / 32 - kAttnRegKeys / 32;
+  return t > 0 ? t : 0;
+}
 
 // ---- attention in the reference's float32 order (k_attn_exact.hip) ----
 // out[T][ldo] (head h at h*hd) from q[T][ldq], k/v[T][ldkv] (kv head h / (H/HKV)),

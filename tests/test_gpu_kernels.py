@@ -493,10 +493,12 @@ def test_attention_vs_oracle(gpu_ctx, oracle, lens):
 
 
 # Past 512 keys the tiles beyond the register-held ones keep their scores in a
-# global spill buffer (one slot range per workgroup and kv head) and reach pass
-# 2 through the V^T items' copies: the longest sequence (2048 keys, 48 spilled
-# tiles), a sequence ending one key into a tile, and grouped kv heads.
-@pytest.mark.parametrize("lens,heads", [([2048, 700, 1, 513], (3, 1)), ([1000, 40, 545], (4, 2))])
+# global spill buffer (slots only for the workgroups of sequences that long, per
+# kv head) and reach pass 2 through the V^T items' copies: the longest sequence
+# (2048 keys, 48 spilled tiles), a sequence ending one key into a tile, grouped
+# kv heads, and long sequences among many short ones.
+@pytest.mark.parametrize("lens,heads", [([2048, 700, 1, 513], (3, 1)), ([1000, 40, 545], (4, 2)),
+                                        ([33] * 30 + [1500] + [7] * 20 + [600], (3, 1))])
 def test_attention_spilled_scores_vs_oracle(gpu_ctx, oracle, lens, heads):
     import torch
     from semantica_gpu import kernels
