@@ -562,7 +562,7 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
         uint32_t u = 0;
 #pragma unroll
         for (int j = 0; j < 4; j++)
-          u |= (uint32_t)(uint8_t)(int8_t)(int)sg_quant_code(o[mt][j] * f, inv) << (8 * j);
+          u |= (uint32_t)(uint8_t)(int8_t)(int)sg_quant_code_nb(o[mt][j] * f, inv) << (8 * j);
         *reinterpret_cast<uint32_t*>(qo.q8 + ((int64_t)(col >> 5) * qo.a_rows + row) * 32 + (col & 31)) = u;
       }
     }

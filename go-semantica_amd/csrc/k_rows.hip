@@ -17,6 +17,7 @@ namespace {
 constexpr int kRowsPerBlock = 32;  // 256 threads, 8 lanes per row
 static_assert(kRowsPerBlock == sgk::kRowKernelRows, "row kernels' workgroup rows");
 constexpr int kThreads = 256;
+constexpr int kQuantNbRows = 8192;  // the quantizers' branch-free form below this many rows
 
 __device__ __forceinline__ uint16_t rd_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
@@ -212,8 +213,9 @@ __global__ __launch_bounds__(kThreads) void k_quantize(const float* __restrict__
 // when they folded max|xn| into amax (so every value, and the scale, is the
 // one the unfused path quantizes), then quantized as k_quantize does
 // (model_int8.go:194-199 / :216-221: RMSNorm, then QuantizeSymmetricINT8 of
-// the normed sequence).  Saves writing xn and reading it back.
-template <int NC>
+// the normed sequence).  Saves writing xn and reading it back.  NB: the
+// branch-free codes, for small launches.
+template <int NC, bool NB>
 __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restrict__ h, const float* __restrict__ w,
                                                             float eps, int T, const int32_t* __restrict__ row_seq,
                                                             const float* __restrict__ amax,
@@ -247,7 +249,7 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
   for (int c = 0; c < NC; c++) {
     float cv[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) cv[t] = sg_quant_code(x[c][t], inv);
+    for (int t = 0; t < 4; t++) cv[t] = NB ? sg_quant_code_nb(x[c][t], inv) : sg_quant_code(x[c][t], inv);
     store_codes4(qr + (int64_t)c * a_rows * 32, cv);
   }
 }
@@ -255,8 +257,9 @@ __global__ __launch_bounds__(kThreads) void k_norm_quantize(const float* __restr
 // The GEMM-operand form of k_quantize on the float4 row layout: an 8-lane
 // group per row, lane j handling elements 32c + 4j .. + 3 of every chunk c
 // (chunk c is K-block c), so a wave's stores cover 8 consecutive rows' 64-byte
-// block pieces: 512 contiguous bytes per instruction.
-template <int NC>
+// block pieces: 512 contiguous bytes per instruction.  NB: the branch-free
+// codes, for small launches (latency-bound rather than bandwidth-bound).
+template <int NC, bool NB>
 __global__ __launch_bounds__(kThreads) void k_quantize_blocked(const float* __restrict__ x, int ldx, int rows,
                                                                const int32_t* __restrict__ row_seq,
                                                                const float* __restrict__ amax,
@@ -281,7 +284,7 @@ __global__ __launch_bounds__(kThreads) void k_quantize_blocked(const float* __re
   for (int c = 0; c < NC; c++) {
     float cv[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) cv[t] = sg_quant_code(v[c][t], inv);
+    for (int t = 0; t < 4; t++) cv[t] = NB ? sg_quant_code_nb(v[c][t], inv) : sg_quant_code(v[c][t], inv);
     store_codes4(qr + (int64_t)c * a_rows * 32, cv);
   }
 }
@@ -412,7 +415,7 @@ __global__ __launch_bounds__(kThreads) void k_post_res_norm_q(const float* __res
   for (int c = 0; c < NC; c++) {
     float cv[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) cv[t] = sg_quant_code(x[c][t], inv);
+    for (int t = 0; t < 4; t++) cv[t] = sg_quant_code_nb(x[c][t], inv);
     store_codes4(qr + (int64_t)c * a_rows * 32, cv);
   }
 }
@@ -725,11 +728,17 @@ hipError_t quantize(const float* x, int ldx, int rows, int cols, const int32_t* 
   if (q8 && (cols % 32 || a_rows < rows)) return hipErrorInvalidValue;
   if (q8 && (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
     const unsigned nb = blocks_for(rows, kRowsPerBlock);
+    // At most one round of workgroups: latency-bound, the branch-free codes.
+    const bool small = rows < kQuantNbRows;
     switch (cols) {  // the widths the forward quantizes: attention output, hidden, FFN
 #define SG_QB(C)                                                                                                   \
   case C:                                                                                                          \
-    hipLaunchKernelGGL((k_quantize_blocked<C / 32>), dim3(nb), dim3(kThreads), 0, s, x, ldx, rows, row_seq, amax, \
-                       q8, a_rows, row_scale);                                                                     \
+    if (small)                                                                                                     \
+      hipLaunchKernelGGL((k_quantize_blocked<C / 32, true>), dim3(nb), dim3(kThreads), 0, s, x, ldx, rows, row_seq, \
+                         amax, q8, a_rows, row_scale);                                                             \
+    else                                                                                                           \
+      hipLaunchKernelGGL((k_quantize_blocked<C / 32, false>), dim3(nb), dim3(kThreads), 0, s, x, ldx, rows,        \
+                         row_seq, amax, q8, a_rows, row_scale);                                                    \
     return hipGetLastError();
       SG_QB(256) SG_QB(512) SG_QB(768) SG_QB(1024) SG_QB(1152)
 #undef SG_QB
@@ -746,9 +755,15 @@ hipError_t norm_quantize(const float* h, const float* w, float eps, int T, int d
                          const float* amax, int8_t* q8, int a_rows, float* row_scale, hipStream_t s) {
   if (T <= 0) return hipSuccess;
   if (a_rows < T) return hipErrorInvalidValue;
-  SG_DISPATCH_NPL(d, NPL,
-                  hipLaunchKernelGGL((k_norm_quantize<NPL / 4>), dim3(blocks_for(T, kRowsPerBlock)), dim3(kThreads),
-                                     0, s, h, w, eps, T, row_seq, amax, q8, a_rows, row_scale));
+  if (T < kQuantNbRows) {
+    SG_DISPATCH_NPL(d, NPL,
+                    hipLaunchKernelGGL((k_norm_quantize<NPL / 4, true>), dim3(blocks_for(T, kRowsPerBlock)),
+                                       dim3(kThreads), 0, s, h, w, eps, T, row_seq, amax, q8, a_rows, row_scale));
+  } else {
+    SG_DISPATCH_NPL(d, NPL,
+                    hipLaunchKernelGGL((k_norm_quantize<NPL / 4, false>), dim3(blocks_for(T, kRowsPerBlock)),
+                                       dim3(kThreads), 0, s, h, w, eps, T, row_seq, amax, q8, a_rows, row_scale));
+  }
   return hipGetLastError();
 }
 
