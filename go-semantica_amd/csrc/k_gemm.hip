@@ -325,6 +325,167 @@ __global__ __launch_bounds__(WM* WN* SG_WAVE, 2) void k_gemm_q8_rd(
                                   row_seq, amax);
 }
 
+// Tiny-M kernel (a few 16-row groups: the serving batches of one or a few
+// short texts).  The register-direct tiles above give a wave 32 rows x 32
+// columns, so at M = 32 half of a 64-row tile's waves (three quarters of the
+// GELU kernel's 128-row tile) compute padding rows, and each wave's 24 blocks
+// x 32 outputs per lane of subtractions and FMAs form a long VALU stream on a
+// SIMD with nothing else to run.  Here a wave owns 16 rows x 16 columns
+// (v_mfma_i32_16x16x32_i8: 4 outputs per lane, 8 VALU instructions per
+// block), a workgroup 4 waves side by side along N (16 rows x 64 columns), so
+// the same work is spread over four times the waves.  Operand fragments:
+// lane l holds row (or weight column) l % 16, bytes 8 (l / 16) .. + 7 of the
+// 32-byte block, the same assignment for A and W; the result's lane l holds
+// rows 4 (l / 16) .. + 3 of column l % 16.  The K loop is the register-direct
+// kernel's MFMA-ahead ring (PF stages, unconditional prefetches).  GELU: the
+// wave's gate and up tiles of the same 16 output columns (W rows paired in
+// groups of kGeluGroup), g = geluquick(gate) * up, the sequences' max|g| into
+// amax.
+typedef int i32x4_mf __attribute__((ext_vector_type(4)));
+template <int T>
+struct TinyStage {
+  long a, w[T];
+  float d[T];
+};
+
+template <bool GELU, int PF>
+__global__ __launch_bounds__(256, 2) void k_gemm_q8_tiny(const int8_t* __restrict__ A, int a_rows,
+                                                         const int8_t* __restrict__ W, const float* __restrict__ St,
+                                                         const float* __restrict__ row_scale, float* __restrict__ Y,
+                                                         int M, int N, int K, const int32_t* __restrict__ row_seq,
+                                                         float* __restrict__ amax) {
+  constexpr int T = GELU ? 2 : 1;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int m0 = blockIdx.y * 16;
+  const int nout = GELU ? N / 2 : N;
+  const int c0 = (blockIdx.x * 4 + wave) * 16;  // this wave's 16 output columns
+  const bool active = c0 < nout;                // wave-uniform
+  const int nb = K >> 5;
+  const int64_t a_bstride = (int64_t)a_rows * 32, w_bstride = (int64_t)N * 32;
+  const int8_t* ap = A + (int64_t)(m0 + lr) * 32 + 8 * lg;
+  const int8_t* wp[T];
+  const float* sp[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    int wr = GELU ? (c0 / sgk::kGeluGroup) * 2 * sgk::kGeluGroup + c0 % sgk::kGeluGroup + t * sgk::kGeluGroup + lr : c0 + lr;
+    wr = wr < N ? wr : N - 1;
+    wp[t] = W + (int64_t)wr * 32 + 8 * lg;
+    sp[t] = St + wr;
+  }
+  auto fetch = [&](TinyStage<T>& st, int b) {
+    st.a = *reinterpret_cast<const long*>(ap + b * a_bstride);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      st.w[t] = *reinterpret_cast<const long*>(wp[t] + b * w_bstride);
+      st.d[t] = sp[t][(int64_t)b * N];
+    }
+  };
+  i32x4_mf bias = {kMagicBits, kMagicBits, kMagicBits, kMagicBits};
+  asm volatile("" : "+v"(bias));
+  auto mfma = [&](const TinyStage<T>& st, i32x4_mf (&p)[T]) {
+#pragma unroll
+    for (int t = 0; t < T; t++) p[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(st.a, st.w[t], bias, 0, 0, 0);
+  };
+  float acc[T][4];
+#pragma unroll
+  for (int t = 0; t < T; t++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
+  auto fma_block = [&](const i32x4_mf (&p)[T], const float (&d)[T]) {
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[t][r] = __builtin_fmaf(__int_as_float(p[t][r]) - kMagic, d[t], acc[t][r]);
+  };
+
+  if (active) {
+    TinyStage<T> st[PF];
+    static_for<0, PF - 1>([&](auto ic) {
+      constexpr int I = decltype(ic)::value;
+      fetch(st[I], min(I, nb - 1));
+    });
+    i32x4_mf p[T];
+    mfma(st[0], p);
+    int b = 0;
+    for (; b + PF <= nb; b += PF)
+      static_for<0, PF>([&](auto ic) {
+        constexpr int I = decltype(ic)::value;
+        fetch(st[(I + PF - 1) % PF], min(b + I + PF - 1, nb - 1));
+        __builtin_amdgcn_sched_barrier(0);
+        i32x4_mf pn[T];
+        mfma(st[(I + 1) % PF], pn);
+        __builtin_amdgcn_sched_barrier(0);
+        fma_block(p, st[I].d);
+#pragma unroll
+        for (int t = 0; t < T; t++) p[t] = pn[t];
+      });
+    static_for<0, PF - 1>([&](auto ic) {  // the last nb % PF blocks, already in stages 0 ..
+      constexpr int I = decltype(ic)::value;
+      if (b + I < nb) {
+        i32x4_mf pn[T];
+        mfma(st[(I + 1) % PF], pn);
+        __builtin_amdgcn_sched_barrier(0);
+        fma_block(p, st[I].d);
+#pragma unroll
+        for (int t = 0; t < T; t++) p[t] = pn[t];
+      }
+    });
+  }
+
+  const int col = c0 + lr;
+  // GELU: each row's max|g| over the wave's columns, then over the four
+  // waves (LDS), then a segmented max over the workgroup's 16 rows (packed
+  // sequence by sequence): one atomic per sequence and workgroup.
+  __shared__ float rmax[GELU ? 4 : 1][16];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int row = m0 + 4 * lg + r;
+    const float rs = row_scale[row < M ? row : M - 1];
+    if constexpr (GELU) {
+      const float gate = acc[0][r] * rs, up = acc[1][r] * rs;
+      const float g = sg_gelu_quick(gate) * up;
+      const bool ok = active && row < M && col < nout;
+      if (ok) Y[(int64_t)row * nout + col] = g;
+      float a = ok ? fabsf(g) : 0.0f;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
+      if (lr == 0) rmax[wave][4 * lg + r] = a;
+    } else {
+      if (active && row < M && col < N) Y[(int64_t)row * N + col] = acc[0][r] * rs;
+    }
+  }
+  if constexpr (GELU) {
+    if (!amax) return;  // grid-uniform
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      const int row = m0 + threadIdx.x;
+      float v = fmaxf(fmaxf(rmax[0][threadIdx.x], rmax[1][threadIdx.x]), fmaxf(rmax[2][threadIdx.x], rmax[3][threadIdx.x]));
+      const int sq = row < M ? row_seq[row] : -1;
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const float vu = __shfl_up(v, o);
+        const int su = __shfl_up(sq, o);
+        if ((int)threadIdx.x >= o && su == sq) v = fmaxf(v, vu);
+      }
+      const int sn = __shfl_down(sq, 1);
+      if (row < M && (threadIdx.x == 15 || sn != sq)) sg_atomic_max_nonneg(amax + sq, v);
+    }
+  }
+}
+
+template <bool GELU, int PF>
+hipError_t launch_tiny(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* rs, float* Y,
+                       int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
+  const int gm = (M + 15) / 16;
+  if ((int64_t)gm * 16 > a_rows) return hipErrorInvalidValue;  // A must cover the padded rows
+  const int nout = GELU ? N / 2 : N;
+  dim3 grid((nout + 63) / 64, gm);
+  hipLaunchKernelGGL((k_gemm_q8_tiny<GELU, PF>), grid, dim3(256), 0, s, A, a_rows, W, St, rs, Y, M, N, K, row_seq,
+                     amax);
+  return hipGetLastError();
+}
+
 template <int WM, int WN, int TM, int TN, bool SUMS, bool GELU = false, int PF = 2, bool PIPE = false>
 hipError_t launch_rd(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* rs, float* Y,
                      int32_t* sums, int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr,
@@ -683,6 +844,8 @@ constexpr int kResRows = 8192;
 // ms, 1 x 512 3.52 -> 3.36 ms.  With the weights in L2 (one weight called
 // again and again) the 3-stage ring is faster (M = 2048: Q/O 7.5 vs 8.2 us).
 constexpr int kPipeTiles = 384;
+// Batches of at most kTinyRows rows take k_gemm_q8_tiny.
+constexpr int kTinyRows = 256;
 inline int rd_tiles(int M, int N, int BM, int BN) { return ((M + BM - 1) / BM) * ((N + BN - 1) / BN); }
 
 hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
@@ -690,6 +853,7 @@ hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St
   if (M <= 0 || N <= 0) return hipSuccess;
   if (K <= 0 || K % 32) return hipErrorInvalidValue;
   if (sums) return launch_rd<1, 1, 1, 1, true>(A, a_rows, W, St, row_scale, Y, sums, M, N, K, s);
+  if (M <= kTinyRows) return launch_tiny<false, 8>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   if (M < kRdRows) {
     if (rd_tiles(M, N, 64, 64) <= kPipeTiles)
       return cold_weights
@@ -707,6 +871,7 @@ hipError_t gemm_q8_gelu(const int8_t* A, int a_rows, const int8_t* W, const floa
   if (M <= 0 || Nh <= 0) return hipSuccess;
   if (K <= 0 || K % 32 || Nh % 32) return hipErrorInvalidValue;
   if (amax && !row_seq) return hipErrorInvalidValue;
+  if (M <= kTinyRows) return launch_tiny<true, 8>(A, a_rows, W, St, row_scale, G, M, 2 * Nh, K, s, row_seq, amax);
   if (M < kGeluLdsRows && rd_tiles(M, 2 * Nh, 128, 64) <= kPipeTiles)
     return cold_weights ? launch_rd<4, 1, 1, 2, false, true, 6, true>(A, a_rows, W, St, row_scale, G, nullptr, M,
                                                                       2 * Nh, K, s, row_seq, amax)
