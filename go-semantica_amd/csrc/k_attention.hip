@@ -92,18 +92,25 @@ constexpr int kRegTiles = sgk::kAttnRegKeys / kBK;
 // applies attn_q_norm and RoPE to its 16 rows itself (the arithmetic of
 // k_qknorm_rope_split, so the operands are bit-identical), which saves writing
 // Q's hi/lo operands and reading them back; tile: the wave's 16 x 40 floats
-// of LDS for the norm.  Otherwise Q arrives split (qh, ql).
+// of LDS for the norm, wtile its 256 floats for the norm weights.  Otherwise
+// Q arrives split (qh, ql).
 template <bool QPRE>
 __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bql)[kHD / 32],
                                           const _Float16* __restrict__ qh, const _Float16* __restrict__ ql, int ldq,
                                           const sg_attn_qpre& qp, int qr, int pos, int head, int ln, int g4,
-                                          int lane, float* tile) {
+                                          int lane, float* tile, float* wtile) {
   if constexpr (QPRE) {
-    // Every global load (Q, the norm weights, the RoPE table rows of the
+    // Every global load (the norm weights, Q, the RoPE table rows of the
     // row's position pos) is issued up front, so the prologue pays one memory
     // latency instead of one per phase; the registers are free this early.
-    // Lane (ln, g4) holds elements e = 32ks + 8g4 + t of row ln.
-    float x[kHD / 32][8], wq[kHD / 32][8];
+    // Lane (ln, g4) holds elements e = 32ks + 8g4 + t of row ln.  The norm
+    // weights, the same for every row, are one 16-byte load per lane (the
+    // whole vector per wave) into wtile, read back as LDS broadcasts: loaded
+    // per lane they took 16 of the wave's 48 load instructions, and the
+    // prologue's time is its load instructions' (each wave's waits for the
+    // other wave of its SIMD).
+    float x[kHD / 32][8];
+    const f32x4_t wl = qp.w ? reinterpret_cast<const f32x4_t*>(qp.w)[lane] : f32x4_t{0, 0, 0, 0};
     const float* src = qp.q + (int64_t)qr * qp.ldq + head * kHD + 8 * g4;
 #pragma unroll
     for (int ks = 0; ks < kHD / 32; ks++) {
@@ -111,13 +118,6 @@ __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bq
       const f32x4_t* s4 = reinterpret_cast<const f32x4_t*>(src + 32 * ks);
       *reinterpret_cast<f32x4_t*>(&x[ks][0]) = __builtin_nontemporal_load(s4);
       *reinterpret_cast<f32x4_t*>(&x[ks][4]) = __builtin_nontemporal_load(s4 + 1);
-    }
-    if (qp.w) {
-#pragma unroll
-      for (int ks = 0; ks < kHD / 32; ks++) {
-        *reinterpret_cast<f32x4_t*>(&wq[ks][0]) = *reinterpret_cast<const f32x4_t*>(qp.w + 32 * ks + 8 * g4);
-        *reinterpret_cast<f32x4_t*>(&wq[ks][4]) = *reinterpret_cast<const f32x4_t*>(qp.w + 32 * ks + 8 * g4 + 4);
-      }
     }
     float cv[kHD / 64][8], sv[kHD / 64][8];
     const float* cr = qp.cos_t + (int64_t)pos * (kHD / 2) + 8 * g4;
@@ -129,6 +129,8 @@ __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bq
       *reinterpret_cast<f32x4_t*>(&sv[ks][0]) = *reinterpret_cast<const f32x4_t*>(sr + 32 * ks);
       *reinterpret_cast<f32x4_t*>(&sv[ks][4]) = *reinterpret_cast<const f32x4_t*>(sr + 32 * ks + 4);
     }
+    static_assert(kHD == 4 * SG_WAVE, "one float4 of the norm weights per lane");
+    if (qp.w) reinterpret_cast<f32x4_t*>(wtile)[lane] = wl;
     if (qp.w) {
       // RMSNorm's sum of squares in the AVX2 lane order (sg_rmsnorm8): lane v
       // of a row chains element 8i + v over i.  Element e sits at i = 4ks + g4,
@@ -157,12 +159,14 @@ __device__ __forceinline__ void q_operand(half8_t (&bqh)[kHD / 32], half8_t (&bq
       const float iA = __shfl(invA, 8 * (ln & 7)), iB = __shfl(invB, 8 * (ln & 7));
       const float inv = ln < 8 ? iA : iB;
 #pragma unroll
-      for (int ks = 0; ks < kHD / 32; ks++)
+      for (int ks = 0; ks < kHD / 32; ks++) {
+        const float* wv = wtile + 32 * ks + 8 * g4;
 #pragma unroll
         for (int t = 0; t < 8; t++) {
           const float u = x[ks][t] * inv;
-          x[ks][t] = u * wq[ks][t];
+          x[ks][t] = u * wv[t];
         }
+      }
     }
     // RoPE (rope_cache.go:85-104): pairs (e, e + 128) are chunks ks and ks + 4
     // of the same lane and slot.
@@ -337,8 +341,10 @@ __global__ __launch_bounds__(kNT, 2) void k_attn_rs(
   half8_t bqh[kHD / 32], bql[kHD / 32];
   // The Q prologue's LDS tiles sit in stage 2, which no copy touches before
   // the first barrier.
+  static_assert(kWaves * (16 * 40 + kHD) * 4 <= kTileBytes, "prologue tiles fit stage 2");
   q_operand<QPRE>(bqh, bql, qh, ql, ldq, qp, qr, qr - r0, head, ln, g4, lane,
-                  reinterpret_cast<float*>(lds + 2 * kTileBytes) + w * (16 * 40));
+                  reinterpret_cast<float*>(lds + 2 * kTileBytes) + w * (16 * 40),
+                  reinterpret_cast<float*>(lds + 2 * kTileBytes) + kWaves * (16 * 40) + w * kHD);
 
   auto key_of = [&](int kt, int st, int r) { return kt + 16 * st + 4 * g4 + r; };
   // ---- pass 1: S^T = K Q^T per tile, kept in registers; row max ----
