@@ -45,6 +45,29 @@ __device__ __forceinline__ i32x16_t magic_bias() {
   return bias;
 }
 
+// acc[r] = fma(float(P_b[r]), d, acc[r]) for the 16 block sums of one 32x32
+// subtile (pp: the MFMA result from the magic start value): the 16
+// subtractions, then 16 v_fmac_f32 (inline assembly, so that the scheduler
+// keeps them after all the subtractions).  Each FMA's operand was produced 16
+// instructions earlier; the compiler's own schedule runs each subtraction into
+// one temporary that the next FMA reads at once, so every pair waits out the
+// VALU latency.  The subtractions stay compiled code: the compiler inserts the
+// wait states an MFMA result needs before its first VALU read, which it does
+// not do for inline assembly.  The arithmetic (x - 12582912, then one fused
+// multiply-add) is unchanged.
+__device__ __forceinline__ void block_fma16(const i32x16_t& pp, float d, f32x16_t& acc) {
+  float p[16], a[16];
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    p[r] = __int_as_float(pp[r]) - kMagic;
+    a[r] = acc[r];
+  }
+#pragma unroll
+  for (int r = 0; r < 16; r++) asm("v_fmac_f32_e32 %0, %1, %2" : "+v"(a[r]) : "v"(p[r]), "v"(d));
+#pragma unroll
+  for (int r = 0; r < 16; r++) acc[r] = a[r];
+}
+
 // XCD-aware tile order.  Workgroups are handed to the 8 XCDs round-robin by
 // linear id, and each XCD has its own L2.  All N-tiles of one M-tile read the
 // same A rows, so they are mapped to one XCD: linear id p runs on XCD p % 8;
@@ -600,9 +623,7 @@ __global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_lds(
       const i32x4_t fw = *reinterpret_cast<const i32x4_t*>(lds + rw_f + ST * W_BYTES + tn * 512);
       const float d = *reinterpret_cast<const float*>(lds + rd + ST * S_BYTES + tn * 128);
       const i32x16_t pp = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fw, bias, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 16; r++)
-        acc[0][tn][r] = __builtin_fmaf(__int_as_float(pp[r]) - kMagic, d, acc[0][tn][r]);
+      block_fma16(pp, d, acc[0][tn]);
     }
   };
   static_for<0, STAGES - 1>([&](auto ic) { issue(min((int)decltype(ic)::value, nb - 1), decltype(ic)::value); });
@@ -733,8 +754,7 @@ __global__ __launch_bounds__(1024, 4) void k_gemm_q8_resnorm(
       const i32x4_t fw = *reinterpret_cast<const i32x4_t*>(lds + rw_f + ST * STAGE + t * 512);
       const float d = *reinterpret_cast<const float*>(lds + rd_f + ST * STAGE + t * 128);
       const i32x16_t pp = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fw, bias, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[t][r] = __builtin_fmaf(__int_as_float(pp[r]) - kMagic, d, acc[t][r]);
+      block_fma16(pp, d, acc[t]);
     }
   };
   static_for<0, STAGES - 1>([&](auto ic) { issue(min((int)decltype(ic)::value, nb - 1), decltype(ic)::value); });
