@@ -91,11 +91,39 @@ __device__ __forceinline__ void xcd_tile(int& bx, int& by) {
 // GELU, g = geluquick(gate) * up over the paired subtiles, with the
 // sequences' max|g| folded into amax).  Wave tile rows mw.., workgroup row
 // tile by, columns n0...
+// stage (optional): this wave's own 32 x 32 float slice of LDS.  Each output
+// subtile then goes out as row-contiguous float4 stores (lane l: row
+// l / 8 + 8 i, columns 4 (l % 8) .. + 3; 4 instructions per subtile) after
+// a transpose through the slice, instead of 16 single-float stores in the
+// MFMA's column-per-lane layout.
+__device__ __forceinline__ void store_subtile(float* stage, const float (&v)[16], float* __restrict__ Y, int ld,
+                                              int row0, int col0, int rows, int cols, int lr, int lh, int lane) {
+#pragma unroll
+  for (int r = 0; r < 16; r++) stage[(8 * (r >> 2) + 4 * lh + (r & 3)) * 32 + lr] = v[r];
+  const int c4 = (lane & 7) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int rl = (lane >> 3) + 8 * i;
+    const f32x4_t o = *reinterpret_cast<const f32x4_t*>(stage + rl * 32 + c4);
+    const int row = row0 + rl, col = col0 + c4;
+    if (row < rows) {
+      if (col + 3 < cols) {
+        *reinterpret_cast<f32x4_t*>(Y + (int64_t)row * ld + col) = o;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+          if (col + t < cols) Y[(int64_t)row * ld + col + t] = o[t];
+      }
+    }
+  }
+}
+
 template <int NW, int TM, int TN, bool GELU>
 __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int mw, int by, int n0, int lr, int lh,
                                               int lane, int wave, int tid, int M, int N,
                                               const float* __restrict__ row_scale, float* __restrict__ Y,
-                                              const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
+                                              const int32_t* __restrict__ row_seq, float* __restrict__ amax,
+                                              float* stage = nullptr) {
   constexpr int BMW = TM * 32;
   if constexpr (GELU) {
     // Subtile pairs (2p, 2p+1) are gate and up of output columns
@@ -110,6 +138,7 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
 #pragma unroll
     for (int tm = 0; tm < TM; tm++) {
       const int mb = mw + tm * 32;
+      float gv[TN / 2][16];
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
@@ -121,7 +150,10 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
           const float gate = acc[tm][2 * pr][r] * rsr, up = acc[tm][2 * pr + 1][r] * rsr;
           const float g = sg_gelu_quick(gate) * up;
           const bool ok = row < M && col < Nh;
-          if (ok) Y[(int64_t)row * Nh + col] = g;
+          if (stage)
+            gv[pr][r] = g;
+          else if (ok)
+            Y[(int64_t)row * Nh + col] = g;
           a = ok ? fmaxf(a, fabsf(g)) : a;
         }
         if (one_seq) {
@@ -131,6 +163,10 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
           for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
           if (lr == 0) rmax[row - r_first] = a;
         }
+      }
+      if (stage) {
+#pragma unroll
+        for (int pr = 0; pr < TN / 2; pr++) store_subtile(stage, gv[pr], Y, Nh, mb, (n0 >> 1) + 32 * pr, M, Nh, lr, lh, lane);
       }
     }
     if (one_seq) {
@@ -156,6 +192,16 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
       for (int r = 0; r < 16; r++) {
         const int row = mb + 8 * (r >> 2) + 4 * lh + (r & 3);
         rs[r] = row_scale[row < M ? row : M - 1];
+      }
+      if (stage) {
+#pragma unroll
+        for (int tn = 0; tn < TN; tn++) {
+          float v[16];
+#pragma unroll
+          for (int r = 0; r < 16; r++) v[r] = acc[tm][tn][r] * rs[r];
+          store_subtile(stage, v, Y, N, mb, n0 + tn * 32, M, N, lr, lh, lane);
+        }
+        continue;
       }
 #pragma unroll
       for (int r = 0; r < 16; r++) {
@@ -632,7 +678,12 @@ __global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_lds(
       if (b + decltype(ic)::value < nb) step(ic, b + decltype(ic)::value);
     });
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // redundant tail copies drained before exit
-  gemm_epilogue<NW, 1, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax);
+  // Every wave's last fragment reads and every copy are done: the ring's
+  // first NW * 4 KB become the waves' store staging slices.
+  static_assert(NW * 4096 <= S_OFF + STAGES * S_BYTES, "staging slices fit the ring");
+  __syncthreads();
+  gemm_epilogue<NW, 1, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax,
+                                 reinterpret_cast<float*>(lds) + wave * 1024);
 }
 
 template <int NW, int TN, bool GELU, int STAGES>
