@@ -643,7 +643,7 @@ hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int3
 hipError_t kv_prep(const float* k, const float* v, int ldkv, const float* kw, int HKV, int T, const int32_t* row_pos,
                    const float* cos_t, const float* sin_t, float eps, _Float16* ks_h, _Float16* ks_l, int ldks,
                    const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vt, int ldvt, hipStream_t s) {
-  if (T <= 0 || n_vtiles <= 0 || HKV <= 0) return hipSuccess;
+  if (T <= 0 || n_vtiles < 0 || HKV <= 0) return hipSuccess;
   if ((ldkv & 3) || (ldks & 7) || (ldvt & 7) || (reinterpret_cast<uintptr_t>(k) & 15) ||
       (reinterpret_cast<uintptr_t>(v) & 15) || (kw && (reinterpret_cast<uintptr_t>(kw) & 15)))
     return hipErrorInvalidValue;  // float4 loads of K and V rows and of the weights

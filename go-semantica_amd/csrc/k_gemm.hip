@@ -27,8 +27,10 @@
 
 #include "sg_device.h"
 #include "sg_kernels.h"
+#include "sg_kv_prep.h"
 
 typedef int i32x16_t __attribute__((ext_vector_type(16)));
+using sgk::sg_vt_out;
 
 namespace {
 
@@ -118,12 +120,65 @@ __device__ __forceinline__ void store_subtile(float* stage, const float (&v)[16]
   }
 }
 
+// One 32 x 32 subtile of V (tokens row0 .., dims dim0 ..) into V^T, through
+// the wave's LDS slice.  A subtile whose 32 tokens are one whole 32-key tile
+// of a sequence (the usual case for sequences that start on a 32-row
+// boundary) goes out as 16-byte hi and lo chunks: lane l covers dim l % 32,
+// positions 8c .. 8c + 7 (c = 2 (l / 32), + 1), each position p holding key
+// vt_key(p), 128 contiguous bytes per dim.  Any other subtile is written value
+// by value at its key's tile and position.
+__device__ __forceinline__ void store_vt_subtile(float* stage, const float (&v)[16], const sg_vt_out& vo, int row0,
+                                                 int dim0, int rows, int lr, int lh, int lane) {
+#pragma unroll
+  for (int r = 0; r < 16; r++) stage[(8 * (r >> 2) + 4 * lh + (r & 3)) * 32 + lr] = v[r];
+  const int dim = lane & 31;
+  const int s0 = vo.row_seq[min(row0, rows - 1)];
+  const int key0 = row0 - vo.seq_off[s0];
+  const bool whole = (key0 & 31) == 0 && row0 + 31 < rows && vo.row_seq[row0 + 31] == s0;  // wave-uniform
+  if (whole) {
+    _Float16* base = vo.vt + ((dim0 + dim) * vo.ldvt + 2 * (vo.voff[s0] + key0));  // < 2^31 (checked at launch)
+#pragma unroll 1
+    for (int cc = 0; cc < 2; cc++) {
+      const int c = 2 * (lane >> 5) + cc;
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        uint32_t hb[2], lb[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+          const hl16 sp = split_f16(stage[sgd::vt_key(8 * c + 2 * m + e) * 32 + dim]);
+          hb[e] = __builtin_bit_cast(uint16_t, sp.hi);
+          lb[e] = __builtin_bit_cast(uint16_t, sp.lo);
+        }
+        hw[m] = hb[0] | (hb[1] << 16);
+        lw[m] = lb[0] | (lb[1] << 16);
+      }
+      *reinterpret_cast<uint4*>(base + 8 * c) = uint4{hw[0], hw[1], hw[2], hw[3]};
+      *reinterpret_cast<uint4*>(base + 32 + 8 * c) = uint4{lw[0], lw[1], lw[2], lw[3]};
+    }
+  } else {
+#pragma unroll 1
+    for (int i = 0; i < 16; i++) {
+      const int rl = 2 * i + (lane >> 5), t = row0 + rl;
+      if (t < rows) {
+        const int sq = vo.row_seq[t], key = t - vo.seq_off[sq];
+        const int p = 8 * ((key & 15) >> 2) + 4 * ((key >> 4) & 1) + (key & 3);  // vt_key(p) == key & 31
+        _Float16* base = vo.vt + ((dim0 + dim) * vo.ldvt + 2 * (vo.voff[sq] + (key & ~31)));
+        const hl16 sp = split_f16(stage[rl * 32 + dim]);
+        base[p] = sp.hi;
+        base[32 + p] = sp.lo;
+      }
+    }
+  }
+}
+
 template <int NW, int TM, int TN, bool GELU>
 __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int mw, int by, int n0, int lr, int lh,
                                               int lane, int wave, int tid, int M, int N,
                                               const float* __restrict__ row_scale, float* __restrict__ Y,
                                               const int32_t* __restrict__ row_seq, float* __restrict__ amax,
-                                              float* stage = nullptr) {
+                                              float* stage = nullptr,
+                                              sg_vt_out vto = sg_vt_out{nullptr, 0, 0, nullptr, nullptr, nullptr}) {
   constexpr int BMW = TM * 32;
   if constexpr (GELU) {
     // Subtile pairs (2p, 2p+1) are gate and up of output columns
@@ -194,12 +249,19 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
         rs[r] = row_scale[row < M ? row : M - 1];
       }
       if (stage) {
+        // Scaled values first, so the row scales die before the stores.
+        float v[TN][16];
 #pragma unroll
-        for (int tn = 0; tn < TN; tn++) {
-          float v[16];
+        for (int tn = 0; tn < TN; tn++)
 #pragma unroll
-          for (int r = 0; r < 16; r++) v[r] = acc[tm][tn][r] * rs[r];
-          store_subtile(stage, v, Y, N, mb, n0 + tn * 32, M, N, lr, lh, lane);
+          for (int r = 0; r < 16; r++) v[tn][r] = acc[tm][tn][r] * rs[r];
+        if (vto.vt && n0 >= vto.col0) {  // workgroup-uniform: the tile is V columns only
+#pragma unroll
+          for (int tn = 0; tn < TN; tn++)
+            store_vt_subtile(stage, v[tn], vto, mb, n0 + tn * 32 - vto.col0, M, lr, lh, lane);
+        } else {
+#pragma unroll
+          for (int tn = 0; tn < TN; tn++) store_subtile(stage, v[tn], Y, N, mb, n0 + tn * 32, M, N, lr, lh, lane);
         }
         continue;
       }
@@ -604,7 +666,7 @@ template <int NW, int TN, bool GELU, int STAGES>
 __global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_lds(
     const int8_t* __restrict__ A, int a_rows, const int8_t* __restrict__ W, const float* __restrict__ St,
     const float* __restrict__ row_scale, float* __restrict__ Y, int M, int N, int K,
-    const int32_t* __restrict__ row_seq, float* __restrict__ amax) {
+    const int32_t* __restrict__ row_seq, float* __restrict__ amax, sg_vt_out vto) {
   constexpr int NWH = NW / 2;
   constexpr int BM = NW * 32, BN = TN * 32;
   static_assert(NW % 2 == 0 && TN == NWH, "copy split: 64 A rows and 32 W rows per wave and half");
@@ -683,18 +745,24 @@ __global__ __launch_bounds__(NW * SG_WAVE, NW == 8 ? 4 : 1) void k_gemm_q8_lds(
   static_assert(NW * 4096 <= S_OFF + STAGES * S_BYTES, "staging slices fit the ring");
   __syncthreads();
   gemm_epilogue<NW, 1, TN, GELU>(acc, mw, by, n0, lr, lh, lane, wave, tid, M, N, row_scale, Y, row_seq, amax,
-                                 reinterpret_cast<float*>(lds) + wave * 1024);
+                                 reinterpret_cast<float*>(lds) + wave * 1024, vto);
 }
 
 template <int NW, int TN, bool GELU, int STAGES>
 hipError_t launch_lds(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* rs, float* Y,
-                      int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr) {
+                      int M, int N, int K, hipStream_t s, const int32_t* row_seq = nullptr, float* amax = nullptr,
+                      const sg_vt_out* vto = nullptr) {
   constexpr int BM = NW * 32, BN = TN * 32;
   const int gm = (M + BM - 1) / BM;
   if ((int64_t)gm * BM > a_rows) return hipErrorInvalidValue;
+  if (vto && (GELU || !vto->vt || vto->col0 <= 0 || vto->col0 % BN || vto->col0 >= N || (vto->ldvt & 7) ||
+              !vto->row_seq || !vto->seq_off || !vto->voff || (reinterpret_cast<uintptr_t>(vto->vt) & 15) ||
+              (int64_t)(N - vto->col0) * vto->ldvt > INT32_MAX))
+    return hipErrorInvalidValue;  // whole V tiles; 16-byte chunk stores; 32-bit V^T offsets
+  const sg_vt_out vo = vto ? *vto : sg_vt_out{nullptr, 0, 0, nullptr, nullptr, nullptr};
   dim3 grid((N + BN - 1) / BN, gm);
   hipLaunchKernelGGL((k_gemm_q8_lds<NW, TN, GELU, STAGES>), grid, dim3(NW * SG_WAVE), 0, s, A, a_rows, W, St, rs, Y,
-                     M, N, K, row_seq, amax);
+                     M, N, K, row_seq, amax, vo);
   return hipGetLastError();
 }
 
@@ -919,10 +987,13 @@ constexpr int kPipeTiles = 384;
 constexpr int kTinyRows = 256;
 inline int rd_tiles(int M, int N, int BM, int BN) { return ((M + BM - 1) / BM) * ((N + BN - 1) / BN); }
 
+bool gemm_writes_vt(int M) { return M >= kRdRows; }
+
 hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
-                   int32_t* sums, int M, int N, int K, hipStream_t s, bool cold_weights) {
+                   int32_t* sums, int M, int N, int K, hipStream_t s, bool cold_weights, const sg_vt_out* vto) {
   if (M <= 0 || N <= 0) return hipSuccess;
   if (K <= 0 || K % 32) return hipErrorInvalidValue;
+  if (vto && (sums || !gemm_writes_vt(M))) return hipErrorInvalidValue;
   if (sums) return launch_rd<1, 1, 1, 1, true>(A, a_rows, W, St, row_scale, Y, sums, M, N, K, s);
   if (M <= kTinyRows) return launch_tiny<false, 8>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
   if (M < kRdRows) {
@@ -932,8 +1003,8 @@ hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St
                  : launch_rd<2, 2, 1, 1, false, false, 3, true>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
     return launch_rd<2, 2, 1, 1, false>(A, a_rows, W, St, row_scale, Y, nullptr, M, N, K, s);
   }
-  if (M < kLds8Rows) return launch_lds<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
-  return launch_lds<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s);
+  if (M < kLds8Rows) return launch_lds<4, 2, false, 6>(A, a_rows, W, St, row_scale, Y, M, N, K, s, nullptr, nullptr, vto);
+  return launch_lds<8, 4, false, 3>(A, a_rows, W, St, row_scale, Y, M, N, K, s, nullptr, nullptr, vto);
 }
 
 hipError_t gemm_q8_gelu(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale,

@@ -525,9 +525,19 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
   auto gemm = [&](const int8_t* w8, const float* st, float* y, int N, int K) {
     return sgk::gemm_q8(a8, ar, w8, st, sx, y, nullptr, T, N, K, s, true);
   };
+  // The QKV GEMM writes V straight into the attention's V^T operand (the
+  // direct-to-LDS kernels' epilogue), so k_kv_prep only prepares K; not in
+  // exact mode (its attention reads V in fp32) nor when Q|K|V is traced.
+  const bool vt_fused = m->attn_mode != SG_ATTN_EXACT && !(tr && tr->qkv) && sgk::gemm_writes_vt(T);
+  const sgk::sg_vt_out vto{vt_h, ldvt, qd + kvd, meta.row_seq, meta.seq_off, meta.voff};
 
   if (l0 == 0) {
     SG_LAUNCH(SG_K_OTHER, 4.0 * 4 * L * ns, sgk::fill_f32(amax, 0.0f, (int64_t)4 * L * ns, s));
+    // V^T positions past each sequence's end stay zero through the layers
+    // (the fused epilogue writes only the sequences' keys).
+    if (vt_fused)
+      SG_LAUNCH(SG_K_OTHER, 4.0 * kvd * meta.Tp,
+                sgk::fill_i32(reinterpret_cast<int32_t*>(vt_h), 0, (int64_t)kvd * meta.Tp, s));
     SG_LAUNCH(SG_K_OTHER, 4.0, sgk::fill_i32(w.err.as<int32_t>(), INT32_MAX, 1, s));
     SG_LAUNCH(SG_K_NORM, t * (34.0 * d / 32 + 4.0 * d),
               sgk::embed_norm(d_tokens, T, m->emb_q, m->emb_s, c.vocab_size, d, m->sqrt_d, m->layers[0].attn_norm,
@@ -549,7 +559,8 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
     // The pre-norm's output xn is never stored: recomputed from h while quantizing.
     if (!a8_ready) SG_LAUNCH(SG_K_QUANTIZE, quant_bytes(d), norm_q(ly.attn_norm, site(l, 0)));
     a8_ready = false;
-    SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d), gemm(ly.wqkv, ly.sqkv, qkv, nqkv, d));
+    SG_LAUNCH(SG_K_GEMM, gemm_ops(nqkv, d),
+              sgk::gemm_q8(a8, ar, ly.wqkv, ly.sqkv, sx, qkv, nullptr, T, nqkv, d, s, true, vt_fused ? &vto : nullptr));
     if (tr && tr->qkv) SG_HIP(tap(tr->qkv, qkv, l, nqkv));
     if (m->attn_mode == SG_ATTN_EXACT) {
       // The reference's float32 order throughout: QK-norm + RoPE in place on
@@ -565,10 +576,10 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
     } else {
       // K's QK-norm + RoPE + split and V's V^T split in one launch; Q's norm and
       // RoPE run inside the attention kernel.
-      SG_LAUNCH(SG_K_NORM, t * kvd * 16.0,
+      SG_LAUNCH(SG_K_NORM, t * kvd * (vt_fused ? 8.0 : 16.0),
                 sgk::kv_prep(qkv + qd, qkv + qd + kvd, nqkv, ly.k_norm, c.num_kv_heads, T, meta.row_pos, m->cos_t,
-                             m->sin_t, eps, ks_h, ks_l, kvd, meta.seq_off, meta.voff, meta.vtiles, meta.n_vtiles,
-                             vt_h, ldvt, s));
+                             m->sin_t, eps, ks_h, ks_l, kvd, meta.seq_off, meta.voff, meta.vtiles,
+                             vt_fused ? 0 : meta.n_vtiles, vt_h, ldvt, s));
       const sg_attn_qpre qpre{qkv, nqkv, ly.q_norm, m->cos_t, m->sin_t, eps};
       const sg_attn_qout qout{a8, ar, sx};
       const sg_attn_spill spill{w.spill.as<float>(), meta.spill_off, meta.spill_total};

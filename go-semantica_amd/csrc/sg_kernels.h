@@ -131,8 +131,23 @@ hipError_t stream_probe(int kind, const float* a, const float* b, void* c, int64
 // the exact block sums int32 [M][N][K/32].  cold_weights: W is not expected
 // in L2 (the forward, one layer after another), which selects deeper load
 // pipelines for small grids; the results are the same either way.
+// The V columns [col0, N) of the QKV GEMM written straight as attention's
+// V^T operand (hi/lo fp16 in the layout and key order k_kv_prep's V half
+// writes: per sequence s at key columns voff[s] ..) instead of fp32 into Y;
+// the bits are the same.  Positions past a sequence's end are not written.
+struct sg_vt_out {
+  _Float16* vt;
+  int ldvt;
+  int col0;
+  const int32_t* row_seq;
+  const int32_t* seq_off;
+  const int32_t* voff;
+};
+// Whether gemm_q8 takes an sg_vt_out at M rows (the direct-to-LDS kernels).
+bool gemm_writes_vt(int M);
 hipError_t gemm_q8(const int8_t* A, int a_rows, const int8_t* W, const float* St, const float* row_scale, float* Y,
-                   int32_t* sums, int M, int N, int K, hipStream_t s, bool cold_weights = false);
+                   int32_t* sums, int M, int N, int K, hipStream_t s, bool cold_weights = false,
+                   const sg_vt_out* vto = nullptr);
 // FFN gate/up GEMM with GELUQuick(gate) * up in the epilogue: W holds 2*Nh rows,
 // gate and up interleaved in groups of kGeluGroup (see repack_q8_0's grouping);
 // G[M][Nh] is bit-identical to the unfused GEMMs + gelu_mul; amax (optional,
@@ -168,7 +183,8 @@ inline int attn_key_pad(int S) { return (S + 31) / 32 * 32; }
 hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles,
                      int n_vtiles, int HKV, _Float16* vt, int ldvt, hipStream_t s);
 // qknorm_rope's K-only split (H = 0) and v_split_t in one launch: K and V
-// share the row stride ldkv (columns of the QKV output).
+// share the row stride ldkv (columns of the QKV output).  n_vtiles = 0: K
+// only (V^T written by the QKV GEMM, sg_vt_out).
 hipError_t kv_prep(const float* k, const float* v, int ldkv, const float* kw, int HKV, int T, const int32_t* row_pos,
                    const float* cos_t, const float* sin_t, float eps, _Float16* ks_h, _Float16* ks_l, int ldks,
                    const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vt,

@@ -380,6 +380,41 @@ def test_short_sequence_fusions_match_unfused(full_gpu, mode):
             assert np.array_equal(e.view(np.uint32), ref.view(np.uint32)), (len(key) // 4, ref_name, name)
 
 
+@pytest.mark.parametrize("lens", [
+    [512] * 20 + [37, 1000, 511, 513, 1, 33, 2048, 64, 95, 700],  # 15,086 tokens: the 8-wave GEMM kernel
+    [31, 32, 33, 512, 1024, 600, 7, 2000, 1500, 500],            # 6,239 tokens: the 4-wave GEMM kernel
+])
+def test_qkv_gemm_writes_vt_operand(tiny_gpu, lens):
+    """From 6144 tokens the QKV GEMM's epilogue writes the V columns straight as
+    the attention's V^T operand (hi/lo fp16, keys in the MMA order; whole
+    32-key tiles as 16-byte chunks, tokens of a subtile that is not one
+    aligned key tile value by value) and k_kv_prep prepares only K.  Tracing
+    Q|K|V turns that off (the fp32 V is then stored and split by k_kv_prep),
+    so the residual stream traced with and without the Q|K|V tap compares the
+    two forms: bit-identical after every layer, for sequences that start on
+    and off 32-row boundaries, of length 1 to 2048.  The batch embedded
+    normally (fused, two sequence groups from 8192 tokens) equals the traced
+    final embeddings' path through batch invariance of single sequences."""
+    import torch
+    rng = np.random.default_rng(21)
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T, L = int(off[-1]), 2
+    toks = rng.integers(0, 4096, size=T).astype(np.int32)
+    say(f"QKV GEMM V^T epilogue: {len(lens)} sequences, {T} tokens")
+    d_tok = torch.from_numpy(toks).cuda()
+    h_fused = torch.empty((L, T, 768), dtype=torch.float32, device="cuda")
+    h_plain = torch.empty_like(h_fused)
+    qkv = torch.empty((L, T, 1280), dtype=torch.float32, device="cuda")
+    tiny_gpu.forward_trace(d_tok.data_ptr(), off, L, d_h_ptr=h_fused.data_ptr())
+    tiny_gpu.forward_trace(d_tok.data_ptr(), off, L, d_qkv_ptr=qkv.data_ptr(), d_h_ptr=h_plain.data_ptr())
+    torch.cuda.synchronize()
+    a, b = h_fused.cpu().numpy(), h_plain.cpu().numpy()
+    for l in range(L):
+        assert np.array_equal(a[l].view(np.uint32), b[l].view(np.uint32)), l
+    y = tiny_gpu.forward_packed(toks, off, 768)
+    _batch_invariance(tiny_gpu, toks, off, 768, y, (0, len(lens) - 3, len(lens) - 1))
+
+
 def test_concurrent_callers_match_serial(tiny_gpu):
     """TestConcurrentBufferPooling (internal/runtime/pooling_test.go:34-75):
     seven host threads call sg_forward on one model at once, four times each
