@@ -340,9 +340,7 @@ __device__ __forceinline__ void block_fma(const i32x16_t (&p)[TM][TN], const flo
           if (row < M && col < N) sums[((int64_t)row * N + col) * nb + b] = p[tm][tn][r] - kMagicBits;
         }
       }
-#pragma unroll
-      for (int r = 0; r < 16; r++)
-        acc[tm][tn][r] = __builtin_fmaf(__int_as_float(p[tm][tn][r]) - kMagic, d[tn], acc[tm][tn][r]);
+      block_fma16(p[tm][tn], d[tn], acc[tm][tn]);
     }
 }
 
@@ -524,10 +522,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm_q8_tiny(const int8_t* __restric
 #pragma unroll
     for (int r = 0; r < 4; r++) acc[t][r] = 0.0f;
   auto fma_block = [&](const i32x4_mf (&p)[T], const float (&d)[T]) {
+    // Every subtraction, then every FMA (as block_fma16: no FMA waits on the
+    // instruction just before it).
+    float q[T][4];
 #pragma unroll
     for (int t = 0; t < T; t++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc[t][r] = __builtin_fmaf(__int_as_float(p[t][r]) - kMagic, d[t], acc[t][r]);
+      for (int r = 0; r < 4; r++) q[t][r] = __int_as_float(p[t][r]) - kMagic;
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) asm("v_fmac_f32_e32 %0, %1, %2" : "+v"(acc[t][r]) : "v"(q[t][r]), "v"(d[t]));
   };
 
   if (active) {
