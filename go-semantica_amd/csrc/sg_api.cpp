@@ -62,6 +62,9 @@ struct Meta {
   // work item: the post-norms and the attention then quantize the next GEMM
   // operand themselves (the short-sequence serving case).
   bool seq_in_row_block = false, seq_one_item = false;
+  // Every sequence starts on a 32-row boundary (so the QKV GEMM's 32-row
+  // subtiles are whole 32-key V^T tiles, except a last sequence's tail).
+  bool seq_start32 = false;
   // device views into one buffer
   int32_t* row_seq = nullptr;
   int32_t* row_pos = nullptr;
@@ -173,6 +176,9 @@ int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev,
   for (int i = 0; i < n_seq; i++)
     if (off[i + 1] > off[i] && off[i] / sgk::kRowKernelRows != (off[i + 1] - 1) / sgk::kRowKernelRows)
       m.seq_in_row_block = false;
+  m.seq_start32 = true;
+  for (int i = 0; i < n_seq; i++)
+    if (off[i] % 32) m.seq_start32 = false;
   m.Tp = vo[n_seq];
   m.row_seq = d;
   m.row_pos = d + T;
@@ -526,9 +532,15 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
     return sgk::gemm_q8(a8, ar, w8, st, sx, y, nullptr, T, N, K, s, true);
   };
   // The QKV GEMM writes V straight into the attention's V^T operand (the
-  // direct-to-LDS kernels' epilogue), so k_kv_prep only prepares K; not in
-  // exact mode (its attention reads V in fp32) nor when Q|K|V is traced.
-  const bool vt_fused = m->attn_mode != SG_ATTN_EXACT && !(tr && tr->qkv) && sgk::gemm_writes_vt(T);
+  // direct-to-LDS kernels' epilogue), so k_kv_prep only prepares K: for
+  // batches whose sequences all start on 32-row boundaries, where the
+  // epilogue's subtiles are whole key tiles (other subtiles go out value by
+  // value: for 256 ragged sequences of 8-512 tokens the GEMM class then took
+  // 8.1 instead of 6.4 ms per forward, far more than k_kv_prep's V half
+  // saves).  Not in exact mode
+  // (its attention reads V in fp32) nor when Q|K|V is traced.
+  const bool vt_fused = m->attn_mode != SG_ATTN_EXACT && !(tr && tr->qkv) && sgk::gemm_writes_vt(T) &&
+                        meta.seq_start32;
   const sgk::sg_vt_out vto{vt_h, ldvt, qd + kvd, meta.row_seq, meta.seq_off, meta.voff};
 
   if (l0 == 0) {

@@ -381,20 +381,21 @@ def test_short_sequence_fusions_match_unfused(full_gpu, mode):
 
 
 @pytest.mark.parametrize("lens", [
-    [512] * 20 + [37, 1000, 511, 513, 1, 33, 2048, 64, 95, 700],  # 15,086 tokens: the 8-wave GEMM kernel
-    [31, 32, 33, 512, 1024, 600, 7, 2000, 1500, 500],            # 6,239 tokens: the 4-wave GEMM kernel
+    [512] * 20 + [32, 992, 64, 2048, 96, 37],                    # 13,509 tokens: the 8-wave GEMM kernel
+    [256] * 20 + [32, 480, 1024, 37],                            # 6,693 tokens: the 4-wave GEMM kernel
+    [512] * 20 + [37, 1000, 511, 513, 1, 33, 2048, 64, 95, 700],  # starts off 32-row boundaries: not fused
 ])
 def test_qkv_gemm_writes_vt_operand(tiny_gpu, lens):
-    """From 6144 tokens the QKV GEMM's epilogue writes the V columns straight as
-    the attention's V^T operand (hi/lo fp16, keys in the MMA order; whole
-    32-key tiles as 16-byte chunks, tokens of a subtile that is not one
-    aligned key tile value by value) and k_kv_prep prepares only K.  Tracing
-    Q|K|V turns that off (the fp32 V is then stored and split by k_kv_prep),
-    so the residual stream traced with and without the Q|K|V tap compares the
-    two forms: bit-identical after every layer, for sequences that start on
-    and off 32-row boundaries, of length 1 to 2048.  The batch embedded
-    normally (fused, two sequence groups from 8192 tokens) equals the traced
-    final embeddings' path through batch invariance of single sequences."""
+    """From 6144 tokens, when every sequence starts on a 32-row boundary, the
+    QKV GEMM's epilogue writes the V columns straight as the attention's V^T
+    operand (hi/lo fp16, keys in the MMA order; whole 32-key tiles as 16-byte
+    chunks, the last sequence's partial tile value by value) and k_kv_prep
+    prepares only K.  Tracing Q|K|V turns that off (the fp32 V is then stored
+    and split by k_kv_prep), so the residual stream traced with and without
+    the Q|K|V tap compares the two forms: bit-identical after every layer.
+    The batch embedded normally (two sequence groups from 8192 tokens) is
+    pinned to single sequences (register-direct GEMMs, never fused) by batch
+    invariance."""
     import torch
     rng = np.random.default_rng(21)
     off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
