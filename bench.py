@@ -412,6 +412,27 @@ def hbm_reference_leg(ctx, T, d=768, reps=20):
     return {"workload": f"[{T}, {d}] fp32 tensors, {reps} launches each", **res}
 
 
+def issue_probe_leg(ctx):
+    """The compute floor of the Q8_0 GEMM kernels: SIMD cycles per 32x32 output
+    subtile and K-block of their arithmetic alone (sg_issue_probe: one int8
+    MFMA, then the block-serial update of 16 subtractions + 16 v_fmac, no
+    memory traffic), of its VALU and MFMA halves alone, at 2 and 4 waves per
+    SIMD (the GEMM kernels run 4).  The MFMA is 32 cycles of the matrix pipe
+    (its issue interval at the dense int8 peak), so 32 / (cycles of kind 0)
+    is the largest fraction of the int8 peak these kernels can reach."""
+    from semantica_gpu import kernels
+    res = {}
+    for w in (2, 4):
+        row = {}
+        for kind, name in ((0, "mfma_plus_update"), (1, "update_only"), (2, "mfma_only")):
+            cyc, ghz = kernels.issue_probe(ctx, kind, w)
+            row[name] = round(cyc, 1)
+        row["clock_GHz"] = round(ghz, 2)
+        row["int8_peak_frac_ceiling"] = round(32.0 / row["mfma_plus_update"], 3)
+        res[f"{w}_waves_per_simd"] = row
+    return {"unit": "SIMD cycles per 32x32 subtile and K-block", **res}
+
+
 def tokenizer_leg(n_texts=64, chars=2000):
     """The host tokenizer (sg_tokenizer_*, internal/tokenizer) on a synthetic
     262,144-token vocabulary (the real one is not available offline): texts of
@@ -603,6 +624,7 @@ def main():
     if not a.no_extras:
         line["exact_attention"] = exact_attention_leg(model, d_tok, off, d_out, max(2, a.steps // 4), B)
         line["hbm_reference"] = hbm_reference_leg(ctx, B * S)
+        line["gemm_issue_floor"] = issue_probe_leg(ctx)
         line["latency"] = small_batch_latency(model)
         line["gemm_c1"] = gemm_c1_leg(ctx)
         line["config3"] = ragged_config_leg(model, 3)

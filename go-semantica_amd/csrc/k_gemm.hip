@@ -954,6 +954,68 @@ __global__ __launch_bounds__(1024, 4) void k_gemm_q8_resnorm(
   }
 }
 
+// Issue-rate yardstick for the K loop's arithmetic (sg_issue_probe), with no
+// memory traffic: per step a wave issues two independent int8 MFMAs
+// (kind 0 and 2), then converts and accumulates the previous step's two
+// block-sum subtiles as block_fma16 does (kind 0 and 1: 32 subtractions and
+// 32 v_fmac).  Kind 0 is the K loop's per-subtile work; 1 and 2 its VALU and
+// matrix halves alone.  Each wave records its shader-clock cycles (s_memtime)
+// and constant-rate wall clock (s_memrealtime) over `iters` steps.
+template <int KIND>
+__global__ __launch_bounds__(256) void k_issue_probe(float* __restrict__ sink, long long* __restrict__ clk, int iters) {
+  const int lane = threadIdx.x & 63;
+  i32x4_t a = {lane, 3, 5, 7}, w = {11, lane, 13, 17};
+  const i32x16_t bias = magic_bias();
+  f32x16_t acc0, acc1;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    acc0[r] = 0.0f;
+    acc1[r] = 0.0f;
+  }
+  i32x16_t p0 = bias, p1 = bias;
+  p0[0] += lane;
+  p1[1] += lane;
+  const float d = 1.0f + lane * 1e-7f;
+  __syncthreads();
+  const long long t0 = clock64(), r0 = wall_clock64();
+  for (int i = 0; i < iters; i += 2) {
+    i32x16_t q0 = p0, q1 = p1;
+    if (KIND != 1) {
+      q0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w, bias, 0, 0, 0);
+      q1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(w, a, bias, 0, 0, 0);
+      if (KIND == 2) asm volatile("" ::"v"(q0), "v"(q1));  // results kept live without the update
+    }
+    if (KIND != 2) {
+      block_fma16(p0, d, acc0);
+      block_fma16(p1, d, acc1);
+    }
+    a.x += 1;
+    if (KIND != 1) {
+      p0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, w, bias, 0, 0, 0);
+      p1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(w, a, bias, 0, 0, 0);
+    } else {
+      p0 = q1;
+      p1 = q0;
+      asm volatile("" : "+v"(p0), "+v"(p1));
+    }
+    if (KIND != 2) {
+      block_fma16(q0, d, acc0);
+      block_fma16(q1, d, acc1);
+    }
+    a.x += 1;
+  }
+  const long long t1 = clock64(), r1 = wall_clock64();
+  float s = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 16; r++) s += acc0[r] + acc1[r] + (float)p0[r] + (float)p1[r];
+  sink[blockIdx.x * 256 + threadIdx.x] = s;
+  if (lane == 0) {
+    const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+    clk[2 * wv] = t1 - t0;
+    clk[2 * wv + 1] = r1 - r0;
+  }
+}
+
 }  // namespace
 
 namespace sgk {
@@ -1057,4 +1119,23 @@ hipError_t gemm_q8_res_norm(const int8_t* A, int a_rows, const int8_t* W, const 
   return hipGetLastError();
 }
 
+hipError_t issue_probe(int kind, int blocks, float* sink, long long* clk, int iters, hipStream_t s) {
+  if (blocks <= 0 || iters <= 0 || iters % 2) return hipErrorInvalidValue;
+  switch (kind) {
+    case 0:
+      hipLaunchKernelGGL(k_issue_probe<0>, dim3(blocks), dim3(256), 0, s, sink, clk, iters);
+      break;
+    case 1:
+      hipLaunchKernelGGL(k_issue_probe<1>, dim3(blocks), dim3(256), 0, s, sink, clk, iters);
+      break;
+    case 2:
+      hipLaunchKernelGGL(k_issue_probe<2>, dim3(blocks), dim3(256), 0, s, sink, clk, iters);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace sgk
+

@@ -1191,6 +1191,57 @@ int sg_hbm_probe(sg_ctx* ctx, int32_t kind, const float* a, const float* b, void
   return SG_OK;
 }
 
+int sg_issue_probe(sg_ctx* ctx, int32_t kind, int32_t waves_per_simd, int32_t iters, void* stream,
+                   float* simd_cycles_per_block, float* clock_ghz) {
+  if (!ctx || !simd_cycles_per_block || !clock_ghz) return fail(SG_ERR_INVALID, "NULL argument");
+  if (kind < 0 || kind > 2) return fail(SG_ERR_INVALID, "unknown probe kind %d", kind);
+  if (waves_per_simd < 1 || waves_per_simd > 8 || iters < 2 || iters % 2 || iters > (1 << 24))
+    return fail(SG_ERR_INVALID, "waves_per_simd 1..8, iters even in 2..2^24");
+  SG_TRY(set_device(ctx));
+  hipStream_t s = pick(ctx, stream);
+  int cus = 0, wall_khz = 0;
+  SG_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
+  SG_HIP(hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, ctx->device));
+  if (cus <= 0 || wall_khz <= 0) return fail(SG_ERR_DEVICE, "device attributes unavailable");
+  const int blocks = cus * waves_per_simd;  // 4 waves per workgroup: waves_per_simd per SIMD
+  float* sink = nullptr;
+  long long* clk = nullptr;
+  SG_HIP(hipMalloc(&sink, sizeof(float) * 256 * (size_t)blocks));
+  if (hipMalloc(&clk, sizeof(long long) * 8 * (size_t)blocks) != hipSuccess) {
+    (void)hipFree(sink);
+    return fail(SG_ERR_NOMEM, "hipMalloc failed");
+  }
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  hipError_t e = sgk::issue_probe(kind, blocks, sink, clk, iters, s);  // warm
+  if (e == hipSuccess) e = hipEventCreate(&e0);
+  if (e == hipSuccess) e = hipEventCreate(&e1);
+  if (e == hipSuccess) e = hipEventRecord(e0, s);
+  if (e == hipSuccess) e = sgk::issue_probe(kind, blocks, sink, clk, iters, s);
+  if (e == hipSuccess) e = hipEventRecord(e1, s);
+  if (e == hipSuccess) e = hipEventSynchronize(e1);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+  std::vector<long long> h((size_t)8 * blocks);
+  if (e == hipSuccess) e = hipMemcpy(h.data(), clk, sizeof(long long) * h.size(), hipMemcpyDeviceToHost);
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (e != hipSuccess) (void)hipStreamSynchronize(s);
+  (void)hipFree(sink);
+  (void)hipFree(clk);
+  SG_HIP(e);
+  double cyc = 0, ticks = 0;
+  for (int i = 0; i < 4 * blocks; i++) {
+    cyc += (double)h[2 * i];
+    ticks += (double)h[2 * i + 1];
+  }
+  if (ticks <= 0 || ms <= 0) return fail(SG_ERR_DEVICE, "probe clocks unavailable");
+  const double ghz = cyc / (ticks / (wall_khz * 1e3)) / 1e9;
+  // every SIMD ran waves_per_simd waves of iters steps, two subtile-blocks each
+  *simd_cycles_per_block = (float)(ms * 1e-3 * ghz * 1e9 / ((double)iters * 2 * waves_per_simd));
+  *clock_ghz = (float)ghz;
+  return SG_OK;
+}
+
 int sg_q8_block_sums(sg_ctx* ctx, int32_t* out, const sg_q8_weight* w, const int8_t* x, int32_t batch, void* stream) {
   return matmul_common(ctx, nullptr, out, w, x, nullptr, batch, stream);
 }

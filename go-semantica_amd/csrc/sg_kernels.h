@@ -123,6 +123,9 @@ hipError_t embed_only(const int32_t* tokens, int T, const int8_t* eq, const floa
 // Streaming yardsticks over n floats (n % 4 == 0, 16-byte aligned): kind 0
 // c = a + b (fp32), kind 1 c = int8 codes of a (b unused).
 hipError_t stream_probe(int kind, const float* a, const float* b, void* c, int64_t n, hipStream_t s);
+// k_issue_probe<kind> on `blocks` workgroups of 4 waves: sink [blocks * 256]
+// floats, clk [blocks * 4 * 2] (per wave: shader cycles, wall-clock ticks).
+hipError_t issue_probe(int kind, int blocks, float* sink, long long* clk, int iters, hipStream_t s);
 
 // ---- GEMM (k_gemm.hip) ----
 // Y[M][N] = (sum_b float(P_b) * St[b][n]) * row_scale[m] with A int8 [M][K]

@@ -120,6 +120,8 @@ _PROTOS = {
     "sg_q8_block_sums": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _vp]),
     "sg_hbm_probe": (ctypes.c_int, [_vp, _i32, _vp, _vp, _vp, ctypes.c_int64, _i32, _vp,
                                     ctypes.POINTER(ctypes.c_float)]),
+    "sg_issue_probe": (ctypes.c_int, [_vp, _i32, _i32, _i32, _vp, ctypes.POINTER(ctypes.c_float),
+                                      ctypes.POINTER(ctypes.c_float)]),
     "sg_ffn_gate_up": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),
     "sg_rmsnorm": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i32, _i32, _f32, _vp]),
     "sg_qknorm_rope": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i32, _vp, _vp, _i32, _i32, _i32, _f32, _f32,

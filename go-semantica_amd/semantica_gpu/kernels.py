@@ -147,6 +147,16 @@ def hbm_probe_us(ctx, kind: int, a, b, c, reps: int, stream=None) -> float:
     return us.value
 
 
+def issue_probe(ctx, kind: int, waves_per_simd: int, iters: int = 20000, stream=None):
+    """sg_issue_probe: SIMD cycles per 32x32 subtile and K-block of the GEMM's
+    arithmetic with no memory traffic (kind 0: MFMA + block-serial update;
+    1: the VALU part; 2: the MFMA), and the shader clock in GHz."""
+    cyc, ghz = ctypes.c_float(), ctypes.c_float()
+    _lib.check(ctx.lib.sg_issue_probe(ctx.handle, kind, waves_per_simd, iters, _stream(stream), ctypes.byref(cyc),
+                                      ctypes.byref(ghz)))
+    return cyc.value, ghz.value
+
+
 def gelu_quick_mul(ctx, dst, gate, up, stream=None):
     _check_dev(dst, gate, up)
     rows, cols = gate.shape

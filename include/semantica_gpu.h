@@ -247,6 +247,20 @@ int sg_matmul_q8_0_int8_noalloc(sg_ctx *ctx, float *dst, const sg_q8_weight *w, 
 int sg_hbm_probe(sg_ctx *ctx, int32_t kind, const float *a, const float *b, void *c, int64_t n,
                  int32_t reps, void *stream, float *us_per_launch);
 
+/* Measurement hook (no counterpart in the reference): the issue rate of the
+ * Q8_0 GEMM's per-K-block arithmetic with no memory traffic, the compute
+ * floor of those kernels.  kind 0: per 32x32 output subtile and K-block one
+ * v_mfma_i32_32x32x32_i8 and the block-serial update (16 subtractions + 16
+ * v_fmac, as the GEMM kernels issue them); kind 1: the VALU part alone;
+ * kind 2: the MFMA alone.  waves_per_simd (1..8) waves run `iters` steps of
+ * two subtiles each on every SIMD.  Returns the SIMD cycles per subtile and
+ * K-block (the launch's event time x the shader clock, which the waves'
+ * s_memtime / s_memrealtime counts give, / subtile-blocks per SIMD) and that
+ * clock in GHz.  Allocates and frees its own small buffers; synchronizes the
+ * stream. */
+int sg_issue_probe(sg_ctx *ctx, int32_t kind, int32_t waves_per_simd, int32_t iters, void *stream,
+                   float *simd_cycles_per_block, float *clock_ghz);
+
 /* Measurement hook for the GEMM kernel alone (no counterpart in the
  * reference): relays x into the operand layout once, then launches the same
  * GEMM kernel sg_matmul_q8_0_int8 uses `reps` times back to back on `stream`

@@ -711,3 +711,19 @@ def test_pool_l2_bit_exact(gpu_ctx, oracle, out_dim):
     for i in range(len(lens)):
         ref = oracle.mean_pool_l2(x[off[i]:off[i + 1]], out_dim)
         assert np.array_equal(got[i].view(np.uint32), ref.view(np.uint32)), i
+
+
+def test_issue_probe(gpu_ctx):
+    """sg_issue_probe (the GEMM arithmetic's compute floor): every kind returns a
+    positive cycle count at a plausible shader clock; the MFMA alone takes about
+    its 32-cycle issue interval; the MFMA plus the block-serial update takes at
+    least as long as either half."""
+    from semantica_gpu import kernels
+    got = {}
+    for kind in (0, 1, 2):
+        cyc, ghz = kernels.issue_probe(gpu_ctx, kind, 4, iters=4000)
+        say(f"issue probe kind {kind}: {cyc:.1f} SIMD cycles per subtile-block at {ghz:.2f} GHz")
+        assert 0.5 < ghz < 4.0
+        got[kind] = cyc
+    assert 24.0 < got[2] < 48.0
+    assert got[0] >= 0.95 * max(got[1], got[2])
