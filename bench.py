@@ -419,7 +419,9 @@ def issue_probe_leg(ctx):
     memory traffic), of its VALU and MFMA halves alone, at 2 and 4 waves per
     SIMD (the GEMM kernels run 4).  The MFMA is 32 cycles of the matrix pipe
     (its issue interval at the dense int8 peak), so 32 / (cycles of kind 0)
-    is the largest fraction of the int8 peak these kernels can reach."""
+    is the largest fraction of the int8 peak these kernels can reach.  Also the
+    attention's v_mfma_f32_16x16x32_f16 streamed alone (kind 3): cycles per
+    instruction and the fp16 rate it reaches on the 1024 SIMDs."""
     from semantica_gpu import kernels
     res = {}
     for w in (2, 4):
@@ -429,6 +431,10 @@ def issue_probe_leg(ctx):
             row[name] = round(cyc, 1)
         row["clock_GHz"] = round(ghz, 2)
         row["int8_peak_frac_ceiling"] = round(32.0 / row["mfma_plus_update"], 3)
+        # the attention's fp16 MFMA stream: one 16x16x32 MFMA (8192 MACs) per reported "block"
+        cyc3, ghz3 = kernels.issue_probe(ctx, 3, w)
+        row["f16_mfma_16x16x32_cycles"] = round(cyc3, 1)
+        row["f16_mfma_PFLOPs"] = round(2 * 8192 / cyc3 * 1024 * ghz3 * 1e9 / 1e15, 2)
         res[f"{w}_waves_per_simd"] = row
     return {"unit": "SIMD cycles per 32x32 subtile and K-block", **res}
 

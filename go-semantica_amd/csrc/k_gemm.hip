@@ -964,6 +964,35 @@ __global__ __launch_bounds__(1024, 4) void k_gemm_q8_resnorm(
 template <int KIND>
 __global__ __launch_bounds__(256) void k_issue_probe(float* __restrict__ sink, long long* __restrict__ clk, int iters) {
   const int lane = threadIdx.x & 63;
+  if constexpr (KIND == 3) {
+    // The attention's matrix instruction alone: four independent chains of
+    // v_mfma_f32_16x16x32_f16 (16 cycles each at the 2.5 PFLOP/s dense fp16
+    // peak), two per probe "subtile" step.
+    typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+    h8_t x, y;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      x[i] = (_Float16)(lane * 0.01f + i);
+      y[i] = (_Float16)(i * 0.5f);
+    }
+    f32x4_t c0 = {0, 0, 0, 0}, c1 = c0, c2 = c0, c3 = c0;
+    __syncthreads();
+    const long long t0 = clock64(), r0 = wall_clock64();
+    for (int i = 0; i < iters; i += 2) {
+      c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, y, c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(y, x, c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, x, c2, 0, 0, 0);
+      c3 = __builtin_amdgcn_mfma_f32_16x16x32_f16(y, y, c3, 0, 0, 0);
+    }
+    const long long t1 = clock64(), r1 = wall_clock64();
+    sink[blockIdx.x * 256 + threadIdx.x] = c0[0] + c1[1] + c2[2] + c3[3];
+    if (lane == 0) {
+      const int wv = blockIdx.x * 4 + (threadIdx.x >> 6);
+      clk[2 * wv] = t1 - t0;
+      clk[2 * wv + 1] = r1 - r0;
+    }
+    return;
+  }
   i32x4_t a = {lane, 3, 5, 7}, w = {11, lane, 13, 17};
   const i32x16_t bias = magic_bias();
   f32x16_t acc0, acc1;
@@ -1130,6 +1159,9 @@ hipError_t issue_probe(int kind, int blocks, float* sink, long long* clk, int it
       break;
     case 2:
       hipLaunchKernelGGL(k_issue_probe<2>, dim3(blocks), dim3(256), 0, s, sink, clk, iters);
+      break;
+    case 3:
+      hipLaunchKernelGGL(k_issue_probe<3>, dim3(blocks), dim3(256), 0, s, sink, clk, iters);
       break;
     default:
       return hipErrorInvalidValue;

@@ -1194,7 +1194,7 @@ int sg_hbm_probe(sg_ctx* ctx, int32_t kind, const float* a, const float* b, void
 int sg_issue_probe(sg_ctx* ctx, int32_t kind, int32_t waves_per_simd, int32_t iters, void* stream,
                    float* simd_cycles_per_block, float* clock_ghz) {
   if (!ctx || !simd_cycles_per_block || !clock_ghz) return fail(SG_ERR_INVALID, "NULL argument");
-  if (kind < 0 || kind > 2) return fail(SG_ERR_INVALID, "unknown probe kind %d", kind);
+  if (kind < 0 || kind > 3) return fail(SG_ERR_INVALID, "unknown probe kind %d", kind);
   if (waves_per_simd < 1 || waves_per_simd > 8 || iters < 2 || iters % 2 || iters > (1 << 24))
     return fail(SG_ERR_INVALID, "waves_per_simd 1..8, iters even in 2..2^24");
   SG_TRY(set_device(ctx));

@@ -252,11 +252,12 @@ int sg_hbm_probe(sg_ctx *ctx, int32_t kind, const float *a, const float *b, void
  * floor of those kernels.  kind 0: per 32x32 output subtile and K-block one
  * v_mfma_i32_32x32x32_i8 and the block-serial update (16 subtractions + 16
  * v_fmac, as the GEMM kernels issue them); kind 1: the VALU part alone;
- * kind 2: the MFMA alone.  waves_per_simd (1..8) waves run `iters` steps of
- * two subtiles each on every SIMD.  Returns the SIMD cycles per subtile and
- * K-block (the launch's event time x the shader clock, which the waves'
- * s_memtime / s_memrealtime counts give, / subtile-blocks per SIMD) and that
- * clock in GHz.  Allocates and frees its own small buffers; synchronizes the
+ * kind 2: the MFMA alone; kind 3: the attention's v_mfma_f32_16x16x32_f16
+ * alone (four independent chains; one instruction per "subtile-block").
+ * waves_per_simd (1..8) waves run `iters` steps of two subtiles each on every
+ * SIMD.  Returns the SIMD cycles per subtile and K-block (the launch's event
+ * time x the shader clock, which the waves' s_memtime / s_memrealtime counts
+ * give, / subtile-blocks per SIMD) and that clock in GHz.  Allocates and frees its own small buffers; synchronizes the
  * stream. */
 int sg_issue_probe(sg_ctx *ctx, int32_t kind, int32_t waves_per_simd, int32_t iters, void *stream,
                    float *simd_cycles_per_block, float *clock_ghz);
