@@ -98,8 +98,13 @@ __device__ __forceinline__ void xcd_tile(int& bx, int& by) {
 // l / 8 + 8 i, columns 4 (l % 8) .. + 3; 4 instructions per subtile) after
 // a transpose through the slice, instead of 16 single-float stores in the
 // MFMA's column-per-lane layout.
+// ROWMAX: also fold each of the lane's four rows' max|value| over the
+// subtile's valid columns into rm[i] (row row0 + l / 8 + 8 i), complete in
+// every lane of the row's 8-lane group.
+template <bool ROWMAX = false>
 __device__ __forceinline__ void store_subtile(float* stage, const float (&v)[16], float* __restrict__ Y, int ld,
-                                              int row0, int col0, int rows, int cols, int lr, int lh, int lane) {
+                                              int row0, int col0, int rows, int cols, int lr, int lh, int lane,
+                                              float* rm = nullptr) {
 #pragma unroll
   for (int r = 0; r < 16; r++) stage[(8 * (r >> 2) + 4 * lh + (r & 3)) * 32 + lr] = v[r];
   const int c4 = (lane & 7) * 4;
@@ -116,6 +121,14 @@ __device__ __forceinline__ void store_subtile(float* stage, const float (&v)[16]
         for (int t = 0; t < 4; t++)
           if (col + t < cols) Y[(int64_t)row * ld + col + t] = o[t];
       }
+    }
+    if constexpr (ROWMAX) {
+      float m = 0.0f;
+#pragma unroll
+      for (int t = 0; t < 4; t++) m = (row < rows && col + t < cols) ? fmaxf(m, fabsf(o[t])) : m;
+#pragma unroll
+      for (int x = 1; x < 8; x <<= 1) m = fmaxf(m, __shfl_xor(m, x));
+      rm[i] = fmaxf(rm[i], m);
     }
   }
 }
@@ -190,6 +203,10 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
     const int r_first = by * NW * BMW, r_last = min(r_first + NW * BMW, M) - 1;
     const bool one_seq = amax && row_seq[r_first] == row_seq[r_last];  // workgroup-uniform
     float mx = 0.0f;
+    // Rows of several sequences: per-row maxima into rmax.  With the staged
+    // stores they come from the row-contiguous read-back (three lane
+    // exchanges per row slot) instead of five per MFMA row.
+    const bool staged_rmax = stage && amax && !one_seq;  // workgroup-uniform
 #pragma unroll
     for (int tm = 0; tm < TM; tm++) {
       const int mb = mw + tm * 32;
@@ -213,13 +230,25 @@ __device__ __forceinline__ void gemm_epilogue(const f32x16_t (&acc)[TM][TN], int
         }
         if (one_seq) {
           mx = fmaxf(mx, a);
-        } else if (amax) {  // rows of several sequences: per-row maxima, folded below
+        } else if (amax && !staged_rmax) {  // rows of several sequences: per-row maxima, folded below
 #pragma unroll
           for (int o = 1; o < 32; o <<= 1) a = fmaxf(a, __shfl_xor(a, o));
           if (lr == 0) rmax[row - r_first] = a;
         }
       }
-      if (stage) {
+      if (staged_rmax) {
+        float rm[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int pr = 0; pr < TN / 2; pr++)
+          store_subtile<true>(stage, gv[pr], Y, Nh, mb, (n0 >> 1) + 32 * pr, M, Nh, lr, lh, lane, rm);
+        if ((lane & 7) == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const int row = mb + (lane >> 3) + 8 * i;
+            if (row <= r_last) rmax[row - r_first] = rm[i];
+          }
+        }
+      } else if (stage) {
 #pragma unroll
         for (int pr = 0; pr < TN / 2; pr++) store_subtile(stage, gv[pr], Y, Nh, mb, (n0 >> 1) + 32 * pr, M, Nh, lr, lh, lane);
       }
