@@ -592,16 +592,18 @@ __global__ __launch_bounds__(sgd::kKvThreads) void k_kv_prep(
     const float* __restrict__ k, const float* __restrict__ v, int ldkv, const float* __restrict__ kw, int HKV, int T,
     const int32_t* __restrict__ row_pos, const float* __restrict__ cos_t, const float* __restrict__ sin_t, float eps,
     _Float16* __restrict__ ks_h, _Float16* __restrict__ ks_l, int ldks, int nkb, const int32_t* __restrict__ seq_off,
-    const int32_t* __restrict__ voff, const sg_item* __restrict__ vtiles, int n_vtiles, _Float16* __restrict__ vt, int ldvt) {
+    const int32_t* __restrict__ voff, const sg_item* __restrict__ vtiles, int n_vtiles, _Float16* __restrict__ vt, int ldvt,
+    sgk::sg_kv_q qp) {
   __shared__ __attribute__((aligned(16))) float tv[kBK][sgd::kVtRowStride];
   const int b = blockIdx.x;
   if (b < nkb) {  // workgroup-uniform
     const int64_t g = (int64_t)b * sgd::kKvRows + (threadIdx.x >> 3);
     float* tile = &tv[0][0] + (threadIdx.x / SG_WAVE) * (8 * 40);  // 8 x 40 floats per wave
-    // No query heads (H = 0): the Q arguments are never read.  (Passing null
-    // for them crashed this compiler's device pass.)
-    sgd::qk_split_group(g, threadIdx.x & 7, (threadIdx.x >> 3) & 7, tile, k, ldkv, k, ldkv, kw, kw, 0, HKV, T,
-                        row_pos, cos_t, sin_t, eps, ks_h, ks_l, ldks, ks_h, ks_l, ldks);
+    // (token, head) groups, query heads first.  With no query heads (qp.H =
+    // 0) the Q arguments are never read; they then point at K (passing null
+    // for them crashed this compiler's device pass).
+    sgd::qk_split_group(g, threadIdx.x & 7, (threadIdx.x >> 3) & 7, tile, qp.q, qp.ldq, k, ldkv, qp.qw, kw, qp.H,
+                        HKV, T, row_pos, cos_t, sin_t, eps, qp.qs_h, qp.qs_l, qp.ldqs, ks_h, ks_l, ldks);
   } else {
     const int vb = b - nkb;
     sgd::v_split_tile(vtiles[vb % n_vtiles], vb / n_vtiles, tv, v, ldkv, seq_off, voff, vt, ldvt);
@@ -642,16 +644,24 @@ hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int3
 
 hipError_t kv_prep(const float* k, const float* v, int ldkv, const float* kw, int HKV, int T, const int32_t* row_pos,
                    const float* cos_t, const float* sin_t, float eps, _Float16* ks_h, _Float16* ks_l, int ldks,
-                   const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vt, int ldvt, hipStream_t s) {
+                   const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vt, int ldvt, hipStream_t s,
+                   const sg_kv_q* qpart) {
   if (T <= 0 || n_vtiles < 0 || HKV <= 0) return hipSuccess;
   if ((ldkv & 3) || (ldks & 7) || (ldvt & 7) || (reinterpret_cast<uintptr_t>(k) & 15) ||
       (reinterpret_cast<uintptr_t>(v) & 15) || (kw && (reinterpret_cast<uintptr_t>(kw) & 15)))
     return hipErrorInvalidValue;  // float4 loads of K and V rows and of the weights
-  const int64_t nkb = ((int64_t)T * HKV + sgd::kKvRows - 1) / sgd::kKvRows;
+  sgk::sg_kv_q qp{k, ldkv, kw, 0, ks_h, ks_l, ldks};
+  if (qpart && qpart->H > 0) {
+    if (!qpart->q || !qpart->qs_h || !qpart->qs_l || (qpart->ldq & 3) || (qpart->ldqs & 7) ||
+        (reinterpret_cast<uintptr_t>(qpart->q) & 15) || (qpart->qw && (reinterpret_cast<uintptr_t>(qpart->qw) & 15)))
+      return hipErrorInvalidValue;  // float4 loads of the Q rows and weights, 16-byte split stores
+    qp = *qpart;
+  }
+  const int64_t nkb = ((int64_t)T * (qp.H + HKV) + sgd::kKvRows - 1) / sgd::kKvRows;
   const int64_t nb = nkb + (int64_t)n_vtiles * HKV;
   if (nb > INT32_MAX) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_kv_prep, dim3((unsigned)nb), dim3(sgd::kKvThreads), 0, s, k, v, ldkv, kw, HKV, T, row_pos, cos_t,
-                     sin_t, eps, ks_h, ks_l, ldks, (int)nkb, seq_off, voff, vtiles, n_vtiles, vt, ldvt);
+                     sin_t, eps, ks_h, ks_l, ldks, (int)nkb, seq_off, voff, vtiles, n_vtiles, vt, ldvt, qp);
   return hipGetLastError();
 }
 

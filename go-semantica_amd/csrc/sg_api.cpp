@@ -349,6 +349,7 @@ struct Profiler {
 struct Lane {
   DevBuf h, xn, qkv, att, o, g, a8, sx, amax, meta_d, err;
   DevBuf ks, vt;  // attention operands, hi/lo fp16 (K row-major; V^T); Q is split inside the attention kernel
+  DevBuf qs;      // Q hi/lo for launches too small to fill the GPU (attn_q_presplit)
   DevBuf xp;      // exact-order attention: scores / weights [H][T][ldp] (SG_ATTN_EXACT only)
   DevBuf spill;   // attention scores past the kernel's register tiles (sequences > 512 keys)
   HostBuf meta_h, io_h;
@@ -366,7 +367,8 @@ struct Lane {
     return SG_OK;
   }
   ~Lane() {
-    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a8, &sx, &amax, &meta_d, &err, &ks, &vt, &xp, &spill}) b->release();
+    for (DevBuf* b : {&h, &xn, &qkv, &att, &o, &g, &a8, &sx, &amax, &meta_d, &err, &ks, &vt, &qs, &xp, &spill})
+      b->release();
     meta_h.release();
     io_h.release();
     if (done) (void)hipEventDestroy(done);
@@ -486,6 +488,18 @@ struct Trace {
   float *qkv = nullptr, *att = nullptr, *h = nullptr;
 };
 
+// Attention launches of fewer workgroups than the GPU has CUs run latency-
+// bound, and there the in-kernel Q prologue (one memory round trip, the QK-norm
+// through the LDS tile, RoPE, the split: over half of a 32-token sequence's
+// workgroup) is on the critical path.  Such launches take Q pre-split from
+// k_kv_prep (the same arithmetic, bit-identical operands), which prepares it
+// over many more threads; larger launches keep the prologue, which saves
+// writing Q's operands and reading them back.
+constexpr int kAttnQPresplitItems = 256;
+bool attn_q_presplit(const sg_model* m, const Meta& meta) {
+  return m->attn_mode != SG_ATTN_EXACT && (int64_t)meta.n_items * m->cfg.num_kv_heads < kAttnQPresplitItems;
+}
+
 // Layers [l0, l1) of one sequence group's forward on lane w, stream s: the
 // embedding first when l0 == 0, the pooled embeddings into d_out after the
 // last layer.  stop >= 0: return after `stop` layers with the residual stream
@@ -542,6 +556,10 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
   const bool vt_fused = m->attn_mode != SG_ATTN_EXACT && !(tr && tr->qkv) && sgk::gemm_writes_vt(T) &&
                         meta.seq_start32;
   const sgk::sg_vt_out vto{vt_h, ldvt, qd + kvd, meta.row_seq, meta.seq_off, meta.voff};
+  // Small attention launches take Q pre-split by k_kv_prep (attn_q_presplit).
+  const bool q_pre = attn_q_presplit(m, meta);
+  _Float16* qs_h = q_pre ? w.qs.as<_Float16>() : nullptr;
+  _Float16* qs_l = q_pre ? qs_h + (size_t)T * qd : nullptr;
 
   if (l0 == 0) {
     SG_LAUNCH(SG_K_OTHER, 4.0 * 4 * L * ns, sgk::fill_f32(amax, 0.0f, (int64_t)4 * L * ns, s));
@@ -588,18 +606,19 @@ int run_forward(sg_model* m, Lane& w, const int32_t* d_tokens, const Meta& meta,
     } else {
       // K's QK-norm + RoPE + split and V's V^T split in one launch; Q's norm and
       // RoPE run inside the attention kernel.
-      SG_LAUNCH(SG_K_NORM, t * kvd * (vt_fused ? 8.0 : 16.0),
+      const sgk::sg_kv_q qpart{qkv, nqkv, ly.q_norm, c.num_heads, qs_h, qs_l, qd};
+      SG_LAUNCH(SG_K_NORM, t * ((vt_fused ? 8.0 : 16.0) * kvd + (q_pre ? 8.0 * qd : 0.0)),
                 sgk::kv_prep(qkv + qd, qkv + qd + kvd, nqkv, ly.k_norm, c.num_kv_heads, T, meta.row_pos, m->cos_t,
                              m->sin_t, eps, ks_h, ks_l, kvd, meta.seq_off, meta.voff, meta.vtiles,
-                             vt_fused ? 0 : meta.n_vtiles, vt_h, ldvt, s));
+                             vt_fused ? 0 : meta.n_vtiles, vt_h, ldvt, s, q_pre ? &qpart : nullptr));
       const sg_attn_qpre qpre{qkv, nqkv, ly.q_norm, m->cos_t, m->sin_t, eps};
       const sg_attn_qout qout{a8, ar, sx};
       const sg_attn_spill spill{w.spill.as<float>(), meta.spill_off, meta.spill_total};
       SG_LAUNCH(SG_K_ATTENTION, attn_flops,
-                sgk::attention(nullptr, nullptr, 0, ks_h, ks_l, kvd, vt_h, ldvt, att, qd, meta.seq_off,
-                               meta.voff, meta.items, meta.n_items, c.num_heads, c.num_kv_heads, m->hd,
-                               m->attn_scale, site(l, 1), meta.max_len, s, &qpre, q_attn ? &qout : nullptr,
-                               &spill));
+                sgk::attention(q_pre ? qs_h : nullptr, q_pre ? qs_l : nullptr, q_pre ? qd : 0, ks_h, ks_l, kvd, vt_h,
+                               ldvt, att, qd, meta.seq_off, meta.voff, meta.items, meta.n_items, c.num_heads,
+                               c.num_kv_heads, m->hd, m->attn_scale, site(l, 1), meta.max_len, s,
+                               q_pre ? nullptr : &qpre, q_attn ? &qout : nullptr, &spill));
     }
     if (tr && tr->att) SG_HIP(tap(tr->att, att, l, qd));
     if (!(q_attn && m->attn_mode != SG_ATTN_EXACT))
@@ -697,6 +716,7 @@ int token_error(Lane& w, const int32_t* d_tokens, hipStream_t s) {
   return fail(SG_ERR_TOKEN, "token ID out of range: %d", h[1]);
 }
 
+
 int ensure_workspace(const sg_model* m, Lane& w, const Meta& meta) {
   const int T = meta.T, n_seq = meta.n_seq, Tp = meta.Tp;
   const sg_model_config& c = m->cfg;
@@ -710,6 +730,7 @@ int ensure_workspace(const sg_model* m, Lane& w, const Meta& meta) {
   SG_TRY(w.o.ensure(sizeof(float) * t * c.embed_dim));
   SG_TRY(w.g.ensure(sizeof(float) * t * c.interm_dim));
   SG_TRY(w.a8.ensure((size_t)sgk::gemm_pad_rows(T) * a_cols));
+  if (attn_q_presplit(m, meta)) SG_TRY(w.qs.ensure(2 * sizeof(_Float16) * t * m->qd));
   SG_TRY(w.sx.ensure(sizeof(float) * t));
   SG_TRY(w.amax.ensure(sizeof(float) * 4 * (size_t)c.num_layers * n_seq));
   SG_TRY(w.ks.ensure(2 * sizeof(_Float16) * t * m->kvd));

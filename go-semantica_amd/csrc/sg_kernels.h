@@ -188,10 +188,22 @@ hipError_t v_split_t(const float* v, int ldv, const int32_t* seq_off, const int3
 // qknorm_rope's K-only split (H = 0) and v_split_t in one launch: K and V
 // share the row stride ldkv (columns of the QKV output).  n_vtiles = 0: K
 // only (V^T written by the QKV GEMM, sg_vt_out).
+// Optional Q part of kv_prep: the H query heads' norm (qw), RoPE and hi/lo
+// split as well (k_qknorm_rope_split's arithmetic), into qs_h / qs_l
+// [T][ldqs], for launches that run the attention on pre-split Q.
+struct sg_kv_q {
+  const float* q;
+  int ldq;
+  const float* qw;
+  int H;
+  _Float16* qs_h;
+  _Float16* qs_l;
+  int ldqs;
+};
 hipError_t kv_prep(const float* k, const float* v, int ldkv, const float* kw, int HKV, int T, const int32_t* row_pos,
                    const float* cos_t, const float* sin_t, float eps, _Float16* ks_h, _Float16* ks_l, int ldks,
                    const int32_t* seq_off, const int32_t* voff, const sg_item* vtiles, int n_vtiles, _Float16* vt,
-                   int ldvt, hipStream_t s);
+                   int ldvt, hipStream_t s, const sg_kv_q* qpart = nullptr);
 // rows x cols of x -> hi/lo fp16 of x*scale (row stride ldo).
 hipError_t split_rows(const float* x, int ldx, int rows, int cols, float scale, _Float16* hi, _Float16* lo, int ldo,
                       hipStream_t s);
