@@ -94,6 +94,8 @@ int seq_groups(int S, int G) {
 // sequences are binned to XCDs (largest first, onto the least-loaded bin) and
 // the list interleaves the bins: all workgroups of a sequence then share one
 // L2 copy of its K and V^T.
+constexpr int kAttnLptItems = 512;  // two rounds of attention workgroups on 256 CUs
+
 int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev, hipStream_t s, Meta& m) {
   constexpr int kXcd = 8;
   const int T = off[n_seq];
@@ -157,6 +159,15 @@ int stage_meta(const int32_t* off, int n_seq, int G, HostBuf& host, DevBuf& dev,
       }
       it[k] = bin[b][pos[b]++];
     }
+    // A workgroup's time grows with its sequence's length.  In a launch of at
+    // most two rounds (one workgroup per CU) the last round's workgroups set
+    // its end, so there the longest go first (stable: equal lengths keep the
+    // XCD binning) and the last round holds the short ones.  Longer launches
+    // keep the binning, whose shared L2 copies are worth more than the tail.
+    if (n_items <= kAttnLptItems)
+      std::stable_sort(it, it + n_items, [&](const sg_item& a, const sg_item& b) {
+        return off[a.seq + 1] - off[a.seq] > off[b.seq + 1] - off[b.seq];
+      });
   }
   SG_HIP(hipMemcpyAsync(dev.p, host.p, bytes, hipMemcpyHostToDevice, s));
   SG_TRY(host.record(s));
